@@ -1,0 +1,100 @@
+// attn_device.hpp — gfx950 (CDNA4) device helpers shared by the attention kernels.
+//
+// Vector types for the MFMA operands, the two MFMA shapes the kernels use, dtype traits for
+// fp16/bf16 storage, and a few math helpers. Everything here is written for wave64 CDNA4 only.
+//
+// MFMA lane layouts relied on (v_mfma_f32_32x32x16_{f16,bf16}, wave64):
+//   A (32 x 16):  lane l holds A[l % 32][8*(l/32) + e], e = 0..7 (one 16-byte register quad)
+//   B (16 x 32):  lane l holds B[8*(l/32) + e][l % 32]
+//   C (32 x 32):  lane l, accumulator r = 0..15 holds C[8*(r/4) + 4*(l/32) + (r%4)][l % 32]
+// The contraction index mapping (e -> k) only has to agree between A and B, which it does by
+// construction, so the kernels are free to permute the contraction order; the C layout is the
+// one that fixes where each output element lives.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/fable_attn_abi.h"
+
+namespace fa {
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// storage dtype traits
+template <typename T>
+struct Dt;
+
+template <>
+struct Dt<_Float16> {
+  using V8 = f16x8;
+  using V4 = f16x4;
+  static __device__ __forceinline__ f32x16 mma32(V8 a, V8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(V8 a, V8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+};
+
+template <>
+struct Dt<__bf16> {
+  using V8 = bf16x8;
+  using V4 = bf16x4;
+  static __device__ __forceinline__ f32x16 mma32(V8 a, V8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16(V8 a, V8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
+};
+
+template <typename V, typename U>
+__device__ __forceinline__ V bitcast(U u) {
+  static_assert(sizeof(V) == sizeof(U), "bitcast size");
+  return __builtin_bit_cast(V, u);
+}
+
+// 2^x on the transcendental unit (v_exp_f32): exp2(-inf) = 0.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// tanh from the identity tanh(y) = 1 - 2 / (exp(2y) + 1); saturates to +-1 for large |y|.
+__device__ __forceinline__ float tanh_exp(float y) {
+  const float e = exp2_fast(2.0f * kLog2e * y);
+  return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
+}
+
+// Reductions across lanes l and l^32 (the two halves of one MFMA 32x32 C column) with
+// v_permlane32_swap. Swapping a register with itself leaves, in every lane, the pair
+// {x[l], x[l^32]} spread over the two results, so a symmetric op over both results is the
+// cross-half reduction whichever result holds which value.
+__device__ __forceinline__ float half_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float half_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// blockIdx.x -> work index so that consecutive work items land on the same XCD (one L2).
+// Workgroups are dispatched round-robin over the 8 XCDs of an MI355X.
+__device__ __forceinline__ int xcd_remap(int L, int N) {
+  constexpr int kXcd = 8;
+  const int x = L % kXcd, idx = L / kXcd;
+  const int per = N / kXcd, rem = N % kXcd;
+  return x * per + (x < rem ? x : rem) + idx;
+}
+
+}  // namespace fa

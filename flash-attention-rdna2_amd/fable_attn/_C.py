@@ -1,0 +1,256 @@
+"""Host glue between torch tensors and the C-ABI launchers (the reference's `_C` module).
+
+Mirrors the functions of the reference's pybind module (package/csrc/dispatch.cpp:35-231,
+bound at :239-268) with the same names, argument order and meaning:
+    fwd(q, k, v, scale, causal, win_left, win_right, softcap, alibi, dropout_p, seed,
+        attn_chunk=0, out=None) -> (out, lse)
+    bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, alibi,
+        dropout_p, seed) -> (dq, dk, dv)
+    fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win_right,
+               softcap, alibi, dropout_p, seed, attn_chunk=0, seqused_q=None,
+               seqused_k=None, return_lse=False) -> out  (or (out, lse) when return_lse)
+    dec(q, k_cache, v_cache, block_table, cache_seqlens, new_k, new_v, rotary_cos,
+        rotary_sin, rotary_interleaved, scale, window, num_splits, cache_leftpad=None,
+        return_lse=False, softcap=0.0, alibi=None, rotary_dim=0, rotary_pos=None) -> (out, lse)
+    combine(out_partial, lse_partial, out_dtype) -> out
+Tensor checks raise RuntimeError as TORCH_CHECK does there. torch only allocates outputs and
+workspaces and supplies the current stream; all compute is in libfable_attn_hip.so. There is
+no fallback: if the library is missing, importing this module raises ImportError.
+"""
+import ctypes
+
+import torch
+
+from . import _lib
+from ._lib import BwdParams, CombineParams, DecParams, FwdParams, Strides
+
+_L = _lib.load()
+
+
+def _req(cond, msg):
+    if not cond:
+        raise RuntimeError("fable_attn: " + msg)
+
+
+def _dt(t):
+    if t.dtype == torch.float16:
+        return _lib.FA_F16
+    if t.dtype == torch.bfloat16:
+        return _lib.FA_BF16
+    if t.dtype == torch.float32:
+        return _lib.FA_F32
+    raise RuntimeError(f"fable_attn: dtype {t.dtype} not supported")
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(t):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _bhs(t):
+    """(b, h, s) element strides of a [B,H,S,D] view."""
+    return Strides(t.stride(0), t.stride(1), t.stride(2))
+
+
+def _rows_aligned(t):
+    """16-byte aligned rows with a contiguous head_dim: what the kernels' vector loads need."""
+    el = t.element_size()
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and
+            all((s * el) % 16 == 0 for s in t.stride()[:-1]))
+
+
+def _check_bhsd(name, t, dtype, dev):
+    _req(t.is_cuda, f"{name}: GPU tensor required")
+    _req(t.dim() == 4, f"{name}: expected [B,H,S,D]")
+    _req(t.dtype == dtype, f"{name}: dtype {t.dtype} differs from q ({dtype})")
+    _req(t.device == dev, f"{name}: device mismatch")
+    _req(_rows_aligned(t), f"{name}: head_dim must be contiguous with 16-byte aligned rows")
+
+
+def fwd(q, k, v, scale, causal, win_left, win_right, softcap, alibi, dropout_p, seed,
+        attn_chunk=0, out=None):
+    """q [B,Hq,SQ,D], k/v [B,Hk,SK,D] (strided views). Returns (out, lse [B,Hq,SQ] fp32).
+    Reference: dispatch.cpp:35-80 (one launch here; the reference looped over the batch)."""
+    B, Hq, SQ, D = q.shape
+    Hk, SK = k.shape[1], k.shape[2]
+    for n, t in (("q", q), ("k", k), ("v", v)):
+        _check_bhsd(n, t, q.dtype, q.device)
+    _req(k.shape[0] == B and v.shape == k.shape and k.shape[3] == D, "k/v shape mismatch")
+    _req(Hq % Hk == 0, "Hq must be a multiple of Hk (GQA)")
+    if out is None:
+        out = torch.empty((B, SQ, Hq, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+    else:
+        _req(tuple(out.shape) == tuple(q.shape), "out must have the shape of q [B,H,SQ,D]")
+        _req(out.dtype == q.dtype, "out must have the dtype of q")
+        _req(_rows_aligned(out), "out: head_dim must be contiguous with 16-byte aligned rows")
+    lse = torch.empty((B, Hq, SQ), dtype=torch.float32, device=q.device)
+    al = alibi.float().contiguous() if alibi is not None else None
+    p = FwdParams()
+    p.Q, p.K, p.V, p.O, p.LSE = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
+    p.sQ, p.sK, p.sV, p.sO = _bhs(q), _bhs(k), _bhs(v), _bhs(out)
+    p.SQ, p.SK, p.HD, p.NH, p.gqa = SQ, SK, D, Hq, Hq // Hk
+    p.scale, p.softcap = float(scale), float(softcap)
+    p.win_left, p.win_right = int(win_left), int(win_right)
+    p.alibi_slopes = al.data_ptr() if al is not None else None
+    p.causal = 1 if causal else 0
+    p.dropout_p, p.philox_seed = float(dropout_p), int(seed) & ((1 << 64) - 1)
+    p.cu_q = p.cu_k = None
+    p.batch = B
+    p.attn_chunk = int(attn_chunk)
+    p.seqused_q = p.seqused_k = None
+    p.lse_sb, p.lse_sh = Hq * SQ, SQ
+    with torch.cuda.device(q.device):
+        _lib.check(_L.fa_forward_launch(p, _dt(q), _stream(q)), "fa_forward_launch")
+    return out, lse
+
+
+def fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win_right, softcap,
+               alibi, dropout_p, seed, attn_chunk=0, seqused_q=None, seqused_k=None,
+               return_lse=False):
+    """q (total_q, Hq, D), k/v (total_k, Hk, D), cu_* int32 [batch+1]. One launch for all
+    sequences; LSE [Hq, total_q] is produced on request (the reference wrote none,
+    dispatch.cpp:116,139). Reference: dispatch.cpp:117-157."""
+    _req(q.is_cuda and k.is_cuda and v.is_cuda, "GPU tensors required")
+    _req(q.dim() == 3 and k.dim() == 3 and v.dim() == 3, "varlen expects [total, H, D]")
+    Hq, D, Hk = q.shape[1], q.shape[2], k.shape[1]
+    _req(Hq % Hk == 0, "Hq must be a multiple of Hk (GQA)")
+    for n, t in (("q", q), ("k", k), ("v", v)):
+        _req(t.dtype == q.dtype, f"{n}: dtype mismatch")
+        _req(_rows_aligned(t), f"{n}: head_dim must be contiguous with 16-byte aligned rows")
+    _req(cu_q.dtype == torch.int32 and cu_k.dtype == torch.int32, "cu_seqlens must be int32")
+    batch = cu_q.numel() - 1
+    out = torch.zeros_like(q) if seqused_q is not None else torch.empty_like(q)
+    lse = torch.empty((Hq, q.shape[0]), dtype=torch.float32, device=q.device) if return_lse else None
+    al = alibi.float().contiguous() if alibi is not None else None
+    p = FwdParams()
+    p.Q, p.K, p.V, p.O = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
+    p.LSE = lse.data_ptr() if lse is not None else None
+    p.sQ = Strides(0, q.stride(1), q.stride(0))
+    p.sK = Strides(0, k.stride(1), k.stride(0))
+    p.sV = Strides(0, v.stride(1), v.stride(0))
+    p.sO = Strides(0, out.stride(1), out.stride(0))
+    p.SQ, p.SK, p.HD, p.NH, p.gqa = int(max_sq), int(max_sk), D, Hq, Hq // Hk
+    p.scale, p.softcap = float(scale), float(softcap)
+    p.win_left, p.win_right = int(win_left), int(win_right)
+    p.alibi_slopes = al.data_ptr() if al is not None else None
+    p.causal = 1 if causal else 0
+    p.dropout_p, p.philox_seed = float(dropout_p), int(seed) & ((1 << 64) - 1)
+    p.cu_q, p.cu_k = cu_q.data_ptr(), cu_k.data_ptr()
+    p.batch = batch
+    p.attn_chunk = int(attn_chunk)
+    p.seqused_q = seqused_q.data_ptr() if seqused_q is not None else None
+    p.seqused_k = seqused_k.data_ptr() if seqused_k is not None else None
+    p.lse_sb, p.lse_sh = 0, q.shape[0]
+    with torch.cuda.device(q.device):
+        _lib.check(_L.fa_forward_launch(p, _dt(q), _stream(q)), "fa_forward_launch (varlen)")
+    return (out, lse) if return_lse else out
+
+
+def bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, alibi, dropout_p,
+        seed):
+    """All tensors [B,H,S,D] views (D contiguous); lse [B,Hq,SQ] fp32. Returns (dq, dk, dv)
+    with the (B,S,H,D)-dense memory of the public API, viewed as [B,H,S,D].
+    Reference: dispatch.cpp:83-111 (no bf16 .item() host syncs here)."""
+    B, Hq, SQ, D = q.shape
+    Hk, SK = k.shape[1], k.shape[2]
+    for n, t in (("dout", dout), ("q", q), ("k", k), ("v", v), ("out", out)):
+        _check_bhsd(n, t, q.dtype, q.device)
+    _req(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (B, Hq, SQ),
+         "lse must be contiguous fp32 [B,Hq,SQ]")
+    dq = torch.empty((B, SQ, Hq, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+    dk = torch.empty((B, SK, Hk, D), dtype=k.dtype, device=q.device).transpose(1, 2)
+    dv = torch.empty((B, SK, Hk, D), dtype=v.dtype, device=q.device).transpose(1, 2)
+    dsum = torch.empty((B, Hq, SQ), dtype=torch.float32, device=q.device)
+    al = alibi.float().contiguous() if alibi is not None else None
+    p = BwdParams()
+    p.Q, p.K, p.V, p.O, p.dO = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr()
+    p.dQ, p.dK, p.dV = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    p.lse, p.dsum = lse.data_ptr(), dsum.data_ptr()
+    p.qs, p.ks, p.vs, p.os, p.dos = _bhs(q), _bhs(k), _bhs(v), _bhs(out), _bhs(dout)
+    p.dqs, p.dks, p.dvs = _bhs(dq), _bhs(dk), _bhs(dv)
+    p.B, p.Hq, p.Hk, p.SQ, p.SK, p.D, p.gqa = B, Hq, Hk, SQ, SK, D, Hq // Hk
+    p.scale, p.softcap = float(scale), float(softcap)
+    p.alibi = al.data_ptr() if al is not None else None
+    p.causal, p.win_left, p.win_right = 1 if causal else 0, int(win_left), int(win_right)
+    p.dropout = 1 if dropout_p > 0 else 0
+    p.drop_seed, p.dropout_p = int(seed) & ((1 << 64) - 1), float(dropout_p)
+    p.keep_scale = 1.0 / (1.0 - dropout_p) if dropout_p > 0 else 1.0
+    with torch.cuda.device(q.device):
+        _lib.check(_L.fable_attn_backward_launch(p, _dt(q), _stream(q)), "fable_attn_backward_launch")
+    return dq, dk, dv
+
+
+def num_splits(batch, nq, nheads, gqa, ctx_bound, hint):
+    return int(_L.fa_decode_num_splits(batch, nq, nheads, gqa, int(ctx_bound), int(hint)))
+
+
+def dec(q, k_cache, v_cache, block_table, cache_seqlens, new_k, new_v, rotary_cos, rotary_sin,
+        rotary_interleaved, scale, window, num_splits=0, cache_leftpad=None, return_lse=False,
+        softcap=0.0, alibi=None, rotary_dim=0, rotary_pos=None):
+    """q [B,nq,Hq,D]; caches [num_blocks,page,Hk,D] contiguous; block_table [B,max_blocks]
+    int32; cache_seqlens [B] int32 (length before append). Returns (out [B,nq,Hq,D],
+    lse [B,nq,Hq] or an empty tensor). Reference: dispatch.cpp:162-231."""
+    _req(q.is_cuda and k_cache.is_cuda and v_cache.is_cuda, "GPU tensors required")
+    _req(q.dim() == 4, "decode expects q [B,nq,Hq,D]")
+    _req(k_cache.dim() == 4, "k_cache expected [num_blocks, page, nheads_k, D]")
+    B, NQ, Hq, D = q.shape
+    page, Hk = k_cache.shape[1], k_cache.shape[2]
+    _req(Hq % Hk == 0, "Hq must be a multiple of nheads_k (GQA)")
+    _req(page > 0 and (page & (page - 1)) == 0, "page must be a power of two")
+    for n, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
+        _req(t.is_contiguous() and t.dtype == q.dtype, f"{n}: contiguous, dtype of q")
+    _req(block_table.dtype == torch.int32 and block_table.is_contiguous(), "block_table int32")
+    _req(cache_seqlens.dtype == torch.int32, "cache_seqlens int32")
+    ctx_bound = block_table.shape[1] * page
+    nsplit = int(_L.fa_decode_num_splits(B, NQ, Hq, Hq // Hk, ctx_bound, int(num_splits or 0)))
+    out = torch.empty((B, NQ, Hq, D), dtype=q.dtype, device=q.device)
+    scratch = torch.empty((B * NQ * Hq * nsplit * (D + 2),), dtype=torch.float32, device=q.device)
+    lse = (torch.empty((B, NQ, Hq), dtype=torch.float32, device=q.device) if return_lse
+           else torch.empty((0,), dtype=torch.float32, device=q.device))
+    p = DecParams()
+    p.q, p.Kc, p.Vc = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr()
+    p.block_table, p.o, p.scratch = block_table.data_ptr(), out.data_ptr(), scratch.data_ptr()
+    p.ctx_len = cache_seqlens.data_ptr()
+    p.cos = rotary_cos.data_ptr() if rotary_cos is not None else None
+    p.sin = rotary_sin.data_ptr() if rotary_sin is not None else None
+    p.batch, p.NH, p.gqa, p.HD, p.page = B, Hq, Hq // Hk, D, page
+    p.max_blocks, p.nsplit, p.window = block_table.shape[1], nsplit, int(window)
+    p.rotary = (2 if rotary_interleaved else 1) if rotary_cos is not None else 0
+    p.scale = float(scale)
+    p.leftpad = cache_leftpad.data_ptr() if cache_leftpad is not None else None
+    p.lse_out = lse.data_ptr() if return_lse else None
+    p.softcap = float(softcap)
+    p.alibi = alibi.data_ptr() if alibi is not None else None
+    p.nq, p.rotary_dim = NQ, int(rotary_dim)
+    p.rotary_pos = rotary_pos.data_ptr() if rotary_pos is not None else None
+    if new_k is not None:
+        _req(new_k.is_contiguous() and new_v is not None and new_v.is_contiguous(),
+             "new_k/new_v contiguous [B,nq,Hk,D]")
+    with torch.cuda.device(q.device):
+        _lib.check(_L.fa_decode_launch(p, _dt(q), _stream(q), _ptr(new_k), _ptr(new_v)),
+                   "fa_decode_launch")
+    return out, lse
+
+
+def combine(out_partial, lse_partial, out_dtype):
+    """out_partial [nsplit,B,S,H,D] (D contiguous), lse_partial [nsplit,B,H,S] fp32 ->
+    dense [B,S,H,D] in out_dtype. Reference math: flash_attn_interface.py:567-580."""
+    _req(out_partial.is_cuda and lse_partial.is_cuda, "GPU tensors required")
+    _req(out_partial.dim() == 5 and lse_partial.dim() == 4, "shapes [nsplit,B,S,H,D] / [nsplit,B,H,S]")
+    _req(out_partial.stride(-1) == 1, "out_partial: head_dim must be contiguous")
+    ns, B, S, H, D = out_partial.shape
+    lp = lse_partial.float()
+    out = torch.empty((B, S, H, D), dtype=out_dtype, device=out_partial.device)
+    c = CombineParams()
+    c.out_partial, c.lse_partial, c.out = out_partial.data_ptr(), lp.data_ptr(), out.data_ptr()
+    c.nsplit, c.B, c.S, c.H, c.D = ns, B, S, H, D
+    c.op_split, c.op_b, c.op_seq, c.op_h = (out_partial.stride(0), out_partial.stride(1),
+                                            out_partial.stride(2), out_partial.stride(3))
+    c.lp_split, c.lp_b, c.lp_h, c.lp_seq = lp.stride(0), lp.stride(1), lp.stride(2), lp.stride(3)
+    c.in_dtype, c.out_dtype = _dt(out_partial), _dt(out)
+    with torch.cuda.device(out_partial.device):
+        _lib.check(_L.fa_combine_launch(c, _stream(out_partial)), "fa_combine_launch")
+    return out

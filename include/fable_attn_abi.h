@@ -1,0 +1,201 @@
+/*
+ * fable_attn_abi.h — the C-ABI boundary of the MI355X (gfx950) exact-attention library
+ * `libfable_attn_hip.so`.
+ *
+ * One header, included verbatim by the HIP translation units that implement the entry points
+ * and by every host caller (the Python ctypes binding mirrors these structs field for field and
+ * a CPU test checks the offsets against this file compiled with gcc). Parameter structs are
+ * passed BY VALUE, exactly as the reference passes them, and are plain C: fixed-width fields,
+ * device pointers as `const void*` / `void*`, strides in ELEMENTS, the innermost (head_dim)
+ * stride is always 1. No torch or HIP types appear in any signature; a stream is `void*`
+ * (a `hipStream_t`, NULL = the legacy default stream).
+ *
+ * Reference interface replaced (paths relative to the reference repository root):
+ *   package/csrc/fa_iface.h:9-24   struct Strides + struct FwdParams
+ *   package/csrc/fa_iface.h:27-38  struct Str + struct BwdParams
+ *   package/csrc/fa_iface.h:42-63  struct DecParams
+ *   package/csrc/fa_iface.h:65-68  the three extern "C" launchers
+ *   package/csrc/stream.cu:8-10    fable_current_stream (not needed: callers pass their stream)
+ *
+ * Deliberate differences from the reference's mirror structs (each one removes a defect or a
+ * gfx1030-only mechanism; field meanings are otherwise unchanged):
+ *   - launchers return an int status (FA_OK == 0) instead of printf+abort(); the message of the
+ *     last failure on the calling thread is available from fable_attn_last_error();
+ *   - one definition of every struct for host and device (the reference's kernel-side BwdParams
+ *     carried a trailing `probe` field its host mirror lacked, backward.hip:72 vs fa_iface.h:38);
+ *   - the bf16 power-of-two shift fields (sc_q/sc_k/sc_v, shQ/shK/shV/shdO) are gone: gfx950 MFMA
+ *     consumes bf16 natively, so no host-side `.item()` synchronisation is needed;
+ *   - the forward writes LSE for every batch element in one launch (lse_sb/lse_sh strides), so
+ *     the host no longer loops over the batch (reference dispatch.cpp:61-78), and the varlen
+ *     forward can return LSE too (the reference passed LSE=nullptr, dispatch.cpp:139).
+ */
+#ifndef FABLE_ATTN_ABI_H
+#define FABLE_ATTN_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define FABLE_ATTN_ABI_VERSION 1
+
+/* dtype codes, same values as the reference (fa_forward.hip:403, backward.hip:25) */
+enum { FA_F16 = 0, FA_BF16 = 1, FA_F32 = 2 };
+
+/* status codes returned by every launcher */
+enum {
+  FA_OK = 0,
+  FA_ERR_DTYPE = 1,        /* dtype not implemented by this entry point */
+  FA_ERR_HEADDIM = 2,      /* head_dim has no instantiated kernel */
+  FA_ERR_ARG = 3,          /* inconsistent argument (shape, alignment, null pointer) */
+  FA_ERR_UNSUPPORTED = 4,  /* feature combination not implemented */
+  FA_ERR_LAUNCH = 5        /* the HIP runtime rejected the launch */
+};
+
+/* Element strides of a [batch, head, seq, head_dim] view; head_dim stride is 1.
+ * Reference: fa_iface.h:9 (Strides), fa_iface.h:27 (Str). */
+typedef struct fa_strides {
+  int64_t b, h, s;
+} fa_strides;
+
+/* Forward parameters. Reference: fa_iface.h:10-24 / fa_forward.hip:23-49.
+ * Dense: Q [B,NH,SQ,HD], K/V [B,NH/gqa,SK,HD] as strided views, batch = B.
+ * Varlen: cu_q/cu_k non-null (int32, batch+1 entries), SQ/SK = max_seqlen_q/k (grid size),
+ *         sequence z occupies rows cu_q[z]..cu_q[z+1] (seq stride sQ.s), sQ.b/sK.b are ignored;
+ *         seqused_q/seqused_k (optional) shorten sequence z to seqused[z] rows.
+ * Visibility of key j to query i (delta = SK_z - SQ_z, bottom-right alignment):
+ *         causal: j <= i+delta;  win_left >= 0: j >= i+delta-win_left;
+ *         win_right >= 0: j <= i+delta+win_right;  attn_chunk > 0: j in the chunk of
+ *         max(i+delta,0). Logit = scale*q.k, then softcap*tanh(logit/softcap) if softcap > 0,
+ *         then + alibi_slopes[h]*(j-i). A row with no visible key gets O = 0 and LSE = -inf.
+ * LSE (natural log, fp32, optional): dense LSE[b*lse_sb + h*lse_sh + i];
+ *         varlen LSE[h*lse_sh + cu_q[z] + i] (lse_sb ignored). */
+typedef struct FwdParams {
+  const void* Q;
+  const void* K;
+  const void* V;
+  void* O;
+  float* LSE;
+  fa_strides sQ, sK, sV, sO;
+  int32_t SQ, SK, HD, NH, gqa;
+  float scale, softcap;
+  int32_t win_left, win_right;
+  const float* alibi_slopes;
+  int32_t causal;
+  float dropout_p;
+  uint64_t philox_seed;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  int32_t batch;
+  int32_t attn_chunk;
+  const int32_t* seqused_q;
+  const int32_t* seqused_k;
+  int64_t lse_sb, lse_sh;
+} FwdParams;
+
+/* Backward parameters. Reference: fa_iface.h:28-38 / backward.hip:59-73.
+ * Q,O,dO,dQ [B,Hq,SQ,D]; K,V,dK,dV [B,Hk,SK,D] (strided, D contiguous);
+ * lse [B,Hq,SQ] fp32 contiguous (from the forward); dsum: fp32 workspace [B,Hq,SQ]
+ * (caller-allocated, overwritten). Masking/softcap/alibi exactly as FwdParams. */
+typedef struct BwdParams {
+  const void* Q;
+  const void* K;
+  const void* V;
+  const void* O;
+  const void* dO;
+  void* dQ;
+  void* dK;
+  void* dV;
+  const float* lse;
+  float* dsum;
+  fa_strides qs, ks, vs, os, dos, dqs, dks, dvs;
+  int32_t B, Hq, Hk, SQ, SK, D, gqa;
+  float scale, softcap;
+  const float* alibi;
+  int32_t causal, win_left, win_right;
+  int32_t dropout;
+  uint64_t drop_seed;
+  float dropout_p, keep_scale;
+} BwdParams;
+
+/* Paged-KV decode parameters. Reference: fa_iface.h:42-63 / fa_decode.hip:13-35.
+ * q [batch, nq, NH, HD] contiguous; Kc/Vc [num_blocks, page, NH/gqa, HD] contiguous;
+ * block_table [batch, max_blocks] int32; ctx_len [batch] int32 = cache length BEFORE the
+ * append (flash_attn cache_seqlens); o [batch, nq, NH, HD]; scratch fp32
+ * [batch*nq*NH*nsplit*(HD+2)] (caller-allocated); lse_out [batch*nq*NH] or NULL.
+ * New token tk of sequence b sits at position ctx_len[b]+tk and sees keys
+ * [max(leftpad[b], pos-window+1 if window>=0), ctx_len[b] + (append ? tk+1 : 0)).
+ * page must be a power of two. rotary: 0 none, 1 neox (half split), 2 interleaved (pairs);
+ * cos/sin tables [seqlen_ro, rotary_dim/2] fp32, row chosen by (rotary_pos ? rotary_pos[b] :
+ * ctx_len[b]) + tk; rotary_dim 0 means HD. */
+typedef struct DecParams {
+  const void* q;
+  const void* Kc;
+  const void* Vc;
+  const int32_t* block_table;
+  void* o;
+  float* scratch;
+  const int32_t* ctx_len;
+  const float* cos;
+  const float* sin;
+  int32_t batch, NH, gqa, HD, page, max_blocks, nsplit, window;
+  int32_t rotary;
+  float scale;
+  const int32_t* leftpad;
+  float* lse_out;
+  float softcap;
+  const float* alibi;
+  int32_t nq;
+  int32_t rotary_dim;
+  const int32_t* rotary_pos;
+} DecParams;
+
+/* LSE-weighted merge of split partial results (flash_attn_combine).
+ * Reference: package/fable_attn/flash_attn_interface.py:567-580 (pure torch there).
+ * out_partial [nsplit, B, S, H, D] (dtype of in_dtype) with element strides
+ * op_s (split), op_b, op_s_seq, op_h (D contiguous); lse_partial [nsplit, B, H, S] fp32 with
+ * strides lp_s, lp_b, lp_h, lp_seq; out [B, S, H, D] dense in out_dtype. */
+typedef struct CombineParams {
+  const void* out_partial;
+  const float* lse_partial;
+  void* out;
+  int32_t nsplit, B, S, H, D;
+  int64_t op_split, op_b, op_seq, op_h;
+  int64_t lp_split, lp_b, lp_h, lp_seq;
+  int32_t in_dtype, out_dtype;
+} CombineParams;
+
+/* Entry points. Each returns FA_OK or an FA_ERR_* code; work is enqueued asynchronously on
+ * `stream`; nothing is allocated or freed; every pointer is device memory. */
+
+/* replaces fa_iface.h:65  void fa_forward_launch(FwdParams p, int dtype, void* stream) */
+int fa_forward_launch(FwdParams p, int dtype, void* stream);
+
+/* replaces fa_iface.h:66  void fable_attn_backward_launch(BwdParams pr, int MODE, void* stream) */
+int fable_attn_backward_launch(BwdParams p, int dtype, void* stream);
+
+/* replaces fa_iface.h:67-68  void fa_decode_launch(DecParams p, int dtype, void* stream,
+ *                                                  const void* new_k, const void* new_v)
+ * new_k/new_v [batch, nq, NH/gqa, HD] (NULL = no append) are written into the paged cache
+ * (with rotary on k) before attention, in stream order: no device-wide synchronisation. */
+int fa_decode_launch(DecParams p, int dtype, void* stream, const void* new_k, const void* new_v);
+
+/* split count chosen for a decode call (reference heuristic: dispatch.cpp:182-200, retuned for
+ * 256 CUs); num_splits_hint > 0 is honoured (clamped to [1, 512]). */
+int fa_decode_num_splits(int batch, int nq, int NH, int gqa, int64_t ctx_bound, int num_splits_hint);
+
+/* flash_attn_combine as a kernel (the reference computes it with torch ops). */
+int fa_combine_launch(CombineParams p, void* stream);
+
+/* introspection for bindings and tests */
+int fable_attn_abi_version(void);
+size_t fable_attn_struct_size(int which); /* 0 FwdParams, 1 BwdParams, 2 DecParams, 3 CombineParams, 4 fa_strides */
+const char* fable_attn_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FABLE_ATTN_ABI_H */

@@ -1,0 +1,299 @@
+/*
+ * oracle.c — fp64 CPU restatement of the reference's attention oracles.
+ *
+ * TEST INFRASTRUCTURE ONLY. Nothing in the shipped library links, loads or calls this code; it
+ * is the checker used by tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg.
+ *
+ * Every routine accumulates in double, takes inputs that the caller has already rounded to the
+ * storage dtype (fp16/bf16 values held in float), and follows a reference routine:
+ *   oracle_fwd      kernels/fa_common.hpp:102-134 (ref_attention): mask order causal,
+ *                   window left/right, chunk; softcap before alibi; alibi slope*(j-i);
+ *                   a row with no visible key gives O = 0 and LSE = -inf.
+ *                   Batch/GQA indexing as kernels/fa_forward_gate.inc:33-47.
+ *   oracle_bwd      kernels/backward.hip:566-597 (fp64 backward of the gate): recompute P from
+ *                   the exact forward, Di = sum(O*dO), dS = P*(dP - Di)*softcap'(.), dQ,dK,dV.
+ *                   Dropout is not restated (the kernels here do not implement it).
+ *   oracle_decode   kernels/fa_decode_gate.inc:19-25 (rot_at) and :66-96 (oracle loop): new
+ *                   tokens at ctx+tk, causal among new tokens via append, window lo =
+ *                   qpos-window+1, leftpad, softcap, alibi slope*(pos-qpos), rotary (neox /
+ *                   interleaved) applied to q and to appended k at their positions.
+ *
+ * Layouts (all contiguous, float):
+ *   fwd/bwd: Q,O,dO,dQ [B][H][SQ][D]; K,V,dK,dV [B][Hk][SK][D]; LSE [B][H][SQ].
+ *   decode:  q,o [B][nq][H][D]; Kc,Vc [nblocks][page][Hk][D]; block_table [B][max_blocks];
+ *            new_k,new_v [B][nq][Hk][D]; cos,sin [seqlen_ro][rdim/2]; lse [B][nq][H].
+ *
+ * Build: oracle/Makefile (gcc -O2 -fopenmp, no fast-math).
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+typedef struct OracleCfg {
+  int B, H, Hk, SQ, SK, D;
+  double scale, softcap;
+  int win_left, win_right, causal, attn_chunk;
+  const float* alibi; /* [H] or NULL */
+} OracleCfg;
+
+/* visibility of key j to query i — fa_common.hpp:111-118 */
+static int visible(const OracleCfg* c, int i, int j) {
+  const int delta = c->SK - c->SQ;
+  if (c->causal && j > i + delta) return 0;
+  if (c->win_left >= 0 && j < i + delta - c->win_left) return 0;
+  if (c->win_right >= 0 && j > i + delta + c->win_right) return 0;
+  if (c->attn_chunk > 0) {
+    int pp = i + delta;
+    if (pp < 0) pp = 0;
+    int cs = (pp / c->attn_chunk) * c->attn_chunk;
+    if (j < cs || j >= cs + c->attn_chunk) return 0;
+  }
+  return 1;
+}
+
+/* logit of (i, j) — fa_common.hpp:119-123; also returns d(logit)/d(scale*qk) for softcap */
+static double logit(const OracleCfg* c, int h, int i, int j, const float* q, const float* k,
+                    double* deriv) {
+  double s = 0.0;
+  for (int d = 0; d < c->D; d++) s += (double)q[d] * (double)k[d];
+  s *= c->scale;
+  double dv = 1.0;
+  if (c->softcap > 0) {
+    double t = tanh(s / c->softcap);
+    s = c->softcap * t;
+    dv = 1.0 - t * t;
+  }
+  if (c->alibi) s += (double)c->alibi[h] * (double)(j - i);
+  if (deriv) *deriv = dv;
+  return s;
+}
+
+/* Forward. rows: optional list of query indices (n_rows entries) to evaluate for every (b,h);
+ * NULL means all SQ rows. Rows not evaluated are left untouched in O/LSE. */
+void oracle_fwd(const float* Q, const float* K, const float* V, float* O, float* LSE,
+                const OracleCfg* c, const int32_t* rows, int n_rows) {
+  const int gqa = c->H / c->Hk;
+  const int nr = rows ? n_rows : c->SQ;
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int b = 0; b < c->B; b++)
+    for (int h = 0; h < c->H; h++) {
+      const int kvh = h / gqa;
+      double* pr = (double*)malloc(sizeof(double) * (size_t)(c->SK > 0 ? c->SK : 1));
+      const float* Kb = K + ((size_t)b * c->Hk + kvh) * (size_t)c->SK * c->D;
+      const float* Vb = V + ((size_t)b * c->Hk + kvh) * (size_t)c->SK * c->D;
+      for (int r = 0; r < nr; r++) {
+        const int i = rows ? rows[r] : r;
+        const float* q = Q + (((size_t)b * c->H + h) * c->SQ + i) * c->D;
+        double mx = -INFINITY;
+        int cnt = 0;
+        for (int j = 0; j < c->SK; j++) {
+          if (!visible(c, i, j)) { pr[j] = -INFINITY; continue; }
+          double s = logit(c, h, i, j, q, Kb + (size_t)j * c->D, NULL);
+          pr[j] = s;
+          if (s > mx) mx = s;
+          cnt++;
+        }
+        double sum = 0.0;
+        for (int j = 0; j < c->SK; j++) {
+          if (pr[j] == -INFINITY) { pr[j] = 0.0; continue; }
+          pr[j] = exp(pr[j] - mx);
+          sum += pr[j];
+        }
+        float* o = O + (((size_t)b * c->H + h) * c->SQ + i) * c->D;
+        for (int d = 0; d < c->D; d++) {
+          double acc = 0.0;
+          for (int j = 0; j < c->SK; j++) acc += pr[j] * (double)Vb[(size_t)j * c->D + d];
+          o[d] = (float)(cnt ? acc / sum : 0.0);
+        }
+        if (LSE) LSE[((size_t)b * c->H + h) * c->SQ + i] = cnt ? (float)(mx + log(sum)) : -INFINITY;
+      }
+      free(pr);
+    }
+}
+
+/* Backward (exact fp64 gradients of the forward above). dQ/dK/dV are double outputs,
+ * overwritten. dO [B][H][SQ][D]. */
+void oracle_bwd(const float* Q, const float* K, const float* V, const float* dO, double* dQ,
+                double* dK, double* dV, const OracleCfg* c) {
+  const int gqa = c->H / c->Hk;
+  const size_t nq = (size_t)c->B * c->H * c->SQ * c->D, nk = (size_t)c->B * c->Hk * c->SK * c->D;
+  memset(dQ, 0, nq * sizeof(double));
+  memset(dK, 0, nk * sizeof(double));
+  memset(dV, 0, nk * sizeof(double));
+  /* parallel over (b, kv head): each task owns dK/dV of its kv head and dQ of its q heads */
+#pragma omp parallel for collapse(2) schedule(dynamic)
+  for (int b = 0; b < c->B; b++)
+    for (int kvh = 0; kvh < c->Hk; kvh++) {
+      double* P = (double*)malloc(sizeof(double) * (size_t)(c->SK > 0 ? c->SK : 1));
+      double* Dv = (double*)malloc(sizeof(double) * (size_t)(c->SK > 0 ? c->SK : 1));
+      double* o = (double*)malloc(sizeof(double) * (size_t)c->D);
+      const float* Kb = K + ((size_t)b * c->Hk + kvh) * (size_t)c->SK * c->D;
+      const float* Vb = V + ((size_t)b * c->Hk + kvh) * (size_t)c->SK * c->D;
+      double* dKb = dK + ((size_t)b * c->Hk + kvh) * (size_t)c->SK * c->D;
+      double* dVb = dV + ((size_t)b * c->Hk + kvh) * (size_t)c->SK * c->D;
+      for (int h = kvh * gqa; h < (kvh + 1) * gqa; h++)
+        for (int i = 0; i < c->SQ; i++) {
+          const size_t qo = (((size_t)b * c->H + h) * c->SQ + i) * c->D;
+          const float* q = Q + qo;
+          const float* g = dO + qo;
+          double mx = -INFINITY;
+          int cnt = 0;
+          for (int j = 0; j < c->SK; j++) {
+            if (!visible(c, i, j)) { P[j] = -INFINITY; continue; }
+            double dv;
+            P[j] = logit(c, h, i, j, q, Kb + (size_t)j * c->D, &dv);
+            Dv[j] = dv;
+            if (P[j] > mx) mx = P[j];
+            cnt++;
+          }
+          if (!cnt) continue;
+          double sum = 0.0;
+          for (int j = 0; j < c->SK; j++) {
+            if (P[j] == -INFINITY) { P[j] = 0.0; continue; }
+            P[j] = exp(P[j] - mx);
+            sum += P[j];
+          }
+          for (int j = 0; j < c->SK; j++) P[j] /= sum;
+          /* O (exact) and Di = sum_d O*dO — backward.hip:576-579 */
+          double Di = 0.0;
+          for (int d = 0; d < c->D; d++) {
+            double acc = 0.0;
+            for (int j = 0; j < c->SK; j++) acc += P[j] * (double)Vb[(size_t)j * c->D + d];
+            o[d] = acc;
+            Di += acc * (double)g[d];
+          }
+          double* dq = dQ + qo;
+          for (int j = 0; j < c->SK; j++) {
+            if (P[j] == 0.0 && !visible(c, i, j)) continue;
+            double dp = 0.0;
+            for (int d = 0; d < c->D; d++) dp += (double)g[d] * (double)Vb[(size_t)j * c->D + d];
+            const double dS = P[j] * (dp - Di) * Dv[j]; /* backward.hip:585 */
+            for (int d = 0; d < c->D; d++) {
+              dVb[(size_t)j * c->D + d] += P[j] * (double)g[d];
+              dKb[(size_t)j * c->D + d] += c->scale * dS * (double)q[d];
+              dq[d] += c->scale * dS * (double)Kb[(size_t)j * c->D + d];
+            }
+          }
+        }
+      free(P);
+      free(Dv);
+      free(o);
+    }
+}
+
+typedef struct OracleDecCfg {
+  int B, nq, H, Hk, D, page, max_blocks;
+  double scale, softcap;
+  int window;  /* <0 off: number of keys back from the query position */
+  int rotary;  /* 0 none, 1 neox, 2 interleaved */
+  int rdim;    /* rotary dim (0 => D) */
+  int append;  /* new_k/new_v present */
+  const float* alibi; /* [H] or NULL */
+} OracleDecCfg;
+
+/* rot_at — fa_decode_gate.inc:20-25, generalised to rotary_dim <= D */
+static void rot_at(double* v, int rdim, const float* cs, const float* sn, int mode, int pos) {
+  const int half = rdim / 2;
+  const float* c = cs + (size_t)pos * half;
+  const float* s = sn + (size_t)pos * half;
+  if (mode == 1) {
+    for (int d = 0; d < half; d++) {
+      double x = v[d], y = v[d + half];
+      v[d] = x * c[d] - y * s[d];
+      v[d + half] = y * c[d] + x * s[d];
+    }
+  } else if (mode == 2) {
+    for (int d = 0; d < half; d++) {
+      double x = v[2 * d], y = v[2 * d + 1];
+      v[2 * d] = x * c[d] - y * s[d];
+      v[2 * d + 1] = y * c[d] + x * s[d];
+    }
+  }
+}
+
+/* Decode oracle — fa_decode_gate.inc:66-96. leftpad/rotary_pos may be NULL. */
+void oracle_decode(const float* q, const float* Kc, const float* Vc, const int32_t* block_table,
+                   const int32_t* ctx_len, const float* new_k, const float* new_v,
+                   const float* cos_t, const float* sin_t, const int32_t* leftpad,
+                   const int32_t* rotary_pos, float* o, float* lse, const OracleDecCfg* c) {
+  const int gqa = c->H / c->Hk;
+  const int rdim = c->rdim > 0 ? c->rdim : c->D;
+#pragma omp parallel for collapse(3) schedule(dynamic)
+  for (int b = 0; b < c->B; b++)
+    for (int tk = 0; tk < c->nq; tk++)
+      for (int h = 0; h < c->H; h++) {
+        const int kvh = h / gqa;
+        const int ctx = ctx_len[b];
+        const int qpos = ctx + tk;
+        const int rp = (rotary_pos ? rotary_pos[b] : ctx) + tk;
+        const int cend = ctx + (c->append ? tk + 1 : 0);
+        int lo = 0;
+        if (c->window >= 0 && qpos - c->window + 1 > lo) lo = qpos - c->window + 1;
+        if (leftpad && leftpad[b] > lo) lo = leftpad[b];
+        double* qr = (double*)malloc(sizeof(double) * c->D);
+        double* kk = (double*)malloc(sizeof(double) * c->D);
+        double* pr = (double*)malloc(sizeof(double) * (size_t)(cend > 0 ? cend : 1));
+        const float* qs = q + (((size_t)b * c->nq + tk) * c->H + h) * c->D;
+        for (int d = 0; d < c->D; d++) qr[d] = qs[d];
+        if (c->rotary) rot_at(qr, rdim, cos_t, sin_t, c->rotary, rp);
+        double mx = -INFINITY;
+        for (int pos = 0; pos < cend; pos++) {
+          pr[pos] = -INFINITY;
+          if (pos < lo) continue;
+          if (c->append && pos >= ctx) {
+            const float* nk = new_k + (((size_t)b * c->nq + (pos - ctx)) * c->Hk + kvh) * c->D;
+            for (int d = 0; d < c->D; d++) kk[d] = nk[d];
+            if (c->rotary) rot_at(kk, rdim, cos_t, sin_t, c->rotary, rp - tk + (pos - ctx));
+          } else {
+            const int blk = block_table[(size_t)b * c->max_blocks + pos / c->page];
+            const float* kp = Kc + (((size_t)blk * c->page + pos % c->page) * c->Hk + kvh) * c->D;
+            for (int d = 0; d < c->D; d++) kk[d] = kp[d];
+          }
+          double s = 0.0;
+          for (int d = 0; d < c->D; d++) s += qr[d] * kk[d];
+          s *= c->scale;
+          if (c->softcap > 0) s = c->softcap * tanh(s / c->softcap);
+          if (c->alibi) s += (double)c->alibi[h] * (double)(pos - qpos);
+          pr[pos] = s;
+          if (s > mx) mx = s;
+        }
+        double sum = 0.0;
+        for (int pos = 0; pos < cend; pos++) {
+          if (pr[pos] == -INFINITY) { pr[pos] = 0.0; continue; }
+          pr[pos] = exp(pr[pos] - mx);
+          sum += pr[pos];
+        }
+        float* os = o + (((size_t)b * c->nq + tk) * c->H + h) * c->D;
+        for (int d = 0; d < c->D; d++) {
+          double acc = 0.0;
+          for (int pos = 0; pos < cend; pos++) {
+            if (pr[pos] == 0.0) continue;
+            float vv;
+            if (c->append && pos >= ctx)
+              vv = new_v[(((size_t)b * c->nq + (pos - ctx)) * c->Hk + kvh) * c->D + d];
+            else {
+              const int blk = block_table[(size_t)b * c->max_blocks + pos / c->page];
+              vv = Vc[(((size_t)blk * c->page + pos % c->page) * c->Hk + kvh) * c->D + d];
+            }
+            acc += pr[pos] * (double)vv;
+          }
+          os[d] = (float)(sum > 0 ? acc / sum : 0.0);
+        }
+        if (lse) lse[((size_t)b * c->nq + tk) * c->H + h] = sum > 0 ? (float)(mx + log(sum)) : -INFINITY;
+        free(qr);
+        free(kk);
+        free(pr);
+      }
+}
+
+/* rel_rms — fa_common.hpp:136-139 (||got-ref||_2 / ||ref||_2) */
+double oracle_rel_rms(const float* got, const float* ref, size_t n) {
+  double e = 0, r = 0;
+  for (size_t i = 0; i < n; i++) {
+    double d = (double)got[i] - ref[i];
+    e += d * d;
+    r += (double)ref[i] * ref[i];
+  }
+  return r > 0 ? sqrt(e / r) : sqrt(e);
+}

@@ -1,0 +1,149 @@
+"""Forward parity on the GPU: HIP kernels (through the C-ABI via fable_attn._C) vs the fp64
+oracle on identical seeded inputs.
+
+Cases follow the reference forward gate (kernels/fa_forward_gate.inc:170-211: causal, GQA,
+SQ != SK bottom-right, empty rows, windows, softcap, alibi, head dims, attention_chunk, varlen
++/- seqused) at the BASELINE.json tolerances: rel_rms <= 5e-4 (fp16) / 4e-3 (bf16), LSE within
+1e-3 absolute, empty rows exactly O = 0 and LSE = -inf.
+"""
+import math
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.helpers import LSE_ABS, TOL, gen, lse_err, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+# name, B, SQ, SK, D, H, gqa, causal, wl, wr, softcap, alibi, chunk
+CASES = [
+    ("C1 d64 full S1024 H8", 1, 1024, 1024, 64, 8, 1, False, -1, -1, 0.0, False, 0),
+    ("d128 causal GQA4", 1, 256, 256, 128, 32, 4, True, -1, -1, 0.0, False, 0),
+    ("d128 causal GQA1 B2", 2, 256, 256, 128, 8, 1, True, -1, -1, 0.0, False, 0),
+    ("d128 full", 1, 192, 192, 128, 16, 4, False, -1, -1, 0.0, False, 0),
+    ("d128 SQ<SK bottom-right", 1, 128, 320, 128, 16, 4, True, -1, -1, 0.0, False, 0),
+    ("d128 SQ>SK empty rows", 1, 256, 64, 128, 16, 4, True, -1, -1, 0.0, False, 0),
+    ("window (63,0)", 1, 256, 256, 128, 16, 4, True, 63, 0, 0.0, False, 0),
+    ("window (32,32)", 1, 256, 256, 128, 16, 4, False, 32, 32, 0.0, False, 0),
+    ("window (0,0) diagonal", 1, 256, 256, 128, 16, 4, False, 0, 0, 0.0, False, 0),
+    ("window (0,-1)", 1, 256, 256, 128, 16, 4, False, 0, -1, 0.0, False, 0),
+    ("window (16,48)", 1, 192, 192, 128, 16, 4, False, 16, 48, 0.0, False, 0),
+    ("window (32,32) SQ<SK", 1, 128, 320, 128, 16, 4, False, 32, 32, 0.0, False, 0),
+    ("softcap 30", 1, 200, 200, 128, 16, 4, True, -1, -1, 30.0, False, 0),
+    ("alibi", 1, 200, 200, 128, 16, 4, True, -1, -1, 0.0, True, 0),
+    ("d64 causal ragged", 1, 200, 200, 64, 16, 4, True, -1, -1, 0.0, False, 0),
+    ("d256 causal", 1, 160, 160, 256, 8, 4, True, -1, -1, 0.0, False, 0),
+    ("d256 full SQ<SK", 1, 96, 200, 256, 8, 2, False, -1, -1, 0.0, False, 0),
+    ("chunk 64 causal", 1, 256, 256, 128, 16, 4, True, -1, -1, 0.0, False, 64),
+    ("chunk 100 causal", 1, 256, 256, 128, 16, 4, True, -1, -1, 0.0, False, 100),
+    ("chunk 128 full", 1, 256, 256, 128, 16, 4, False, -1, -1, 0.0, False, 128),
+    ("chunk 64 SQ<SK", 1, 128, 320, 128, 16, 4, True, -1, -1, 0.0, False, 64),
+    ("d256 window+softcap (C5 features)", 1, 300, 300, 256, 16, 1, True, 64, 0, 30.0, False, 0),
+]
+
+
+def _alibi(H):
+    return (-np.float32(2.0) ** (-(8.0 * np.arange(1, H + 1) / H))).astype(np.float32)
+
+
+def run_case(case, dt, seed=0):
+    import torch
+
+    from fable_attn import _C
+    name, B, SQ, SK, D, H, gqa, causal, wl, wr, sc, alibi, chunk = case
+    Hk = H // gqa
+    q = gen((B, H, SQ, D), seed + 1, dt)
+    k = gen((B, Hk, SK, D), seed + 2, dt)
+    v = gen((B, Hk, SK, D), seed + 3, dt)
+    al = _alibi(H) if alibi else None
+    scale = 1.0 / math.sqrt(D)
+    o_ref, l_ref = orc.fwd(q, k, v, scale, causal, wl, wr, sc, al, chunk)
+    # kernel: BSHD storage (the public API layout), [B,H,S,D] views
+    qd = to_dev(q, dt).transpose(1, 2).contiguous().transpose(1, 2)
+    kd = to_dev(k, dt).transpose(1, 2).contiguous().transpose(1, 2)
+    vd = to_dev(v, dt).transpose(1, 2).contiguous().transpose(1, 2)
+    ald = torch.from_numpy(al).cuda() if al is not None else None
+    out, lse = _C.fwd(qd, kd, vd, scale, causal, wl, wr, sc, ald, 0.0, 0, chunk)
+    torch.cuda.synchronize()
+    return to_np(out), to_np(lse), o_ref, l_ref
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+def test_forward_parity(case, dt):
+    print(f"[fwd] {case[0]} {dt}", flush=True)
+    o, l, o_ref, l_ref = run_case(case, dt)
+    rel = orc.rel_rms(o, o_ref)
+    lerr, inf_ok = lse_err(l, l_ref)
+    empty = np.isneginf(l_ref)
+    assert np.isfinite(o).all(), "non-finite output"
+    assert rel <= TOL[dt], f"rel_rms {rel:.3e} > {TOL[dt]}"
+    assert inf_ok, "empty-row LSE (-inf) pattern differs"
+    assert lerr <= LSE_ABS, f"LSE abs err {lerr:.3e}"
+    if empty.any():
+        rows = np.broadcast_to(empty[..., None], o.shape)
+        assert (o[rows] == 0).all(), "empty rows must be exactly zero"
+
+
+def test_forward_deterministic():
+    case = CASES[1]
+    a = run_case(case, "f16", seed=5)
+    b = run_case(case, "f16", seed=5)
+    assert np.array_equal(a[0], b[0]) and np.array_equal(a[1], b[1])
+
+
+def _varlen(dt, lens, used_q=None, used_k=None, D=128, H=8, gqa=4, causal=True, wl=-1, wr=-1,
+            sc=0.0, seed=11):
+    import torch
+
+    from fable_attn import _C
+    Hk = H // gqa
+    tot = sum(lens)
+    cu = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    q = gen((tot, H, D), seed + 1, dt)
+    k = gen((tot, Hk, D), seed + 2, dt)
+    v = gen((tot, Hk, D), seed + 3, dt)
+    scale = 1.0 / math.sqrt(D)
+    o_ref = np.zeros_like(q)
+    l_ref = np.full((H, tot), -np.inf, dtype=np.float32)
+    for i, L in enumerate(lens):
+        lq = used_q[i] if used_q else L
+        lk = used_k[i] if used_k else L
+        a = int(cu[i])
+        qs = q[a:a + lq].transpose(1, 0, 2)[None]
+        ks = k[a:a + lk].transpose(1, 0, 2)[None]
+        vs = v[a:a + lk].transpose(1, 0, 2)[None]
+        o, l = orc.fwd(qs, ks, vs, scale, causal, wl, wr, sc)
+        o_ref[a:a + lq] = o[0].transpose(1, 0, 2)
+        l_ref[:, a:a + lq] = l[0]
+    cut = torch.from_numpy(cu).cuda()
+    uq = torch.tensor(used_q, dtype=torch.int32).cuda() if used_q else None
+    uk = torch.tensor(used_k, dtype=torch.int32).cuda() if used_k else None
+    out, lse = _C.fwd_varlen(to_dev(q, dt), to_dev(k, dt), to_dev(v, dt), cut, cut, max(lens),
+                             max(lens), scale, causal, wl, wr, sc, None, 0.0, 0, 0, uq, uk,
+                             return_lse=True)
+    torch.cuda.synchronize()
+    o, l = to_np(out), to_np(lse)
+    if used_q:
+        for i, L in enumerate(lens):   # rows past seqused_q are not part of the result
+            a = int(cu[i])
+            l[:, a + used_q[i]:a + L] = -np.inf
+    return o, l, o_ref, l_ref
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("kind", ["plain", "seqused", "window_softcap_d256"])
+def test_varlen_parity(kind, dt):
+    print(f"[varlen] {kind} {dt}", flush=True)
+    if kind == "plain":
+        r = _varlen(dt, [100, 64, 200])
+    elif kind == "seqused":
+        r = _varlen(dt, [100, 64, 200], used_q=[70, 64, 150], used_k=[90, 30, 180])
+    else:
+        r = _varlen(dt, [300, 77, 512, 129], D=256, H=16, gqa=1, wl=64, wr=0, sc=30.0)
+    o, l, o_ref, l_ref = r
+    rel = orc.rel_rms(o, o_ref)
+    lerr, inf_ok = lse_err(l, l_ref)
+    assert rel <= TOL[dt], f"rel_rms {rel:.3e}"
+    assert inf_ok and lerr <= LSE_ABS, f"LSE err {lerr:.3e} inf_ok={inf_ok}"
