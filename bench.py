@@ -1,0 +1,234 @@
+"""Benchmark of the hot path on one MI355X (driver contract: one JSON line on stdout).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extras fwd,bwd,decode,varlen]
+
+A step is one pass of the hot path over one batch of synthetic input:
+  headline (`value`): BASELINE.json configs[1], causal fp16 forward through flash_attn_func,
+  B=1, S=16384, H=32, D=128, q/k/v ~ N(0,1) resident in HBM before timing.
+  TFLOP/s counts the causal half only: 2*B*H*S^2*D (reference convention,
+  lab/bench_e2e.py:137-138).
+`roofline` reports the dominant kernel (the forward kernel): algorithmic FLOP per launch divided
+by its average duration, measured with HIP events on the stream the kernel is launched on
+(torch's current stream), against the dense fp16 MFMA peak of 2.5 PFLOP/s.
+`cpu_baseline` times the exact fp32 torch reference (oracle/torch_ref.py) on the host cores over
+a bounded sample of heads of the same workload and scales to TFLOP/s with the same numerator.
+`extra` holds the other BASELINE.json configs (backward, paged decode, varlen) measured the
+same way; they are not the headline.
+"""
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path[:0] = [ROOT, os.path.join(ROOT, "flash-attention-rdna2_amd")]
+
+PEAK_MFMA_TFLOPS = 2500.0   # MI355X dense fp16/bf16 MFMA
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+METRIC = "fwd/bwd TFLOP/s (% MFMA peak), paged decode GB/s (% HBM peak), 1×MI355X"
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def time_steps(fn, steps, warmup):
+    """Returns (wall ms/step, HIP-event ms/step) over exactly `steps` calls after `warmup`."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    st = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(st)
+    for _ in range(steps):
+        fn()
+    e1.record(st)
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3 / steps
+    ev = e0.elapsed_time(e1) / steps
+    return wall, ev
+
+
+def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", seed=0):
+    import torch
+    from fable_attn import flash_attn_func
+    dt = torch.float16 if dtype == "fp16" else torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q = torch.randn(B, S, H, D, device="cuda", dtype=dt, generator=g)
+    k = torch.randn(B, S, H, D, device="cuda", dtype=dt, generator=g)
+    v = torch.randn(B, S, H, D, device="cuda", dtype=dt, generator=g)
+    flops = 4.0 * B * H * S * S * D / (2 if causal else 1)
+    wall, ev = time_steps(lambda: flash_attn_func(q, k, v, causal=causal), steps, warmup)
+    return {"S": S, "H": H, "D": D, "B": B, "causal": causal, "dtype": dtype, "flops": flops,
+            "ms": wall, "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
+            "kernel_tflops": flops / (ev * 1e-3) / 1e12}
+
+
+def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0):
+    """C3: causal bf16 backward, timed without the forward; bitwise-identical check over 3 runs."""
+    import torch
+    from fable_attn import _C
+    from fable_attn.flash_attn_interface import _kernel_view
+    dt = torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q, k, v, do = (torch.randn(B, S, H, D, device="cuda", dtype=dt, generator=g) for _ in range(4))
+    qh, kh, vh, doh = (_kernel_view(x) for x in (q, k, v, do))
+    scale = D ** -0.5
+    out, lse = _C.fwd(qh, kh, vh, scale, True, -1, 0, 0.0, None, 0.0, 0)
+
+    def step():
+        return _C.bwd(doh, qh, kh, vh, out, lse, scale, True, -1, 0, 0.0, None, 0.0, 0)
+    ref = step()
+    same = all(all(torch.equal(a, b) for a, b in zip(ref, step())) for _ in range(2))
+    wall, ev = time_steps(step, steps, warmup)
+    flops = 2.5 * 4.0 * B * H * S * S * D / 2
+    return {"B": B, "S": S, "H": H, "D": D, "dtype": "bf16", "flops": flops, "ms": wall,
+            "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
+            "bitwise_identical_x3": bool(same)}
+
+
+def bench_decode(steps, warmup, batch=16, Hq=32, Hk=8, D=128, ctx=32768, page=256, seed=0):
+    """C4: paged-KV decode fp16, block_table = seeded permutation of the physical pages."""
+    import torch
+    from fable_attn import flash_attn_with_kvcache
+    dt = torch.float16
+    nblk = batch * ctx // page
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    kc = torch.randn(nblk, page, Hk, D, device="cuda", dtype=dt, generator=g)
+    vc = torch.randn(nblk, page, Hk, D, device="cuda", dtype=dt, generator=g)
+    q = torch.randn(batch, 1, Hq, D, device="cuda", dtype=dt, generator=g)
+    cg = torch.Generator().manual_seed(seed)
+    bt = torch.randperm(nblk, generator=cg).view(batch, ctx // page).int().cuda()
+    cs = torch.full((batch,), ctx, dtype=torch.int32, device="cuda")
+    f = lambda: flash_attn_with_kvcache(q, kc, vc, cache_seqlens=cs, block_table=bt)
+    wall, ev = time_steps(f, steps, warmup)
+    nbytes = 2.0 * batch * ctx * Hk * D * 2
+    return {"batch": batch, "Hq": Hq, "Hk": Hk, "D": D, "ctx": ctx, "page": page, "bytes": nbytes,
+            "ms": wall, "kernel_ms": ev, "GBs": nbytes / (wall * 1e-3) / 1e9,
+            "frac_hbm": nbytes / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS}
+
+
+def bench_varlen(steps, warmup, H=16, D=256, seed=0):
+    """C5: varlen bf16, 8 sequences with lengths ~U[512, 8192] (seeded), window (512,0) +
+    causal, softcap 30; FLOP counts exact unmasked pairs."""
+    import torch
+    from fable_attn import flash_attn_varlen_func
+    cg = torch.Generator().manual_seed(seed)
+    lens = torch.randint(512, 8193, (8,), generator=cg).tolist()
+    cu = torch.tensor([0] + list(__import__("itertools").accumulate(lens)), dtype=torch.int32, device="cuda")
+    T = sum(lens)
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    q, k, v = (torch.randn(T, H, D, device="cuda", dtype=torch.bfloat16, generator=g) for _ in range(3))
+    f = lambda: flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), causal=True,
+                                       window_size=(512, 0), softcap=30.0, softmax_scale=D ** -0.5)
+    wall, ev = time_steps(f, steps, warmup)
+    pairs = sum(sum(min(i, 512) + 1 for i in range(L)) for L in lens)
+    flops = 4.0 * D * H * pairs
+    return {"lens": lens, "H": H, "D": D, "flops": flops, "ms": wall, "kernel_ms": ev,
+            "tflops": flops / (wall * 1e-3) / 1e12}
+
+
+def cpu_baseline(S=16384, H=32, D=128, heads=2, seed=0):
+    """Exact fp32 torch reference on the host cores, `heads` of the H heads of the headline
+    workload (one head at a time to bound memory), scaled to the full workload's FLOP rate."""
+    import torch
+    from oracle.torch_ref import attention_bhsd
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(1, 1, S, D, generator=g).half().float() for _ in range(3))
+    attention_bhsd(q[:, :, :256], k[:, :, :256], v[:, :, :256], D ** -0.5, causal=True)  # warm
+    t0 = time.perf_counter()
+    for _ in range(heads):
+        attention_bhsd(q, k, v, D ** -0.5, causal=True)
+    dt = time.perf_counter() - t0
+    flops = 4.0 * heads * S * S * D / 2
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{heads} of {H} heads of the causal S={S} D={D} forward, fp32 torch "
+                      f"reference on CPU tensors, {dt:.1f} s; rate scales linearly to all heads"}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-heads", type=int, default=2)
+    ap.add_argument("--extras", default="fwd,bwd,decode,varlen")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="also run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
+    a = ap.parse_args()
+    if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build measures one GPU only (the reference has no multi-GPU "
+              "path); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    if not torch.cuda.is_available():
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(2)
+
+    log("[bench] headline: causal fp16 forward S=16384 H=32 D=128")
+    head = bench_fwd(16384, a.steps, a.warmup)
+    log(f"[bench] fwd S=16384: {head['ms']:.3f} ms  {head['tflops']:.1f} TFLOP/s")
+    extra = {}
+    for name in [x for x in a.extras.split(",") if x]:
+        try:
+            if name == "fwd":
+                for S in (4096, 8192):
+                    extra[f"fwd_causal_S{S}"] = bench_fwd(S, max(a.steps, 10), a.warmup)
+                extra["fwd_C1_S1024_D64_noncausal"] = bench_fwd(1024, 20, 3, causal=False, H=8, D=64)
+            elif name == "bwd":
+                extra["bwd_C3"] = bench_bwd(max(5, a.steps // 2), 2)
+            elif name == "decode":
+                extra["decode_C4"] = bench_decode(max(a.steps, 20), a.warmup)
+            elif name == "varlen":
+                extra["varlen_C5"] = bench_varlen(max(5, a.steps // 2), 2)
+            log(f"[bench] extra {name} done")
+        except RuntimeError as e:
+            extra[name] = {"error": str(e)[:300]}
+            log(f"[bench] extra {name}: {e}")
+    if a.copy_calib:
+        x = torch.empty(1 << 29, dtype=torch.float16, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            y.copy_(x)
+        torch.cuda.synchronize()
+        extra["copy_calib_bytes_each_way"] = x.numel() * 2
+    cpu = None
+    if not a.no_cpu:
+        log("[bench] cpu baseline")
+        cpu = cpu_baseline(heads=a.cpu_heads)
+        log(f"[bench] cpu: {cpu['value']:.4f} TFLOP/s on {cpu['cores']} cores")
+    ach = head["kernel_tflops"]
+    line = {
+        "metric": METRIC,
+        "value": round(head["tflops"], 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(head["ms"], 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic",
+        "config": {"workload": "flash_attn_func causal fp16 forward (BASELINE.json configs[1])",
+                   "batch": 1, "seq_len": 16384, "heads": 32, "head_dim": 128,
+                   "causal": True, "flop_per_step": head["flops"]},
+        "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_MFMA_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(ach / PEAK_MFMA_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+        "extra": extra,
+    }
+    print(json.dumps(line))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,13 +1,389 @@
-// decode.hip — paged decode entry points (kernels land in a following change).
+// decode.hip — paged-KV split-KV decode for gfx950: KV append, partial attention per split,
+// LSE-weighted combine.
+//
+// Replaces the reference decode (kernels/fa_decode.hip: fd_partial :57-252, fd_combine
+// :255-272, fd_append :275-302, launcher :319-362) with the same DecParams contract
+// (include/fable_attn_abi.h) and a different design:
+//  * one workgroup (4 waves) per (sequence*new token, kv head, 16-head group, split); the q
+//    heads sharing the kv head are packed into the N=16 dimension of v_mfma_f32_16x16x32, so
+//    K and V are read from HBM once per kv head whatever the GQA ratio;
+//  * S^T = K . Q^T: each lane loads 16 bytes of one key row straight from the paged cache into
+//    the A operand (no LDS); the 16x16 result leaves every lane with one head and four keys;
+//  * P^T is the B operand of O^T = V^T . P^T without leaving registers; V is staged per wave in
+//    LDS (row-major, chunk-swizzled) and read back transposed with ds_read_b64_tr_b16;
+//  * each wave streams its own 32-key chunks (no barriers in the loop); the four waves merge
+//    in LDS at the end and write one (max, sum, acc[HD]) partial per head and split;
+//  * the combine kernel merges the splits (natural-log LSE optional);
+//  * appending new_k/new_v (with rotary on k) is a kernel earlier in the same stream: the
+//    reference's hipDeviceSynchronize() after the append (fa_decode.hip:348-351) is gone.
+// Scores are handled in the log2 domain; partial maxima are stored in log2 units.
 #include "attn_device.hpp"
 #include "status.hpp"
 
-extern "C" int fa_decode_num_splits(int batch, int nq, int NH, int gqa, int64_t ctx_bound, int hint) {
-  (void)batch; (void)nq; (void)NH; (void)gqa; (void)ctx_bound;
-  return hint > 0 ? hint : 1;
+namespace fa {
+
+constexpr int kDecChunk = 32;  // keys per wave iteration
+constexpr int kDecWaves = 4;
+
+__device__ __forceinline__ float xor16_max(float x) {
+  return fmaxf(x, __shfl_xor(x, 16));
+}
+__device__ __forceinline__ float xor16_sum(float x) { return x + __shfl_xor(x, 16); }
+
+struct DecRange {
+  int qpos, hi, lo, start, end;
+};
+
+__device__ __forceinline__ DecRange dec_range(const DecParams& p, int b, int tk, int sp, int append) {
+  DecRange r;
+  const int ctx = p.ctx_len[b];
+  r.qpos = ctx + tk;
+  r.hi = min(ctx + (append ? tk + 1 : 0), p.max_blocks * p.page);
+  int lo = p.leftpad ? p.leftpad[b] : 0;
+  if (p.window >= 0) lo = max(lo, r.qpos - p.window + 1);
+  r.lo = max(lo, 0);
+  const int n = max(r.hi - r.lo, 0);
+  const int chunk = (((n + p.nsplit - 1) / p.nsplit) + kDecChunk - 1) / kDecChunk * kDecChunk;
+  r.start = r.lo + sp * chunk;
+  r.end = min(r.start + chunk, r.hi);
+  return r;
 }
 
-extern "C" int fa_decode_launch(DecParams p, int dtype, void* stream, const void* nk, const void* nv) {
-  (void)p; (void)dtype; (void)stream; (void)nk; (void)nv;
-  return fa::fail(FA_ERR_UNSUPPORTED, "fa_decode_launch: not implemented yet");
+template <typename T, int HD, bool FEAT>
+__global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_shift, int ngrp, int append) {
+  using V8 = typename Dt<T>::V8;
+  constexpr int NDS = HD / 32;  // S^T contraction steps
+  constexpr int NDB = HD / 16;  // 16-row blocks of O^T
+  constexpr int RCH = HD / 8;   // 16-byte chunks per key row
+  static_assert(RCH >= 8, "swizzle needs >= 8 chunks per row");
+  __shared__ float qsh[16][HD];
+  __shared__ __attribute__((aligned(16))) char vraw[kDecWaves * kDecChunk * HD * 2];
+  __shared__ float red_m[kDecWaves][16], red_l[kDecWaves][16];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lg = lane >> 4, lh = lane & 15;  // lane group (0..3), lane in group
+  const int b = blockIdx.x / p.nq, tk = blockIdx.x % p.nq;
+  const int kvh = blockIdx.y / ngrp, hgi = blockIdx.y % ngrp;
+  const int h0 = kvh * p.gqa + 16 * hgi, hg = min(16, p.gqa - 16 * hgi);
+  const int sp = blockIdx.z;
+  const int NKV = p.NH / p.gqa;
+  const DecRange rg = dec_range(p, b, tk, sp, append);
+
+  // ---- q rows of this head group -> LDS (fp32), rotary
+  const T* qg = (const T*)p.q + ((long long)(b * p.nq + tk) * p.NH + h0) * HD;
+  for (int i = tid; i < 16 * HD; i += 256) {
+    const int g = i / HD, d = i % HD;
+    qsh[g][d] = g < hg ? (float)qg[(long long)g * HD + d] : 0.0f;
+  }
+  __syncthreads();
+  if (p.rotary) {
+    const int rdim = p.rotary_dim > 0 ? p.rotary_dim : HD, half = rdim / 2;
+    const int rp = (p.rotary_pos ? p.rotary_pos[b] : p.ctx_len[b]) + tk;
+    for (int i = tid; i < hg * half; i += 256) {
+      const int g = i / half, j = i % half;
+      const float c = p.cos[(long long)rp * half + j], s = p.sin[(long long)rp * half + j];
+      const int ia = p.rotary == 1 ? j : 2 * j, ib = p.rotary == 1 ? j + half : 2 * j + 1;
+      const float x = qsh[g][ia], y = qsh[g][ib];
+      qsh[g][ia] = x * c - y * s;
+      qsh[g][ib] = y * c + x * s;
+    }
+    __syncthreads();
+  }
+  // Q^T as the B operand: lane holds head lh, head-dim 32*ds + 8*lg + e. A rotated q is not
+  // representable in T; it is carried as hi + lo (two MFMAs per step) so rotation costs no
+  // precision beyond fp32.
+  const bool qsplit = p.rotary != 0;
+  V8 qb[NDS], ql[NDS];
+#pragma unroll
+  for (int ds = 0; ds < NDS; ds++)
+#pragma unroll
+    for (int e = 0; e < 8; e++) {
+      const float x = qsh[lh][32 * ds + 8 * lg + e];
+      const T hi = (T)x;
+      qb[ds][e] = hi;
+      ql[ds][e] = (T)(x - (float)hi);
+    }
+
+  f32x4 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  const float c_log2 = p.scale * kLog2e;
+  const float slope = (FEAT && p.alibi && lh < hg) ? p.alibi[h0 + lh] : 0.0f;
+  const T* Kc = (const T*)p.Kc;
+  const T* Vc = (const T*)p.Vc;
+  const int* bt = p.block_table + (long long)b * p.max_blocks;
+  const int pmask = p.page - 1;
+  T* vb = (T*)vraw + wave * kDecChunk * HD;
+
+  auto row_base = [&](int key) -> long long {
+    const int blk = bt[key >> page_shift];
+    return (((long long)blk * p.page + (key & pmask)) * NKV + kvh) * HD;
+  };
+
+  for (int kc0 = rg.start + kDecChunk * wave; kc0 < rg.end; kc0 += kDecChunk * kDecWaves) {
+    // K rows for the A operand: key kc0 + 16*kb + lh, head-dim 32*ds + 8*lg
+    u32x4 kreg[2][NDS];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+      const int key = kc0 + 16 * kb + lh;
+      const bool ok = key < rg.end;
+      const long long base = ok ? row_base(key) : 0;
+#pragma unroll
+      for (int ds = 0; ds < NDS; ds++)
+        kreg[kb][ds] = ok ? *(const u32x4*)(Kc + base + 32 * ds + 8 * lg) : u32x4{0, 0, 0, 0};
+    }
+    // V rows: instruction i covers keys kc0 + 4i + lg, chunk lh of each row (HD=128: 8 loads)
+    constexpr int NVI = kDecChunk * RCH / 64;
+    u32x4 vreg[NVI];
+#pragma unroll
+    for (int i = 0; i < NVI; i++) {
+      const int row = (64 * i + lane) / RCH, ch = (64 * i + lane) % RCH;
+      const int key = kc0 + row;
+      vreg[i] = key < rg.end ? *(const u32x4*)(Vc + row_base(key) + 8 * ch) : u32x4{0, 0, 0, 0};
+    }
+    // S^T = K . Q^T
+    f32x4 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+      s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ds = 0; ds < NDS; ds++) s[kb] = Dt<T>::mma16(bitcast<V8>(kreg[kb][ds]), qb[ds], s[kb]);
+      if (qsplit) {
+#pragma unroll
+        for (int ds = 0; ds < NDS; ds++) s[kb] = Dt<T>::mma16(bitcast<V8>(kreg[kb][ds]), ql[ds], s[kb]);
+      }
+    }
+    // logits (log2 domain) and masking: s[kb][r] is key kc0 + 16*kb + 4*lg + r, head lh
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int key = kc0 + 16 * kb + 4 * lg + r;
+        float t;
+        if (FEAT) {
+          float x = s[kb][r] * p.scale;
+          if (p.softcap > 0.0f) x = p.softcap * tanh_exp(x / p.softcap);
+          x += slope * (float)(key - rg.qpos);
+          t = x * kLog2e;
+        } else {
+          t = s[kb][r] * c_log2;
+        }
+        t = key < rg.end ? t : -INFINITY;
+        s[kb][r] = t;
+        mx = fmaxf(mx, t);
+      }
+    mx = half_max(xor16_max(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float corr = exp2_fast(m_run - m_use);
+    float rs = 0.0f;
+    V8 pb;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float e = exp2_fast(s[kb][r] - m_use);
+        rs += e;
+        pb[4 * kb + r] = (T)e;
+      }
+    l_run = l_run * corr + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) oacc[db] *= corr;
+    // V -> this wave's LDS slice, chunk-swizzled: physical chunk = chunk ^ 2*(row % 4)
+#pragma unroll
+    for (int i = 0; i < NVI; i++) {
+      const int row = (64 * i + lane) / RCH, ch = (64 * i + lane) % RCH;
+      *(u32x4*)(vb + row * HD + 8 * (ch ^ (2 * (row & 3)))) = vreg[i];
+    }
+    // O^T += V^T . P^T, A operand by transposing LDS reads: lane lh of group lg addresses
+    // row 16*half + 4*lg + lh/4, head-dim 16*db + 4*(lh%4); it receives V[16*half+4*lg+r][16*db+lh]
+#pragma unroll
+    for (int db = 0; db < NDB; db++) {
+      typename Dt<T>::V4 part[2];
+#pragma unroll
+      for (int hf = 0; hf < 2; hf++) {
+        const int row = 16 * hf + 4 * lg + (lh >> 2);
+        const int col = 16 * db + 4 * (lh & 3);
+        const int off = row * HD + 8 * ((col >> 3) ^ (2 * (row & 3))) + (col & 7);
+        typedef short s4 __attribute__((ext_vector_type(4)));
+        s4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) s4*)((__attribute__((address_space(3))) T*)vb + off));
+        part[hf] = bitcast<typename Dt<T>::V4>(t);
+      }
+      V8 a;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        a[e] = part[0][e];
+        a[4 + e] = part[1][e];
+      }
+      oacc[db] = Dt<T>::mma16(a, pb, oacc[db]);
+    }
+  }
+
+  // ---- merge the four waves: per head max, sum and O^T accumulators through LDS
+  const float l_grp = half_sum(xor16_sum(l_run));
+  __syncthreads();  // every wave is done with its V slice: reuse it for the accumulators
+  float* red_o = (float*)vraw;  // [wave][16 heads][HD]
+  if (lg == 0) {
+    red_m[wave][lh] = m_run;
+    red_l[wave][lh] = l_grp;
+  }
+#pragma unroll
+  for (int db = 0; db < NDB; db++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) red_o[(wave * 16 + lh) * HD + 16 * db + 4 * lg + r] = oacc[db][r];
+  __syncthreads();
+  for (int i = tid; i < hg * HD; i += 256) {
+    const int g = i / HD, d = i % HD;
+    float gm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; w++) gm = fmaxf(gm, red_m[w][g]);
+    float l = 0.0f, acc = 0.0f;
+    if (gm != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kDecWaves; w++) {
+        const float f = exp2_fast(red_m[w][g] - gm);
+        l += f * red_l[w][g];
+        acc += f * red_o[(w * 16 + g) * HD + d];
+      }
+    }
+    float* out = p.scratch + (((long long)(b * p.nq + tk) * p.NH + h0 + g) * p.nsplit + sp) * (HD + 2);
+    if (d == 0) {
+      out[0] = gm;
+      out[1] = l;
+    }
+    out[2 + d] = acc;
+  }
+}
+
+// merge nsplit partials of one (token, head): grid (batch*nq, NH), block HD
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void dec_combine_kernel(DecParams p) {
+  const int row = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
+  const float* base = p.scratch + ((long long)row * p.NH + h) * p.nsplit * (HD + 2);
+  float gm = -INFINITY;
+  for (int s = 0; s < p.nsplit; s++) gm = fmaxf(gm, base[(long long)s * (HD + 2)]);
+  float l = 0.0f, acc = 0.0f;
+  if (gm != -INFINITY) {
+    for (int s = 0; s < p.nsplit; s++) {
+      const float* ps = base + (long long)s * (HD + 2);
+      const float w = exp2_fast(ps[0] - gm);
+      l += w * ps[1];
+      acc += w * ps[2 + d];
+    }
+  }
+  const bool ok = gm != -INFINITY && l > 0.0f;
+  ((T*)p.o)[((long long)row * p.NH + h) * HD + d] = (T)(ok ? acc / l : 0.0f);
+  if (p.lse_out && d == 0) p.lse_out[(long long)row * p.NH + h] = ok ? gm * kLn2 + __logf(l) : -INFINITY;
+}
+
+// write new_k (rotary applied) / new_v at positions ctx_len[b]+tk: grid (batch*nq, NKV), block HD
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void dec_append_kernel(DecParams p, const T* nk, const T* nv, int page_shift) {
+  __shared__ float ks[HD];
+  const int b = blockIdx.x / p.nq, tk = blockIdx.x % p.nq, kvh = blockIdx.y, d = threadIdx.x;
+  const int NKV = p.NH / p.gqa;
+  const int pos = p.ctx_len[b] + tk;
+  const bool ok = pos >= 0 && (pos >> page_shift) < p.max_blocks;
+  const long long src = ((long long)(b * p.nq + tk) * NKV + kvh) * HD;
+  ks[d] = (float)nk[src + d];
+  __syncthreads();
+  if (p.rotary) {
+    const int rdim = p.rotary_dim > 0 ? p.rotary_dim : HD, half = rdim / 2;
+    const int rp = (p.rotary_pos ? p.rotary_pos[b] : p.ctx_len[b]) + tk;
+    const bool act = d < half;
+    const int ia = p.rotary == 1 ? d : 2 * d, ib = p.rotary == 1 ? d + half : 2 * d + 1;
+    float x = 0.0f, y = 0.0f, c = 0.0f, s = 0.0f;
+    if (act) {
+      c = p.cos[(long long)rp * half + d];
+      s = p.sin[(long long)rp * half + d];
+      x = ks[ia];
+      y = ks[ib];
+    }
+    __syncthreads();
+    if (act) {
+      ks[ia] = x * c - y * s;
+      ks[ib] = y * c + x * s;
+    }
+    __syncthreads();
+  }
+  if (!ok) return;
+  const int blk = p.block_table[(long long)b * p.max_blocks + (pos >> page_shift)];
+  const long long dst = (((long long)blk * p.page + (pos & (p.page - 1))) * NKV + kvh) * HD + d;
+  ((T*)p.Kc)[dst] = (T)ks[d];
+  ((T*)p.Vc)[dst] = nv[src + d];
+}
+
+template <typename T, int HD>
+static int launch_dec(const DecParams& p, hipStream_t st, const void* nk, const void* nv) {
+  const int page_shift = __builtin_ctz((unsigned)p.page);
+  const int NKV = p.NH / p.gqa;
+  const int ngrp = (p.gqa + 15) / 16;
+  if (nk) {
+    hipLaunchKernelGGL((dec_append_kernel<T, HD>), dim3(p.batch * p.nq, NKV), dim3(HD), 0, st, p,
+                       (const T*)nk, (const T*)nv, page_shift);
+    if (int rc = launch_status("fa_decode_launch (append)")) return rc;
+  }
+  const bool feat = p.softcap > 0.0f || p.alibi != nullptr;
+  dim3 grid(p.batch * p.nq, NKV * ngrp, p.nsplit);
+  if (feat)
+    hipLaunchKernelGGL((dec_partial_kernel<T, HD, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+  else
+    hipLaunchKernelGGL((dec_partial_kernel<T, HD, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+  if (int rc = launch_status("fa_decode_launch (partial)")) return rc;
+  hipLaunchKernelGGL((dec_combine_kernel<T, HD>), dim3(p.batch * p.nq, p.NH), dim3(HD), 0, st, p);
+  return launch_status("fa_decode_launch (combine)");
+}
+
+template <typename T>
+static int dec_dispatch(const DecParams& p, hipStream_t st, const void* nk, const void* nv) {
+  switch (p.HD) {
+    case 64: return launch_dec<T, 64>(p, st, nk, nv);
+    case 128: return launch_dec<T, 128>(p, st, nk, nv);
+    case 256: return launch_dec<T, 256>(p, st, nk, nv);
+    default: return fail(FA_ERR_HEADDIM, "fa_decode_launch: head_dim=%d has no kernel (64, 128, 256)", p.HD);
+  }
+}
+
+}  // namespace fa
+
+// Split count: ~1536 workgroups (6 per CU on 256 CUs), at least 256 keys per split, [1, 512].
+// Reference heuristic (72 CUs, ~288 workgroups): package/csrc/dispatch.cpp:182-200.
+extern "C" int fa_decode_num_splits(int batch, int nq, int NH, int gqa, int64_t ctx_bound, int hint) {
+  int n;
+  if (hint > 0) {
+    n = hint;
+  } else {
+    const int g = gqa > 0 ? gqa : 1;
+    long long groups = (long long)batch * (nq > 0 ? nq : 1) * (NH / g > 0 ? NH / g : 1) * ((g + 15) / 16);
+    if (groups < 1) groups = 1;
+    n = (int)((1536 + groups - 1) / groups);
+    long long maxn = (ctx_bound + 255) / 256;
+    if (maxn < 1) maxn = 1;
+    if (n > maxn) n = (int)maxn;
+  }
+  return n < 1 ? 1 : (n > 512 ? 512 : n);
+}
+
+extern "C" int fa_decode_launch(DecParams p, int dtype, void* stream, const void* new_k, const void* new_v) {
+  using namespace fa;
+  if (!p.q || !p.Kc || !p.Vc || !p.block_table || !p.o || !p.scratch || !p.ctx_len)
+    return fail(FA_ERR_ARG, "fa_decode_launch: null pointer");
+  if (p.page <= 0 || (p.page & (p.page - 1))) return fail(FA_ERR_ARG, "fa_decode_launch: page=%d is not a power of two", p.page);
+  if (p.NH <= 0 || p.gqa <= 0 || p.NH % p.gqa) return fail(FA_ERR_ARG, "fa_decode_launch: NH=%d gqa=%d", p.NH, p.gqa);
+  if (p.nsplit < 1 || p.nsplit > 512) return fail(FA_ERR_ARG, "fa_decode_launch: nsplit=%d", p.nsplit);
+  if (p.nq < 1) p.nq = 1;
+  if ((new_k == nullptr) != (new_v == nullptr)) return fail(FA_ERR_ARG, "fa_decode_launch: new_k and new_v go together");
+  if (p.rotary && (!p.cos || !p.sin)) return fail(FA_ERR_ARG, "fa_decode_launch: rotary needs cos and sin");
+  if (p.rotary && (p.rotary_dim < 0 || p.rotary_dim > p.HD || p.rotary_dim % 2)) return fail(FA_ERR_ARG, "fa_decode_launch: rotary_dim=%d", p.rotary_dim);
+  if (p.batch <= 0) return FA_OK;
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case FA_F16: return dec_dispatch<_Float16>(p, st, new_k, new_v);
+    case FA_BF16: return dec_dispatch<__bf16>(p, st, new_k, new_v);
+    default: return fail(FA_ERR_DTYPE, "fa_decode_launch: dtype %d not implemented (fp16/bf16)", dtype);
+  }
 }

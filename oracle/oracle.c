@@ -190,7 +190,35 @@ typedef struct OracleDecCfg {
   int rdim;    /* rotary dim (0 => D) */
   int append;  /* new_k/new_v present */
   const float* alibi; /* [H] or NULL */
+  int round_append; /* 0: keep the rotated appended k exact; 1: round it to fp16; 2: to bf16 */
 } OracleDecCfg;
+
+/* Round a float to the nearest fp16 value (ties to even), overflow to inf, subnormals kept. */
+static float round_f16(float x) {
+  const float ax = fabsf(x);
+  if (x != x) return x;
+  if (!(ax < 65520.0f)) return copysignf(INFINITY, x);
+  float q;
+  if (ax < 6.103515625e-05f) {
+    q = 5.9604644775390625e-08f; /* 2^-24: fp16 subnormal quantum */
+  } else {
+    int e;
+    frexpf(ax, &e);
+    q = ldexpf(1.0f, e - 11); /* 10 stored mantissa bits */
+  }
+  return copysignf(nearbyintf(ax / q) * q, x);
+}
+
+/* Round a float to bf16 (ties to even), as fa_forward_gate.inc:4-5. */
+static float round_bf16(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7F800000u) == 0x7F800000u) return x;
+  u = (u + 0x7FFFu + ((u >> 16) & 1u)) & 0xFFFF0000u;
+  float r;
+  memcpy(&r, &u, 4);
+  return r;
+}
 
 /* rot_at — fa_decode_gate.inc:20-25, generalised to rotary_dim <= D */
 static void rot_at(double* v, int rdim, const float* cs, const float* sn, int mode, int pos) {
@@ -245,6 +273,12 @@ void oracle_decode(const float* q, const float* Kc, const float* Vc, const int32
             const float* nk = new_k + (((size_t)b * c->nq + (pos - ctx)) * c->Hk + kvh) * c->D;
             for (int d = 0; d < c->D; d++) kk[d] = nk[d];
             if (c->rotary) rot_at(kk, rdim, cos_t, sin_t, c->rotary, rp - tk + (pos - ctx));
+            /* the cache stores the rotated key in its dtype before attention reads it
+               (fa_decode.hip:298-300, fd_append) */
+            if (c->round_append == 1)
+              for (int d = 0; d < c->D; d++) kk[d] = round_f16((float)kk[d]);
+            else if (c->round_append == 2)
+              for (int d = 0; d < c->D; d++) kk[d] = round_bf16((float)kk[d]);
           } else {
             const int blk = block_table[(size_t)b * c->max_blocks + pos / c->page];
             const float* kp = Kc + (((size_t)blk * c->page + pos % c->page) * c->Hk + kvh) * c->D;
@@ -285,6 +319,11 @@ void oracle_decode(const float* q, const float* Kc, const float* Vc, const int32
         free(kk);
         free(pr);
       }
+}
+
+/* exported for tests: y[i] = round(x[i]) to fp16 (mode 1) or bf16 (mode 2) */
+void oracle_round(const float* x, float* y, size_t n, int mode) {
+  for (size_t i = 0; i < n; i++) y[i] = mode == 1 ? round_f16(x[i]) : mode == 2 ? round_bf16(x[i]) : x[i];
 }
 
 /* rel_rms — fa_common.hpp:136-139 (||got-ref||_2 / ||ref||_2) */

@@ -35,7 +35,7 @@ class OracleDecCfg(ctypes.Structure):
                 ("max_blocks", ctypes.c_int), ("scale", ctypes.c_double),
                 ("softcap", ctypes.c_double), ("window", ctypes.c_int),
                 ("rotary", ctypes.c_int), ("rdim", ctypes.c_int), ("append", ctypes.c_int),
-                ("alibi", ctypes.c_void_p)]
+                ("alibi", ctypes.c_void_p), ("round_append", ctypes.c_int)]
 
 
 def build():
@@ -168,9 +168,11 @@ def bwd(q, k, v, do, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0
 
 def decode(q, k_cache, v_cache, block_table, ctx_len, scale, new_k=None, new_v=None,
            rotary_cos=None, rotary_sin=None, rotary=0, rotary_dim=0, leftpad=None,
-           rotary_pos=None, window=-1, softcap=0.0, alibi=None):
+           rotary_pos=None, window=-1, softcap=0.0, alibi=None, append_dtype=None):
     """fp64 paged-decode oracle. q [B,nq,H,D]; caches [nblocks,page,Hk,D]; block_table
-    [B,max_blocks] int; ctx_len [B] (length before append). Returns (o [B,nq,H,D], lse [B,nq,H])."""
+    [B,max_blocks] int; ctx_len [B] (length before append). append_dtype ('f16'/'bf16') rounds
+    the rotated appended keys to the cache dtype, as storing them in the cache does.
+    Returns (o [B,nq,H,D], lse [B,nq,H])."""
     q = _f32(q)
     kc, vc = _f32(k_cache), _f32(v_cache)
     B, nq, H, D = q.shape
@@ -188,7 +190,8 @@ def decode(q, k_cache, v_cache, block_table, ctx_len, scale, new_k=None, new_v=N
     lse = np.zeros((B, nq, H), dtype=np.float32)
     cfg = OracleDecCfg(B, nq, H, Hk, D, page, bt.shape[1], _f32s(scale), _f32s(softcap),
                        int(window), int(rotary), int(rotary_dim), int(nk is not None),
-                       al.ctypes.data if al is not None else None)
+                       al.ctypes.data if al is not None else None,
+                       {None: 0, "f16": 1, "bf16": 2}[append_dtype])
     lib().oracle_decode(_p(q), _p(kc), _p(vc), _p(bt), _p(cl), _p(nk), _p(nv), _p(cs), _p(sn),
                         _p(lp), _p(rp), _p(o), _p(lse), ctypes.byref(cfg))
     return o, lse
