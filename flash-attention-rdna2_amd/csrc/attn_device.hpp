@@ -88,6 +88,25 @@ __device__ __forceinline__ float half_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// ds_read_b64_tr_b16 on LDS: within each group of 16 lanes, lane i receives element i%4 of
+// the 4-element (8-byte) runs addressed by lanes i/4, i/4+4, i/4+8, i/4+12. If lane j of a
+// group addresses row R0 + j/4, column C0 + 4*(j%4) of a row-major 16-bit matrix, lane i gets
+// column C0 + i of rows R0..R0+3: a transposed read.
+template <typename T>
+__device__ __forceinline__ typename Dt<T>::V4 lds_read_tr(const T* p) {
+  typedef short s4 __attribute__((ext_vector_type(4)));
+  s4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) s4*)((__attribute__((address_space(3))) T*)p));
+  return __builtin_bit_cast(typename Dt<T>::V4, t);
+}
+
+// Offset (in elements) of row r, 16-byte chunk c of a row-major LDS tile with HD columns;
+// chunks are XOR-swizzled by the row so that 8 consecutive rows read at one column hit
+// different banks.
+__device__ __forceinline__ int kofs(int r, int c, int HD, int KSW) {
+  return r * HD + 8 * (c ^ (r % KSW));
+}
+
 // blockIdx.x -> work index so that consecutive work items land on the same XCD (one L2).
 // Workgroups are dispatched round-robin over the 8 XCDs of an MI355X.
 __device__ __forceinline__ int xcd_remap(int L, int N) {

@@ -1,8 +1,527 @@
-// bwd.hip — backward entry point (kernels land in a following change).
+// bwd.hip — exact attention backward for gfx950, fp16/bf16, atomic-free and deterministic.
+//
+// Replaces the reference backward (kernels/backward.hip: fa_bwd_preprocess :86-96, fill_pd
+// :109-202, fa_bwd_dkdv :205-295, fa_bwd_dq :298-387, launcher :508-521); same BwdParams
+// contract and math (P recomputed from the forward LSE; dS = P*(dP - D)*softcap'), two kernels
+// in stream order, no atomics, fixed reduction order => bitwise reproducible:
+//
+//  1. dQ kernel: a wave owns 32 queries, Q and dO live in registers as MFMA B operands. It first
+//     computes D = rowsum(O*dO) for its rows (and writes it for kernel 2; no separate
+//     preprocess launch), then streams K/V tiles through LDS: S^T = K.Q^T and dP^T = V.dO^T on
+//     v_mfma_f32_32x32x16; dS^T stays in registers as the B operand of dQ^T = K^T.dS^T, with
+//     K^T read from the row-major K tile by ds_read_b64_tr_b16.
+//  2. dK/dV kernel: a wave owns 32 keys, K and V live in registers as B operands. It streams
+//     Q/dO tiles (and their LSE/D rows) of every q head sharing the kv head, in a fixed order:
+//     S = Q.K^T and dP = dO.V^T; P and dS stay in registers as B operands of
+//     dV^T += dO^T.P and dK^T += Q^T.dS (dO^T/Q^T by transposing LDS reads).
+// S and dP are computed in both kernels (the price of no atomics, as in the reference).
+// Probabilities are evaluated as exp2(s*scale*log2e - LSE*log2e).
 #include "attn_device.hpp"
 #include "status.hpp"
 
+namespace fa {
+
+template <bool CAUSAL, bool FEAT>
+__device__ __forceinline__ bool visible_b(const BwdParams& p, int q, int key, int delta, int SQ, int SK) {
+  if (key >= SK || q >= SQ) return false;
+  if (CAUSAL && key > q + delta) return false;
+  if (FEAT) {
+    if (p.win_left >= 0 && key < q + delta - p.win_left) return false;
+    if (p.win_right >= 0 && key > q + delta + p.win_right) return false;
+  }
+  return true;
+}
+
+// keys visible to query rows [r0, r1]: [k0, k1)
+template <bool CAUSAL, bool FEAT>
+__device__ __forceinline__ void key_range_b(const BwdParams& p, int r0, int r1, int delta, int SK, int& k0, int& k1) {
+  k0 = 0;
+  k1 = SK;
+  if (CAUSAL) k1 = min(k1, r1 + delta + 1);
+  if (FEAT) {
+    if (p.win_left >= 0) k0 = max(k0, r0 + delta - p.win_left);
+    if (p.win_right >= 0) k1 = min(k1, r1 + delta + p.win_right + 1);
+  }
+}
+
+// queries that see some key in [k0, k1]: [q0, q1)
+template <bool CAUSAL, bool FEAT>
+__device__ __forceinline__ void query_range_b(const BwdParams& p, int k0, int k1, int delta, int SQ, int& q0, int& q1) {
+  q0 = 0;
+  q1 = SQ;
+  if (CAUSAL) q0 = max(q0, k0 - delta);
+  if (FEAT) {
+    if (p.win_right >= 0) q0 = max(q0, k0 - delta - p.win_right);
+    if (p.win_left >= 0) q1 = min(q1, k1 - delta + p.win_left + 1);
+  }
+}
+
+// logit transform of one score: returns log2-domain logit, and d(logit)/d(scale*q.k)
+template <bool FEAT>
+__device__ __forceinline__ float bwd_logit2(const BwdParams& p, float s, float c_log2, float slope, int q,
+                                            int key, float& deriv) {
+  if (!FEAT) {
+    deriv = 1.0f;
+    return s * c_log2;
+  }
+  float x = s * p.scale;
+  deriv = 1.0f;
+  if (p.softcap > 0.0f) {
+    const float t = tanh_exp(x / p.softcap);
+    x = p.softcap * t;
+    deriv = 1.0f - t * t;
+  }
+  x += slope * (float)(key - q);
+  return x * kLog2e;
+}
+
+// ------------------------------------------------------------------------------------ dQ
+template <int HD_, int BC_, int NW_, int WPE_, int DSPLIT_ = 1>
+struct BwdQCfg {
+  static constexpr int HD = HD_, BC = BC_, NW = NW_, WPE = WPE_, DSPLIT = DSPLIT_;
+  static constexpr int NT = NW * 64;
+  static constexpr int BQ = NW * 32;
+  static constexpr int NB = BC / 32;
+  static constexpr int NG = BC / 16;
+  static constexpr int NDS = HD / 16;
+  static constexpr int NDB = HD / 32 / DSPLIT;  // 32-row blocks of dQ^T owned by one pass
+  static constexpr int DCH = HD / 8;
+  static constexpr int KSW = DCH < 16 ? DCH : 16;
+  static constexpr int KCH = BC * DCH;  // 16-byte chunks per K (or V) tile
+  static constexpr int HALF = NT / 2;
+  static constexpr int PER = KCH / HALF;
+  static constexpr int KT = BC * HD;
+  static constexpr int STAGE = 2 * KT;
+  static_assert(KCH % HALF == 0, "loader split");
+};
+
+template <typename T, class C, bool CAUSAL, bool FEAT>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
+                          amdgpu_waves_per_eu(C::WPE, C::WPE))) void
+bwd_dq_kernel(BwdParams p, int nqt) {
+  using V8 = typename Dt<T>::V8;
+  using V4 = typename Dt<T>::V4;
+  __shared__ __attribute__((aligned(16))) T lds[2 * C::STAGE];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
+
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int dpass = w % C::DSPLIT, w2 = w / C::DSPLIT;  // head-dim slice of dQ owned here
+  const int qti = w2 % nqt, zh = w2 / nqt;
+  const int h = zh % p.Hq, b = zh / p.Hq;
+  const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
+  const int kvh = h / p.gqa;
+  const int SQ = p.SQ, SK = p.SK, delta = SK - SQ;
+  const int qb = qt * C::BQ;
+  const int dbase = dpass * C::NDB * 32;
+  if (qb >= SQ) return;
+
+  const T* Qg = (const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h;
+  const T* dOg = (const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h;
+  const T* Og = (const T*)p.O + (long long)b * p.os.b + (long long)h * p.os.h;
+  const T* Kg = (const T*)p.K + (long long)b * p.ks.b + (long long)kvh * p.ks.h;
+  const T* Vg = (const T*)p.V + (long long)b * p.vs.b + (long long)kvh * p.vs.h;
+  T* dQg = (T*)p.dQ + (long long)b * p.dqs.b + (long long)h * p.dqs.h;
+  const long long row0 = ((long long)b * p.Hq + h) * SQ;
+
+  const int qw = qb + 32 * wave, qi = qw + l32;
+  const bool wave_rows = qw < SQ;
+  int bk0, bk1, wk0 = 0, wk1 = 0;
+  key_range_b<CAUSAL, FEAT>(p, qb, min(qb + C::BQ, SQ) - 1, delta, SK, bk0, bk1);
+  if (wave_rows) key_range_b<CAUSAL, FEAT>(p, qw, min(qw + 32, SQ) - 1, delta, SK, wk0, wk1);
+  const int kstart = (bk0 / C::BC) * C::BC;
+  const int ntiles = bk1 > bk0 ? (bk1 - kstart + C::BC - 1) / C::BC : 0;
+
+  // Q, dO rows as B operands; D = rowsum(O*dO)
+  V8 qreg[C::NDS], doreg[C::NDS];
+  float dpart = 0.0f;
+#pragma unroll
+  for (int ds = 0; ds < C::NDS; ds++) {
+    const int d0 = 16 * ds + 8 * hh;
+    if (qi < SQ) {
+      qreg[ds] = *(const V8*)(Qg + (long long)qi * p.qs.s + d0);
+      doreg[ds] = *(const V8*)(dOg + (long long)qi * p.dos.s + d0);
+      const V8 o = *(const V8*)(Og + (long long)qi * p.os.s + d0);
+#pragma unroll
+      for (int e = 0; e < 8; e++) dpart += (float)o[e] * (float)doreg[ds][e];
+    } else {
+      qreg[ds] = bitcast<V8>(u32x4{0, 0, 0, 0});
+      doreg[ds] = qreg[ds];
+    }
+  }
+  const float Di = half_sum(dpart);
+  float lse2 = INFINITY;  // rows past SQ and rows without visible keys contribute nothing
+  if (qi < SQ) {
+    const float l = p.lse[row0 + qi];
+    lse2 = l == -INFINITY ? INFINITY : l * kLog2e;
+    if (hh == 0 && dpass == 0) p.dsum[row0 + qi] = Di;
+  }
+  const float c_log2 = p.scale * kLog2e;
+  const float slope = (FEAT && p.alibi) ? p.alibi[h] : 0.0f;
+
+  f32x16 dqacc[C::NDB];
+#pragma unroll
+  for (int db = 0; db < C::NDB; db++) dqacc[db] = f32x16{};
+
+  const bool kloader = wave < C::NW / 2;
+  const int lt = kloader ? tid : tid - C::HALF;
+  const T* src = kloader ? Kg : Vg;
+  const long long sstride = kloader ? p.ks.s : p.vs.s;
+  u32x4 ld[C::PER];
+  auto gload = [&](int kb) {
+#pragma unroll
+    for (int j = 0; j < C::PER; j++) {
+      const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
+      const int key = kb + r;
+      ld[j] = key < SK ? *(const u32x4*)(src + (long long)key * sstride + 8 * c) : u32x4{0, 0, 0, 0};
+    }
+  };
+  auto lstore = [&](int stage) {
+    T* base = lds + stage * C::STAGE + (kloader ? 0 : C::KT);
+#pragma unroll
+    for (int j = 0; j < C::PER; j++) {
+      const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
+      *(u32x4*)(base + kofs(r, c, C::HD, C::KSW)) = ld[j];
+    }
+  };
+
+  if (ntiles > 0) {
+    gload(kstart);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < ntiles; t++) {
+    const int kb = kstart + t * C::BC;
+    const int stage = t & 1;
+    if (t + 1 < ntiles) gload(kb + C::BC);
+    const bool active = wave_rows && kb < wk1 && kb + C::BC > wk0;
+    if (active) {
+      const T* ks = lds + stage * C::STAGE;
+      const T* vs = ks + C::KT;
+      f32x16 s[C::NB], dp[C::NB];
+#pragma unroll
+      for (int jb = 0; jb < C::NB; jb++) {
+        s[jb] = f32x16{};
+        dp[jb] = f32x16{};
+      }
+#pragma unroll
+      for (int ds = 0; ds < C::NDS; ds++)
+#pragma unroll
+        for (int jb = 0; jb < C::NB; jb++) {
+          const int off = kofs(jb * 32 + l32, 2 * ds + hh, C::HD, C::KSW);
+          s[jb] = Dt<T>::mma32(*(const V8*)(ks + off), qreg[ds], s[jb]);
+          dp[jb] = Dt<T>::mma32(*(const V8*)(vs + off), doreg[ds], dp[jb]);
+        }
+      const bool edge = FEAT || (CAUSAL ? (kb + C::BC - 1 > qw + delta) : (kb + C::BC > SK));
+      const int kq = kb + 4 * hh;
+#pragma unroll
+      for (int jb = 0; jb < C::NB; jb++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+          const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
+          float deriv;
+          const float x = bwd_logit2<FEAT>(p, s[jb][r], c_log2, slope, qi, key, deriv);
+          float pr = exp2_fast(x - lse2);
+          if (edge && !visible_b<CAUSAL, FEAT>(p, qi, key, delta, SQ, SK)) pr = 0.0f;
+          s[jb][r] = pr * (dp[jb][r] - Di) * deriv;  // dS^T
+        }
+      V8 pb[C::NG];
+#pragma unroll
+      for (int jb = 0; jb < C::NB; jb++)
+#pragma unroll
+        for (int sh = 0; sh < 2; sh++)
+#pragma unroll
+          for (int e = 0; e < 8; e++) pb[2 * jb + sh][e] = (T)s[jb][8 * sh + e];
+      // dQ^T += K^T . dS^T: lane j16 of group (mh, hh) addresses key row 16g+8a+4hh+j16/4,
+      // head-dim 32db+16mh+4*(j16%4)
+#pragma unroll
+      for (int db = 0; db < C::NDB; db++) {
+        const int col = dbase + 32 * db + 16 * mh + 4 * (j16 & 3);
+#pragma unroll
+        for (int g = 0; g < C::NG; g++) {
+          V4 part[2];
+#pragma unroll
+          for (int a = 0; a < 2; a++) {
+            const int row = 16 * g + 8 * a + 4 * hh + (j16 >> 2);
+            part[a] = lds_read_tr<T>(ks + kofs(row, col >> 3, C::HD, C::KSW) + (col & 7));
+          }
+          V8 av;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            av[e] = part[0][e];
+            av[4 + e] = part[1][e];
+          }
+          dqacc[db] = Dt<T>::mma32(av, pb[g], dqacc[db]);
+        }
+      }
+    }
+    if (t + 1 < ntiles) lstore(stage ^ 1);
+    __syncthreads();
+  }
+  if (qi < SQ) {
+    T* row = dQg + (long long)qi * p.dqs.s;
+#pragma unroll
+    for (int db = 0; db < C::NDB; db++)
+#pragma unroll
+      for (int rq = 0; rq < 4; rq++) {
+        V4 v;
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = (T)(dqacc[db][4 * rq + c] * p.scale);
+        *(V4*)(row + dbase + 32 * db + 8 * rq + 4 * hh) = v;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------- dK, dV
+template <int HD_, int NW_, int WPE_, int DSPLIT_ = 1>
+struct BwdKVCfg {
+  static constexpr int HD = HD_, NW = NW_, WPE = WPE_, DSPLIT = DSPLIT_;
+  static constexpr int NT = NW * 64;
+  static constexpr int BQ = 32;         // queries per stage
+  static constexpr int BK = NW * 32;    // keys per workgroup
+  static constexpr int NDS = HD / 16;
+  static constexpr int NDB = HD / 32 / DSPLIT;  // 32-row blocks of dK^T/dV^T owned by one pass
+  static constexpr int DCH = HD / 8;
+  static constexpr int KSW = DCH < 16 ? DCH : 16;
+  static constexpr int TT = BQ * HD;    // halfs per Q (or dO) tile
+  static constexpr int STAGE = 2 * TT;
+  static constexpr int CH = 2 * BQ * DCH;  // chunks per stage (Q and dO)
+  static constexpr int PER = (CH + NT - 1) / NT;
+};
+
+template <typename T, class C, bool CAUSAL, bool FEAT>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
+                          amdgpu_waves_per_eu(C::WPE, C::WPE))) void
+bwd_dkdv_kernel(BwdParams p, int nkt) {
+  using V8 = typename Dt<T>::V8;
+  using V4 = typename Dt<T>::V4;
+  __shared__ __attribute__((aligned(16))) T lds[2 * C::STAGE];
+  __shared__ __attribute__((aligned(16))) float rowv[2][2][C::BQ];  // [stage][lse2 | D][q]
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
+
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int dpass = w % C::DSPLIT, w2 = w / C::DSPLIT;  // head-dim slice of dK/dV owned here
+  const int kt = w2 % nkt, zh = w2 / nkt;
+  const int kvh = zh % p.Hk, b = zh / p.Hk;
+  const int dbase = dpass * C::NDB * 32;
+  const int SQ = p.SQ, SK = p.SK, delta = SK - SQ;
+  const int kb0 = kt * C::BK;
+  if (kb0 >= SK) return;
+
+  const T* Kg = (const T*)p.K + (long long)b * p.ks.b + (long long)kvh * p.ks.h;
+  const T* Vg = (const T*)p.V + (long long)b * p.vs.b + (long long)kvh * p.vs.h;
+  const int kw = kb0 + 32 * wave, key = kw + l32;
+  const bool wave_keys = kw < SK;
+
+  V8 kreg[C::NDS], vreg[C::NDS];
+#pragma unroll
+  for (int ds = 0; ds < C::NDS; ds++) {
+    const int d0 = 16 * ds + 8 * hh;
+    if (key < SK) {
+      kreg[ds] = *(const V8*)(Kg + (long long)key * p.ks.s + d0);
+      vreg[ds] = *(const V8*)(Vg + (long long)key * p.vs.s + d0);
+    } else {
+      kreg[ds] = bitcast<V8>(u32x4{0, 0, 0, 0});
+      vreg[ds] = kreg[ds];
+    }
+  }
+  f32x16 dkacc[C::NDB], dvacc[C::NDB];
+#pragma unroll
+  for (int db = 0; db < C::NDB; db++) {
+    dkacc[db] = f32x16{};
+    dvacc[db] = f32x16{};
+  }
+  int bq0, bq1, wq0 = 0, wq1 = 0;
+  query_range_b<CAUSAL, FEAT>(p, kb0, min(kb0 + C::BK, SK) - 1, delta, SQ, bq0, bq1);
+  if (wave_keys) query_range_b<CAUSAL, FEAT>(p, kw, min(kw + 32, SK) - 1, delta, SQ, wq0, wq1);
+  const int qstart = (max(bq0, 0) / C::BQ) * C::BQ;
+  const int ntq = bq1 > bq0 ? (bq1 - qstart + C::BQ - 1) / C::BQ : 0;
+  const int total = ntq * p.gqa;
+  const float c_log2 = p.scale * kLog2e;
+
+  u32x4 ld[C::PER];
+  float lv = 0.0f;
+  auto gload = [&](int it) {
+    const int hg = it / ntq, qt0 = qstart + (it % ntq) * C::BQ;
+    const int h = kvh * p.gqa + hg;
+    const T* Qg = (const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h;
+    const T* dOg = (const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h;
+#pragma unroll
+    for (int j = 0; j < C::PER; j++) {
+      const int idx = tid + j * C::NT;
+      const int tsel = idx / (C::BQ * C::DCH), rem = idx % (C::BQ * C::DCH);
+      const int r = rem / C::DCH, c = rem % C::DCH, q = qt0 + r;
+      const bool ok = idx < C::CH && q < SQ;
+      const T* sp = tsel == 0 ? Qg + (long long)q * p.qs.s : dOg + (long long)q * p.dos.s;
+      ld[j] = ok ? *(const u32x4*)(sp + 8 * c) : u32x4{0, 0, 0, 0};
+    }
+    if (tid < 2 * C::BQ) {
+      const int q = qt0 + (tid % C::BQ);
+      const long long ri = ((long long)b * p.Hq + h) * SQ + q;
+      if (tid < C::BQ) {
+        const float l = q < SQ ? p.lse[ri] : INFINITY;
+        lv = (l == -INFINITY || q >= SQ) ? INFINITY : l * kLog2e;
+      } else {
+        lv = q < SQ ? p.dsum[ri] : 0.0f;
+      }
+    }
+  };
+  auto lstore = [&](int stage) {
+    T* base = lds + stage * C::STAGE;
+#pragma unroll
+    for (int j = 0; j < C::PER; j++) {
+      const int idx = tid + j * C::NT;
+      if (idx < C::CH) {
+        const int tsel = idx / (C::BQ * C::DCH), rem = idx % (C::BQ * C::DCH);
+        const int r = rem / C::DCH, c = rem % C::DCH;
+        *(u32x4*)(base + tsel * C::TT + kofs(r, c, C::HD, C::KSW)) = ld[j];
+      }
+    }
+    if (tid < 2 * C::BQ) rowv[stage][tid / C::BQ][tid % C::BQ] = lv;
+  };
+
+  if (total > 0) {
+    gload(0);
+    lstore(0);
+  }
+  __syncthreads();
+  for (int it = 0; it < total; it++) {
+    const int stage = it & 1;
+    const int hg = it / ntq, qt0 = qstart + (it % ntq) * C::BQ;
+    if (it + 1 < total) gload(it + 1);
+    const bool active = wave_keys && qt0 < wq1 && qt0 + C::BQ > wq0;
+    if (active) {
+      const int h = kvh * p.gqa + hg;
+      const float slope = (FEAT && p.alibi) ? p.alibi[h] : 0.0f;
+      const T* qs = lds + stage * C::STAGE;
+      const T* dos = qs + C::TT;
+      f32x16 s = f32x16{}, dp = f32x16{};
+#pragma unroll
+      for (int ds = 0; ds < C::NDS; ds++) {
+        const int off = kofs(l32, 2 * ds + hh, C::HD, C::KSW);
+        s = Dt<T>::mma32(*(const V8*)(qs + off), kreg[ds], s);
+        dp = Dt<T>::mma32(*(const V8*)(dos + off), vreg[ds], dp);
+      }
+      // s[r] is query qt0 + 8*(r/4) + 4*hh + (r%4), key `key`
+      const bool edge = FEAT || (CAUSAL ? (kw + 31 > qt0 + delta) : false) || qt0 + C::BQ > SQ || kw + 32 > SK;
+      V8 pP[2], pS[2];
+#pragma unroll
+      for (int rq = 0; rq < 4; rq++) {
+        const f32x4 l4 = *(const f32x4*)&rowv[stage][0][8 * rq + 4 * hh];
+        const f32x4 d4 = *(const f32x4*)&rowv[stage][1][8 * rq + 4 * hh];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          const int r = 4 * rq + c, q = qt0 + 8 * rq + 4 * hh + c;
+          float deriv;
+          const float x = bwd_logit2<FEAT>(p, s[r], c_log2, slope, q, key, deriv);
+          float pr = exp2_fast(x - l4[c]);
+          if (edge && !visible_b<CAUSAL, FEAT>(p, q, key, delta, SQ, SK)) pr = 0.0f;
+          const float dsv = pr * (dp[r] - d4[c]) * deriv;
+          pP[r >> 3][r & 7] = (T)pr;
+          pS[r >> 3][r & 7] = (T)dsv;
+        }
+      }
+      // dV^T += dO^T . P, dK^T += Q^T . dS (A operands by transposing reads of the tiles)
+#pragma unroll
+      for (int db = 0; db < C::NDB; db++) {
+        const int col = dbase + 32 * db + 16 * mh + 4 * (j16 & 3);
+#pragma unroll
+        for (int st = 0; st < 2; st++) {
+          V4 po[2], pq[2];
+#pragma unroll
+          for (int a = 0; a < 2; a++) {
+            const int row = 16 * st + 8 * a + 4 * hh + (j16 >> 2);
+            const int off = kofs(row, col >> 3, C::HD, C::KSW) + (col & 7);
+            po[a] = lds_read_tr<T>(dos + off);
+            pq[a] = lds_read_tr<T>(qs + off);
+          }
+          V8 ao, aq;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            ao[e] = po[0][e];
+            ao[4 + e] = po[1][e];
+            aq[e] = pq[0][e];
+            aq[4 + e] = pq[1][e];
+          }
+          dvacc[db] = Dt<T>::mma32(ao, pP[st], dvacc[db]);
+          dkacc[db] = Dt<T>::mma32(aq, pS[st], dkacc[db]);
+        }
+      }
+    }
+    if (it + 1 < total) lstore(stage ^ 1);
+    __syncthreads();
+  }
+  if (key < SK) {
+    T* krow = (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (long long)key * p.dks.s;
+    T* vrow = (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (long long)key * p.dvs.s;
+#pragma unroll
+    for (int db = 0; db < C::NDB; db++)
+#pragma unroll
+      for (int rq = 0; rq < 4; rq++) {
+        V4 vk, vv;
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+          vk[c] = (T)(dkacc[db][4 * rq + c] * p.scale);
+          vv[c] = (T)dvacc[db][4 * rq + c];
+        }
+        *(V4*)(krow + dbase + 32 * db + 8 * rq + 4 * hh) = vk;
+        *(V4*)(vrow + dbase + 32 * db + 8 * rq + 4 * hh) = vv;
+      }
+  }
+}
+
+template <typename T, class CQ, class CKV, bool CAUSAL, bool FEAT>
+static int launch_bwd2(const BwdParams& p, hipStream_t st) {
+  const int nqt = (p.SQ + CQ::BQ - 1) / CQ::BQ;
+  const int nkt = (p.SK + CKV::BK - 1) / CKV::BK;
+  const long long gq = (long long)nqt * p.Hq * p.B * CQ::DSPLIT;
+  const long long gkv = (long long)nkt * p.Hk * p.B * CKV::DSPLIT;
+  if (gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_backward_launch: grid too large");
+  if (gq > 0) {
+    hipLaunchKernelGGL((bwd_dq_kernel<T, CQ, CAUSAL, FEAT>), dim3((unsigned)gq), dim3(CQ::NT), 0, st, p, nqt);
+    if (int rc = launch_status("fable_attn_backward_launch (dq)")) return rc;
+  }
+  if (gkv > 0) {
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
+    if (int rc = launch_status("fable_attn_backward_launch (dkdv)")) return rc;
+  }
+  return FA_OK;
+}
+
+template <typename T, class CQ, class CKV>
+static int launch_bwd(const BwdParams& p, hipStream_t st) {
+  const bool feat = p.softcap > 0.0f || p.alibi != nullptr || p.win_left >= 0 ||
+                    (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
+  if (p.causal)
+    return feat ? launch_bwd2<T, CQ, CKV, true, true>(p, st) : launch_bwd2<T, CQ, CKV, true, false>(p, st);
+  return feat ? launch_bwd2<T, CQ, CKV, false, true>(p, st) : launch_bwd2<T, CQ, CKV, false, false>(p, st);
+}
+
+template <typename T>
+static int bwd_dispatch(const BwdParams& p, hipStream_t st) {
+  switch (p.D) {
+    case 64: return launch_bwd<T, BwdQCfg<64, 64, 4, 2>, BwdKVCfg<64, 4, 2>>(p, st);
+    case 128: return launch_bwd<T, BwdQCfg<128, 32, 4, 2>, BwdKVCfg<128, 4, 1>>(p, st);
+    case 256: return launch_bwd<T, BwdQCfg<256, 32, 4, 1, 2>, BwdKVCfg<256, 4, 1, 4>>(p, st);
+    default: return fail(FA_ERR_HEADDIM, "fable_attn_backward_launch: head_dim=%d has no kernel (64, 128, 256)", p.D);
+  }
+}
+
+}  // namespace fa
+
 extern "C" int fable_attn_backward_launch(BwdParams p, int dtype, void* stream) {
-  (void)p; (void)dtype; (void)stream;
-  return fa::fail(FA_ERR_UNSUPPORTED, "fable_attn_backward_launch: not implemented yet");
+  using namespace fa;
+  if (!p.Q || !p.K || !p.V || !p.O || !p.dO || !p.dQ || !p.dK || !p.dV || !p.lse || !p.dsum)
+    return fail(FA_ERR_ARG, "fable_attn_backward_launch: null pointer");
+  if (p.Hq <= 0 || p.Hk <= 0 || p.Hq % p.Hk || p.gqa != p.Hq / p.Hk)
+    return fail(FA_ERR_ARG, "fable_attn_backward_launch: Hq=%d Hk=%d gqa=%d", p.Hq, p.Hk, p.gqa);
+  if (p.dropout) return fail(FA_ERR_UNSUPPORTED, "fable_attn_backward_launch: dropout is not implemented");
+  if (p.B <= 0 || p.SQ < 0 || p.SK < 0) return FA_OK;  // empty ranges write zero gradients
+  hipStream_t st = (hipStream_t)stream;
+  switch (dtype) {
+    case FA_F16: return bwd_dispatch<_Float16>(p, st);
+    case FA_BF16: return bwd_dispatch<__bf16>(p, st);
+    default: return fail(FA_ERR_DTYPE, "fable_attn_backward_launch: dtype %d not implemented (fp16/bf16)", dtype);
+  }
 }

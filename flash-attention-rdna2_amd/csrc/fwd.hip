@@ -54,10 +54,6 @@ struct FwdCfg {
   static_assert(K_PER == 4 * V_PER, "balanced loaders");
 };
 
-__device__ __forceinline__ int kofs(int r, int c, int HD, int KSW) {
-  return r * HD + 8 * (c ^ (r % KSW));
-}
-
 template <class C>
 __device__ __forceinline__ int vofs(int d, int chunk) {
   const int sw = (d / C::VROWS128) % C::VCH;
