@@ -107,6 +107,17 @@ __device__ __forceinline__ int kofs(int r, int c, int HD, int KSW) {
   return r * HD + 8 * (c ^ (r % KSW));
 }
 
+// Raw buffer resource over [base, base + nbytes): 16-byte loads at offsets >= nbytes return
+// zeros, so tile loads need no per-lane condition. nbytes is clamped to the 32-bit range; the
+// third descriptor word selects 32-bit raw (untyped) access on gfx9-family parts.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, long long nbytes) {
+  const unsigned n = nbytes <= 0 ? 0u : (nbytes >= 0xFFFFFFFFll ? 0xFFFFFFFFu : (unsigned)nbytes);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
+}
+__device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
+}
+
 // blockIdx.x -> work index so that consecutive work items land on the same XCD (one L2).
 // Workgroups are dispatched round-robin over the 8 XCDs of an MI355X.
 __device__ __forceinline__ int xcd_remap(int L, int N) {

@@ -10,11 +10,12 @@
 //    one query and BC/2 of its keys: the row max needs a single cross-half exchange
 //    (v_permlane32_swap) and the probabilities P^T are already laid out as the B operand of
 //    O^T = V^T . P^T. P never touches LDS.
-//  * K and V tiles of BC keys are double-buffered in LDS with one barrier per tile. K is stored
-//    row-major with a 16-byte-chunk XOR swizzle; V is stored transposed (V^T, one row per head
-//    dim) with the keys of each 16-key group permuted so that the 8 keys a lane needs for one
-//    MFMA are one contiguous 16-byte read. The transpose happens in registers on the way in
-//    (each loader thread holds 4 keys x 8 dims and writes 8-byte runs).
+//  * K and V tiles of BC keys are double-buffered in LDS with one barrier per tile, both
+//    row-major with a 16-byte-chunk XOR swizzle. V^T, the A operand of the PV product, comes
+//    from transposing LDS reads (ds_read_b64_tr_b16), so nothing is transposed on the way in.
+//  * tile loads go through buffer descriptors (rows past the sequence end read as zeros), so
+//    they carry no per-lane condition and the prefetch of tile t+1 stays in flight during
+//    tile t.
 //  * online softmax in the log2 domain (one FMA + v_exp_f32 per score); rescaling of the O
 //    accumulator is skipped when no lane's running max moved.
 //  * tiles entirely outside the causal / window / chunk range are never loaded; masking code
@@ -36,29 +37,15 @@ struct FwdCfg {
   static constexpr int NG = BC / 16;        // 16-key groups per tile (PV contraction steps)
   static constexpr int NDS = HD / 16;       // Q.K contraction steps
   static constexpr int NDB = HD / 32;       // 32-row blocks of O^T
-  static constexpr int DCH = HD / 8;        // 16-byte chunks per K row
+  static constexpr int DCH = HD / 8;        // 16-byte chunks per K/V row
   static constexpr int KSW = DCH < 16 ? DCH : 16;
-  static constexpr int VCH = BC / 8;        // 16-byte chunks per V^T row
-  static constexpr int VROWS128 = 8 / VCH > 0 ? 8 / VCH : 1;  // V^T rows per 128 bytes
-  static constexpr int KCH = BC * HD / 8;   // chunks in a K tile
-  static constexpr int VUN = (BC / 4) * DCH;  // (4 keys x 8 dims) units in a V tile
-  static constexpr int HALF = NT / 2;       // threads loading K (the others load V)
-  static constexpr int K_PER = KCH / HALF;
-  static constexpr int V_PER = VUN / HALF;
-  static constexpr int NLD = K_PER > 4 * V_PER ? K_PER : 4 * V_PER;
-  static constexpr int KT = BC * HD;        // halfs per K tile (V^T tile is the same size)
+  static constexpr int KCH = BC * DCH;      // chunks per K (or V) tile
+  static constexpr int PER = 2 * KCH / NT;  // chunks each thread loads per tile (K and V)
+  static constexpr int KT = BC * HD;        // elements per K (or V) tile
   static constexpr int STAGE = 2 * KT;
-  static constexpr int LDS_BYTES = 2 * STAGE * 2;
   static_assert(HD % 32 == 0 && BC % 32 == 0, "shape");
-  static_assert(KCH % HALF == 0 && VUN % HALF == 0, "loader split");
-  static_assert(K_PER == 4 * V_PER, "balanced loaders");
+  static_assert((2 * KCH) % NT == 0 && KCH % NT == 0, "loader split");
 };
-
-template <class C>
-__device__ __forceinline__ int vofs(int d, int chunk) {
-  const int sw = (d / C::VROWS128) % C::VCH;
-  return d * C::BC + 8 * (chunk ^ sw);
-}
 
 struct SeqView {
   int SQ, SK;
@@ -93,7 +80,7 @@ fwd_kernel(FwdParams p, int nqt) {
   __shared__ __attribute__((aligned(16))) T lds[2 * C::STAGE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hh = lane >> 5;
+  const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
 
   // ---- work item -> (sequence z, head h, q tile)
   const int w = xcd_remap(blockIdx.x, gridDim.x);
@@ -161,62 +148,34 @@ fwd_kernel(FwdParams p, int nqt) {
   const float c_log2 = p.scale * kLog2e;
   const float aslope = (FEAT && p.alibi_slopes) ? p.alibi_slopes[h] : 0.0f;
 
-  // ---- global -> register loads of one tile (K by the first half of the threads, V by the rest)
-  const bool kloader = wave < C::NW / 2;
-  const int lt = kloader ? tid : tid - C::HALF;
-  u32x4 ld[C::NLD];
+  // ---- global -> register loads of one tile through buffer descriptors spanning rows
+  // kb..SK-1 of this head: rows past the sequence end read as zeros without a per-lane
+  // condition (a conditional load would make the compiler wait for it at once), and the
+  // per-lane byte offsets are loop invariant. The first KJ chunks of each thread are K.
+  constexpr int KJ = C::KCH / C::NT;
+  int voff[C::PER];
+#pragma unroll
+  for (int j = 0; j < C::PER; j++) {
+    const bool isv = j >= KJ;
+    const int ci = tid + (isv ? j - KJ : j) * C::NT;
+    const int r = ci / C::DCH, c = ci % C::DCH;
+    voff[j] = r * (int)((isv ? p.sV.s : p.sK.s) * 2) + 16 * c;
+  }
+  u32x4 ld[C::PER];
   auto gload = [&](int kb) {
-    if (kloader) {
+    const auto rk = buf_rsrc(Kg + (long long)kb * p.sK.s, (long long)(SK - kb) * p.sK.s * 2);
+    const auto rv = buf_rsrc(Vg + (long long)kb * p.sV.s, (long long)(SK - kb) * p.sV.s * 2);
 #pragma unroll
-      for (int j = 0; j < C::K_PER; j++) {
-        const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
-        const int key = kb + r;
-        ld[j] = key < SK ? *(const u32x4*)(Kg + (long long)key * p.sK.s + 8 * c) : u32x4{0, 0, 0, 0};
-      }
-    } else {
-#pragma unroll
-      for (int j = 0; j < C::V_PER; j++) {
-        const int idx = lt + j * C::HALF, q = idx / C::DCH, dc = idx % C::DCH;
-#pragma unroll
-        for (int u = 0; u < 4; u++) {
-          const int key = kb + 4 * q + u;
-          ld[4 * j + u] = key < SK ? *(const u32x4*)(Vg + (long long)key * p.sV.s + 8 * dc)
-                                   : u32x4{0, 0, 0, 0};
-        }
-      }
-    }
+    for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(j >= KJ ? rv : rk, voff[j]);
   };
   auto lstore = [&](int stage) {
     T* base = lds + stage * C::STAGE;
-    if (kloader) {
 #pragma unroll
-      for (int j = 0; j < C::K_PER; j++) {
-        const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
-        *(u32x4*)(base + kofs(r, c, C::HD, C::KSW)) = ld[j];
-      }
-    } else {
-      T* vt = base + C::KT;
-#pragma unroll
-      for (int j = 0; j < C::V_PER; j++) {
-        const int idx = lt + j * C::HALF, q = idx / C::DCH, dc = idx % C::DCH;
-        const int chunk = 2 * (q >> 2) + (q & 1), half4 = 4 * ((q >> 1) & 1);
-#pragma unroll
-        for (int dd = 0; dd < 8; dd++) {
-          const int wi = dd >> 1;
-          uint32_t a0 = ld[4 * j + 0][wi], a1 = ld[4 * j + 1][wi];
-          uint32_t a2 = ld[4 * j + 2][wi], a3 = ld[4 * j + 3][wi];
-          u32x2 pk;
-          if (dd & 1) {
-            pk[0] = (a0 >> 16) | (a1 & 0xFFFF0000u);
-            pk[1] = (a2 >> 16) | (a3 & 0xFFFF0000u);
-          } else {
-            pk[0] = (a0 & 0xFFFFu) | (a1 << 16);
-            pk[1] = (a2 & 0xFFFFu) | (a3 << 16);
-          }
-          const int d = 8 * dc + dd;
-          *(u32x2*)(vt + vofs<C>(d, chunk) + half4) = pk;
-        }
-      }
+    for (int j = 0; j < C::PER; j++) {
+      const bool isv = j >= KJ;
+      const int ci = tid + (isv ? j - KJ : j) * C::NT;
+      const int r = ci / C::DCH, c = ci % C::DCH;
+      *(u32x4*)(base + (isv ? C::KT : 0) + kofs(r, c, C::HD, C::KSW)) = ld[j];
     }
   };
 
@@ -229,7 +188,7 @@ fwd_kernel(FwdParams p, int nqt) {
   for (int t = 0; t < ntiles; t++) {
     const int kb = kstart + t * C::BC;
     const int stage = t & 1;
-    if (t + 1 < ntiles) gload(kb + C::BC);
+    gload(kb + C::BC);  // past the last tile the descriptor is empty and the loads return zeros
 
     const bool active = wave_rows && kb < wk1 && kb + C::BC > wk0;
     if (active) {
@@ -315,18 +274,31 @@ fwd_kernel(FwdParams p, int nqt) {
         for (int sh = 0; sh < 2; sh++)
 #pragma unroll
           for (int e = 0; e < 8; e++) pb[2 * jb + sh][e] = (T)s[jb][8 * sh + e];
-      // O^T += V^T . P^T
+      // O^T += V^T . P^T. A operand by transposing reads: lane j16 of 16-lane group (mh, hh)
+      // addresses key row 16g+8a+4hh+j16/4, head-dim 32db+16mh+4*(j16%4) and receives head-dim
+      // 32db+16mh+j16 of keys 16g+8a+4hh+0..3 (the keys of its P^T items 4a..4a+3).
 #pragma unroll
       for (int db = 0; db < C::NDB; db++) {
-        const int d = db * 32 + l32;
+        const int col = 32 * db + 16 * mh + 4 * (j16 & 3);
 #pragma unroll
         for (int g = 0; g < C::NG; g++) {
-          const V8 a = *(const V8*)(vt + vofs<C>(d, 2 * g + hh));
-          oacc[db] = Dt<T>::mma32(a, pb[g], oacc[db]);
+          V4 part[2];
+#pragma unroll
+          for (int a = 0; a < 2; a++) {
+            const int row = 16 * g + 8 * a + 4 * hh + (j16 >> 2);
+            part[a] = lds_read_tr<T>(vt + kofs(row, col >> 3, C::HD, C::KSW) + (col & 7));
+          }
+          V8 av;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            av[e] = part[0][e];
+            av[4 + e] = part[1][e];
+          }
+          oacc[db] = Dt<T>::mma32(av, pb[g], oacc[db]);
         }
       }
     }
-    if (t + 1 < ntiles) lstore(stage ^ 1);
+    lstore(stage ^ 1);
     __syncthreads();
   }
 
