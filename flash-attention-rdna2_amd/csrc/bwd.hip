@@ -102,7 +102,7 @@ bwd_dq_kernel(BwdParams p, int nqt) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
   __shared__ __attribute__((aligned(16))) T lds[2 * C::STAGE];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
 
   const int w = xcd_remap(blockIdx.x, gridDim.x);
@@ -163,18 +163,23 @@ bwd_dq_kernel(BwdParams p, int nqt) {
 #pragma unroll
   for (int db = 0; db < C::NDB; db++) dqacc[db] = f32x16{};
 
+  // K/V tiles through buffer descriptors over rows kb..SK-1 (rows past SK read as zeros):
+  // no per-lane condition, loop-invariant lane offsets, prefetch stays in flight.
   const bool kloader = wave < C::NW / 2;
   const int lt = kloader ? tid : tid - C::HALF;
-  const T* src = kloader ? Kg : Vg;
   const long long sstride = kloader ? p.ks.s : p.vs.s;
+  int voff[C::PER];
+#pragma unroll
+  for (int j = 0; j < C::PER; j++) {
+    const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
+    voff[j] = r * (int)(sstride * 2) + 16 * c;
+  }
   u32x4 ld[C::PER];
   auto gload = [&](int kb) {
+    const auto rs = kloader ? buf_rsrc(Kg + (long long)kb * p.ks.s, (long long)(SK - kb) * p.ks.s * 2)
+                            : buf_rsrc(Vg + (long long)kb * p.vs.s, (long long)(SK - kb) * p.vs.s * 2);
 #pragma unroll
-    for (int j = 0; j < C::PER; j++) {
-      const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
-      const int key = kb + r;
-      ld[j] = key < SK ? *(const u32x4*)(src + (long long)key * sstride + 8 * c) : u32x4{0, 0, 0, 0};
-    }
+    for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(rs, voff[j]);
   };
   auto lstore = [&](int stage) {
     T* base = lds + stage * C::STAGE + (kloader ? 0 : C::KT);
@@ -193,7 +198,7 @@ bwd_dq_kernel(BwdParams p, int nqt) {
   for (int t = 0; t < ntiles; t++) {
     const int kb = kstart + t * C::BC;
     const int stage = t & 1;
-    if (t + 1 < ntiles) gload(kb + C::BC);
+    gload(kb + C::BC);  // past the last tile the descriptor is empty: zeros, no condition
     const bool active = wave_rows && kb < wk1 && kb + C::BC > wk0;
     if (active) {
       const T* ks = lds + stage * C::STAGE;
@@ -255,7 +260,7 @@ bwd_dq_kernel(BwdParams p, int nqt) {
         }
       }
     }
-    if (t + 1 < ntiles) lstore(stage ^ 1);
+    lstore(stage ^ 1);
     __syncthreads();
   }
   if (qi < SQ) {
@@ -297,7 +302,7 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
   using V4 = typename Dt<T>::V4;
   __shared__ __attribute__((aligned(16))) T lds[2 * C::STAGE];
   __shared__ __attribute__((aligned(16))) float rowv[2][2][C::BQ];  // [stage][lse2 | D][q]
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
 
   const int w = xcd_remap(blockIdx.x, gridDim.x);
@@ -340,45 +345,49 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
   const int total = ntq * p.gqa;
   const float c_log2 = p.scale * kLog2e;
 
-  u32x4 ld[C::PER];
-  float lv = 0.0f;
-  auto gload = [&](int it) {
-    const int hg = it / ntq, qt0 = qstart + (it % ntq) * C::BQ;
-    const int h = kvh * p.gqa + hg;
-    const T* Qg = (const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h;
-    const T* dOg = (const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h;
+  // Q/dO tiles through buffer descriptors over rows qt0..SQ-1 (rows past SQ read as zeros);
+  // each thread's first QJ chunk slots are Q, the rest dO. The LSE/D row values are loaded
+  // unconditionally (clamped row) and turned into log2-domain LSE / D at store time.
+  static_assert((C::BQ * C::DCH) % C::NT == 0, "Q/dO slot split");
+  constexpr int QJ = C::BQ * C::DCH / C::NT;
+  int voff[C::PER];
 #pragma unroll
-    for (int j = 0; j < C::PER; j++) {
-      const int idx = tid + j * C::NT;
-      const int tsel = idx / (C::BQ * C::DCH), rem = idx % (C::BQ * C::DCH);
-      const int r = rem / C::DCH, c = rem % C::DCH, q = qt0 + r;
-      const bool ok = idx < C::CH && q < SQ;
-      const T* sp = tsel == 0 ? Qg + (long long)q * p.qs.s : dOg + (long long)q * p.dos.s;
-      ld[j] = ok ? *(const u32x4*)(sp + 8 * c) : u32x4{0, 0, 0, 0};
-    }
-    if (tid < 2 * C::BQ) {
-      const int q = qt0 + (tid % C::BQ);
-      const long long ri = ((long long)b * p.Hq + h) * SQ + q;
-      if (tid < C::BQ) {
-        const float l = q < SQ ? p.lse[ri] : INFINITY;
-        lv = (l == -INFINITY || q >= SQ) ? INFINITY : l * kLog2e;
-      } else {
-        lv = q < SQ ? p.dsum[ri] : 0.0f;
-      }
-    }
+  for (int j = 0; j < C::PER; j++) {
+    const int ci = tid + (j < QJ ? j : j - QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
+    voff[j] = r * (int)((j < QJ ? p.qs.s : p.dos.s) * 2) + 16 * c;
+  }
+  u32x4 ld[C::PER];
+  float lraw = 0.0f;
+  bool lok = false;
+  const int rsel = tid % (2 * C::BQ);  // row value slot: [0,BQ) LSE, [BQ,2BQ) D
+  auto gload = [&](int it) {
+    const int hg = min(it / ntq, p.gqa - 1), qt0 = qstart + (it % ntq) * C::BQ;
+    const int h = kvh * p.gqa + hg;
+    const long long rows = it < total ? (long long)(SQ - qt0) : 0;  // past the end: all zeros
+    const auto rq = buf_rsrc((const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h + (long long)qt0 * p.qs.s,
+                             rows * p.qs.s * 2);
+    const auto rd = buf_rsrc((const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + (long long)qt0 * p.dos.s,
+                             rows * p.dos.s * 2);
+#pragma unroll
+    for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(j < QJ ? rq : rd, voff[j]);
+    const int q = qt0 + (rsel % C::BQ);
+    lok = it < total && q < SQ;
+    const long long ri = ((long long)b * p.Hq + h) * SQ + min(q, SQ - 1);
+    lraw = rsel < C::BQ ? p.lse[ri] : p.dsum[ri];
   };
   auto lstore = [&](int stage) {
     T* base = lds + stage * C::STAGE;
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
-      const int idx = tid + j * C::NT;
-      if (idx < C::CH) {
-        const int tsel = idx / (C::BQ * C::DCH), rem = idx % (C::BQ * C::DCH);
-        const int r = rem / C::DCH, c = rem % C::DCH;
-        *(u32x4*)(base + tsel * C::TT + kofs(r, c, C::HD, C::KSW)) = ld[j];
-      }
+      const int ci = tid + (j < QJ ? j : j - QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
+      *(u32x4*)(base + (j < QJ ? 0 : C::TT) + kofs(r, c, C::HD, C::KSW)) = ld[j];
     }
-    if (tid < 2 * C::BQ) rowv[stage][tid / C::BQ][tid % C::BQ] = lv;
+    if (tid < 2 * C::BQ) {
+      // rows past SQ and rows without visible keys (LSE = -inf) get P = 0 through LSE = +inf
+      const float lv = rsel < C::BQ ? ((lok && lraw != -INFINITY) ? lraw * kLog2e : INFINITY)
+                                    : (lok ? lraw : 0.0f);
+      rowv[stage][rsel / C::BQ][rsel % C::BQ] = lv;
+    }
   };
 
   if (total > 0) {
@@ -389,7 +398,7 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
   for (int it = 0; it < total; it++) {
     const int stage = it & 1;
     const int hg = it / ntq, qt0 = qstart + (it % ntq) * C::BQ;
-    if (it + 1 < total) gload(it + 1);
+    gload(it + 1);  // past the last stage the descriptors are empty: zeros, no condition
     const bool active = wave_keys && qt0 < wq1 && qt0 + C::BQ > wq0;
     if (active) {
       const int h = kvh * p.gqa + hg;
@@ -449,7 +458,7 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
         }
       }
     }
-    if (it + 1 < total) lstore(stage ^ 1);
+    lstore(stage ^ 1);
     __syncthreads();
   }
   if (key < SK) {
