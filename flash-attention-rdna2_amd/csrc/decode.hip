@@ -69,11 +69,15 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
   const int NKV = p.NH / p.gqa;
   const DecRange rg = dec_range(p, b, tk, sp, append);
 
-  // ---- q rows of this head group -> LDS (fp32), rotary
+  // ---- q rows of this head group -> LDS (fp32): one 16-byte load per thread and chunk,
+  // head index clamped (rows past the group are zeroed after the load)
   const T* qg = (const T*)p.q + ((long long)(b * p.nq + tk) * p.NH + h0) * HD;
-  for (int i = tid; i < 16 * HD; i += 256) {
-    const int g = i / HD, d = i % HD;
-    qsh[g][d] = g < hg ? (float)qg[(long long)g * HD + d] : 0.0f;
+  for (int i = tid; i < 16 * RCH; i += 256) {
+    const int g = i / RCH, c = i % RCH;
+    const u32x4 raw = *(const u32x4*)(qg + (long long)min(g, hg - 1) * HD + 8 * c);
+    const V8 v = bitcast<V8>(raw);
+#pragma unroll
+    for (int e = 0; e < 8; e++) qsh[g][8 * c + e] = g < hg ? (float)v[e] : 0.0f;
   }
   __syncthreads();
   if (p.rotary) {
@@ -116,32 +120,43 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
   const int pmask = p.page - 1;
   T* vb = (T*)vraw + wave * kDecChunk * HD;
 
-  auto row_base = [&](int key) -> long long {
-    const int blk = bt[key >> page_shift];
+  // Keys of a chunk are clamped into [start, end-1] (masked in the softmax), so every load is
+  // unconditional. Block-table entries of the next chunk are fetched one iteration ahead so the
+  // K/V row loads of a chunk issue back to back instead of behind their table lookups.
+  constexpr int NVI = kDecChunk * RCH / 64;  // V row loads per lane per chunk
+  const int last = rg.end - 1;
+  auto kkey = [&](int kc0, int kb) { return min(kc0 + 16 * kb + lh, last); };
+  auto vkey = [&](int kc0, int i) { return min(kc0 + (64 * i + lane) / RCH, last); };
+  int kblk[2], vblk[NVI];
+  auto table = [&](int kc0) {
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) kblk[kb] = bt[kkey(kc0, kb) >> page_shift];
+#pragma unroll
+    for (int i = 0; i < NVI; i++) vblk[i] = bt[vkey(kc0, i) >> page_shift];
+  };
+  auto row_off = [&](int blk, int key) -> long long {
     return (((long long)blk * p.page + (key & pmask)) * NKV + kvh) * HD;
   };
+  const int kfirst = rg.start + kDecChunk * wave;
+  if (kfirst < rg.end) table(kfirst);
 
-  for (int kc0 = rg.start + kDecChunk * wave; kc0 < rg.end; kc0 += kDecChunk * kDecWaves) {
+  for (int kc0 = kfirst; kc0 < rg.end; kc0 += kDecChunk * kDecWaves) {
     // K rows for the A operand: key kc0 + 16*kb + lh, head-dim 32*ds + 8*lg
     u32x4 kreg[2][NDS];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
-      const int key = kc0 + 16 * kb + lh;
-      const bool ok = key < rg.end;
-      const long long base = ok ? row_base(key) : 0;
+      const long long base = row_off(kblk[kb], kkey(kc0, kb));
 #pragma unroll
-      for (int ds = 0; ds < NDS; ds++)
-        kreg[kb][ds] = ok ? *(const u32x4*)(Kc + base + 32 * ds + 8 * lg) : u32x4{0, 0, 0, 0};
+      for (int ds = 0; ds < NDS; ds++) kreg[kb][ds] = *(const u32x4*)(Kc + base + 32 * ds + 8 * lg);
     }
-    // V rows: instruction i covers keys kc0 + 4i + lg, chunk lh of each row (HD=128: 8 loads)
-    constexpr int NVI = kDecChunk * RCH / 64;
+    // V rows: load i covers row (64i + lane) / RCH of the chunk, 16-byte chunk (64i + lane) % RCH
     u32x4 vreg[NVI];
 #pragma unroll
     for (int i = 0; i < NVI; i++) {
-      const int row = (64 * i + lane) / RCH, ch = (64 * i + lane) % RCH;
-      const int key = kc0 + row;
-      vreg[i] = key < rg.end ? *(const u32x4*)(Vc + row_base(key) + 8 * ch) : u32x4{0, 0, 0, 0};
+      const int ch = (64 * i + lane) % RCH;
+      vreg[i] = *(const u32x4*)(Vc + row_off(vblk[i], vkey(kc0, i)) + 8 * ch);
     }
+    table(kc0 + kDecChunk * kDecWaves);  // past the end the keys clamp to the last one
     // S^T = K . Q^T
     f32x4 s[2];
 #pragma unroll
