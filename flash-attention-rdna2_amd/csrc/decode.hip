@@ -4,7 +4,7 @@
 // Replaces the reference decode (kernels/fa_decode.hip: fd_partial :57-252, fd_combine
 // :255-272, fd_append :275-302, launcher :319-362) with the same DecParams contract
 // (include/fable_attn_abi.h) and a different design:
-//  * one workgroup (4 waves) per (sequence*new token, kv head, 16-head group, split); the q
+//  * one workgroup (4 waves) per (kv head, 16-head group, sequence*new token, split); the q
 //    heads sharing the kv head are packed into the N=16 dimension of v_mfma_f32_16x16x32, so
 //    K and V are read from HBM once per kv head whatever the GQA ratio;
 //  * S^T = K . Q^T: each lane loads 16 bytes of one key row straight from the paged cache into
@@ -56,14 +56,19 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
   constexpr int NDB = HD / 16;  // 16-row blocks of O^T
   constexpr int RCH = HD / 8;   // 16-byte chunks per key row
   static_assert(RCH >= 8, "swizzle needs >= 8 chunks per row");
-  __shared__ float qsh[16][HD];
+  // one LDS region, reused: q staging (fp32) before the loop, per-wave V chunks in the loop,
+  // the four waves' accumulators after it
   __shared__ __attribute__((aligned(16))) char vraw[kDecWaves * kDecChunk * HD * 2];
   __shared__ float red_m[kDecWaves][16], red_l[kDecWaves][16];
+  static_assert(16 * HD * 4 <= sizeof(vraw), "q staging fits the V region");
+  float (*qsh)[HD] = (float (*)[HD])vraw;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lg = lane >> 4, lh = lane & 15;  // lane group (0..3), lane in group
-  const int b = blockIdx.x / p.nq, tk = blockIdx.x % p.nq;
-  const int kvh = blockIdx.y / ngrp, hgi = blockIdx.y % ngrp;
+  // grid x = (kv head, head group) fastest: the workgroups reading the interleaved heads of the
+  // same cache pages are dispatched together
+  const int b = blockIdx.y / p.nq, tk = blockIdx.y % p.nq;
+  const int kvh = blockIdx.x / ngrp, hgi = blockIdx.x % ngrp;
   const int h0 = kvh * p.gqa + 16 * hgi, hg = min(16, p.gqa - 16 * hgi);
   const int sp = blockIdx.z;
   const int NKV = p.NH / p.gqa;
@@ -107,6 +112,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
       qb[ds][e] = hi;
       ql[ds][e] = (T)(x - (float)hi);
     }
+  __syncthreads();  // q staging is dead from here on: the region becomes the V chunk buffers
 
   f32x4 oacc[NDB];
 #pragma unroll
@@ -343,7 +349,7 @@ static int launch_dec(const DecParams& p, hipStream_t st, const void* nk, const 
     if (int rc = launch_status("fa_decode_launch (append)")) return rc;
   }
   const bool feat = p.softcap > 0.0f || p.alibi != nullptr;
-  dim3 grid(p.batch * p.nq, NKV * ngrp, p.nsplit);
+  dim3 grid(NKV * ngrp, p.batch * p.nq, p.nsplit);
   if (feat)
     hipLaunchKernelGGL((dec_partial_kernel<T, HD, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
   else
