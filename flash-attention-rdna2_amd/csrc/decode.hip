@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
   T* vb = (T*)vraw + wave * kDecChunk * HD;
 
   // Keys of a chunk are clamped into [start, end-1] (masked in the softmax), so every load is
-  // unconditional. Block-table entries of the next chunk are fetched one iteration ahead so the
+  // unconditional. Block-table entries are fetched ahead of the row loads that use them, so the
   // K/V row loads of a chunk issue back to back instead of behind their table lookups.
   constexpr int NVI = kDecChunk * RCH / 64;  // V row loads per lane per chunk
   const int last = rg.end - 1;
@@ -143,26 +143,42 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
   auto row_off = [&](int blk, int key) -> long long {
     return (((long long)blk * p.page + (key & pmask)) * NKV + kvh) * HD;
   };
-  const int kfirst = rg.start + kDecChunk * wave;
-  if (kfirst < rg.end) table(kfirst);
-
-  for (int kc0 = kfirst; kc0 < rg.end; kc0 += kDecChunk * kDecWaves) {
-    // K rows for the A operand: key kc0 + 16*kb + lh, head-dim 32*ds + 8*lg
-    u32x4 kreg[2][NDS];
+  // K/V rows of the chunk at kc0: K as the A operand (key kc0 + 16*kb + lh, head-dim
+  // 32*ds + 8*lg); V load i covers row (64i + lane) / RCH, 16-byte chunk (64i + lane) % RCH
+  auto load = [&](int kc0, u32x4 (&kr)[2][NDS], u32x4 (&vr)[NVI]) {
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
       const long long base = row_off(kblk[kb], kkey(kc0, kb));
 #pragma unroll
-      for (int ds = 0; ds < NDS; ds++) kreg[kb][ds] = *(const u32x4*)(Kc + base + 32 * ds + 8 * lg);
+      for (int ds = 0; ds < NDS; ds++) kr[kb][ds] = *(const u32x4*)(Kc + base + 32 * ds + 8 * lg);
     }
-    // V rows: load i covers row (64i + lane) / RCH of the chunk, 16-byte chunk (64i + lane) % RCH
-    u32x4 vreg[NVI];
 #pragma unroll
     for (int i = 0; i < NVI; i++) {
       const int ch = (64 * i + lane) % RCH;
-      vreg[i] = *(const u32x4*)(Vc + row_off(vblk[i], vkey(kc0, i)) + 8 * ch);
+      vr[i] = *(const u32x4*)(Vc + row_off(vblk[i], vkey(kc0, i)) + 8 * ch);
     }
-    table(kc0 + kDecChunk * kDecWaves);  // past the end the keys clamp to the last one
+  };
+  // Software pipeline: the rows of the next chunk are in flight while this one is computed;
+  // table entries run two chunks ahead. Past the end keys clamp to the last one, so the
+  // trailing prefetch reads a valid row.
+  constexpr int kStep = kDecChunk * kDecWaves;
+  const int kfirst = rg.start + kDecChunk * wave;
+  u32x4 kreg[2][NDS], vreg[NVI];
+  if (kfirst < rg.end) {
+    table(kfirst);
+    load(kfirst, kreg, vreg);
+    table(kfirst + kStep);
+  }
+
+  // Double-buffered registers fit for HD <= 128; HD = 256 loads the next chunk after the
+  // compute of this one, leaving latency hiding to the other waves.
+  constexpr bool kPipe = HD <= 128;
+  for (int kc0 = kfirst; kc0 < rg.end; kc0 += kStep) {
+    u32x4 knxt[2][NDS], vnxt[NVI];
+    if constexpr (kPipe) {
+      load(kc0 + kStep, knxt, vnxt);
+      table(kc0 + 2 * kStep);
+    }
     // S^T = K . Q^T
     f32x4 s[2];
 #pragma unroll
@@ -241,6 +257,17 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
         a[4 + e] = part[1][e];
       }
       oacc[db] = Dt<T>::mma16(a, pb, oacc[db]);
+    }
+    if constexpr (kPipe) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int ds = 0; ds < NDS; ds++) kreg[kb][ds] = knxt[kb][ds];
+#pragma unroll
+      for (int i = 0; i < NVI; i++) vreg[i] = vnxt[i];
+    } else {
+      load(kc0 + kStep, kreg, vreg);
+      table(kc0 + 2 * kStep);
     }
   }
 
@@ -371,22 +398,35 @@ static int dec_dispatch(const DecParams& p, hipStream_t st, const void* nk, cons
 
 }  // namespace fa
 
-// Split count: ~1536 workgroups (6 per CU on 256 CUs), at least 256 keys per split, [1, 512].
-// Reference heuristic (72 CUs, ~288 workgroups): package/csrc/dispatch.cpp:182-200.
+// Split count from a model of the partial kernel as a stream of workgroup rounds: one
+// workgroup per CU is resident (256 CUs), the cache read saturates HBM once ~168 workgroups
+// stream together, and each split pays a fixed cost of about 64 keys (prologue, partial
+// write, combine). Time of a round of t workgroups ~ t * (keys per split + 64) / min(t, 168);
+// the smallest n within the minimum wins. At least 256 keys per split, n in [1, 512].
+// On the C4 shape (128 groups, 32768 keys) the model ranks n = 1, 2, 3, 4 as measured on
+// MI355X (474, 371, 414, 375 us). Reference heuristic (72 CUs): package/csrc/dispatch.cpp:182-200.
 extern "C" int fa_decode_num_splits(int batch, int nq, int NH, int gqa, int64_t ctx_bound, int hint) {
-  int n;
-  if (hint > 0) {
-    n = hint;
-  } else {
-    const int g = gqa > 0 ? gqa : 1;
-    long long groups = (long long)batch * (nq > 0 ? nq : 1) * (NH / g > 0 ? NH / g : 1) * ((g + 15) / 16);
-    if (groups < 1) groups = 1;
-    n = (int)((1536 + groups - 1) / groups);
-    long long maxn = (ctx_bound + 255) / 256;
-    if (maxn < 1) maxn = 1;
-    if (n > maxn) n = (int)maxn;
+  if (hint > 0) return hint > 512 ? 512 : hint;
+  constexpr long long kSlots = 256, kSat = 168, kSplitCost = 64;
+  const int g = gqa > 0 ? gqa : 1;
+  long long groups = (long long)batch * (nq > 0 ? nq : 1) * (NH / g > 0 ? NH / g : 1) * ((g + 15) / 16);
+  if (groups < 1) groups = 1;
+  const long long ctx = ctx_bound > 1 ? ctx_bound : 1;
+  long long maxn = (ctx + 255) / 256;
+  maxn = maxn < 1 ? 1 : (maxn > 512 ? 512 : maxn);
+  int best = 1;
+  double best_cost = 0.0;
+  for (long long n = 1; n <= maxn; n++) {
+    const double per = (double)((ctx + n - 1) / n + kSplitCost);
+    const long long wgs = groups * n, full = wgs / kSlots, tail = wgs % kSlots;
+    double cost = (double)full * kSlots * per / kSat;
+    if (tail) cost += (double)tail * per / (double)(tail < kSat ? tail : kSat);
+    if (n == 1 || cost < best_cost * 0.995) {
+      best = (int)n;
+      best_cost = cost;
+    }
   }
-  return n < 1 ? 1 : (n > 512 ? 512 : n);
+  return best;
 }
 
 extern "C" int fa_decode_launch(DecParams p, int dtype, void* stream, const void* new_k, const void* new_v) {
