@@ -19,6 +19,7 @@ import argparse
 import json
 import math
 import os
+import re
 import sys
 import time
 
@@ -109,7 +110,8 @@ def bench_decode(steps, warmup, batch=16, Hq=32, Hk=8, D=128, ctx=32768, page=25
     nbytes = 2.0 * batch * ctx * Hk * D * 2
     return {"batch": batch, "Hq": Hq, "Hk": Hk, "D": D, "ctx": ctx, "page": page, "bytes": nbytes,
             "ms": wall, "kernel_ms": ev, "GBs": nbytes / (wall * 1e-3) / 1e9,
-            "frac_hbm": nbytes / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS}
+            "frac_hbm": nbytes / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS,
+            "traffic_partial_kernel": profiled_traffic(DEC_C4_KERNEL)}
 
 
 def bench_varlen(steps, warmup, H=16, D=256, seed=0):
@@ -130,6 +132,97 @@ def bench_varlen(steps, warmup, H=16, D=256, seed=0):
     flops = 4.0 * D * H * pairs
     return {"lens": lens, "H": H, "D": D, "flops": flops, "ms": wall, "kernel_ms": ev,
             "tflops": flops / (wall * 1e-3) / 1e12}
+
+
+# ---- rocprofv3 summaries (CPU only: they read the CSV files rocprofv3 wrote) ----------------
+
+PROFILES = os.path.join(ROOT, "profiles")
+COPY_KERNEL = "__amd_rocclr_copyBuffer"
+COPY_CALIB_BYTES = 1 << 30   # --copy-calib copies 1 GiB device to device
+
+
+def _rocprof_rows(d, suffix):
+    import csv
+    import glob
+    rows = []
+    for f in sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True)):
+        with open(f, newline="") as fh:
+            rows += list(csv.DictReader(fh))
+    if not rows:
+        raise SystemExit(f"no *{suffix} under {d}")
+    return rows
+
+
+def summarize_pmc(fetch_dir, write_dir, kernel_re=None):
+    """Markdown table of FETCH_SIZE / WRITE_SIZE per dispatch (KiB, averaged per kernel) from
+    two `rocprofv3 --pmc` runs of `bench.py --copy-calib`, and HBM bytes per dispatch scaled by
+    what each counter reads for the 1 GiB calibration copy (its largest copyBuffer dispatch)."""
+    per = {}
+    factor = {}
+    for d, ctr in ((fetch_dir, "FETCH_SIZE"), (write_dir, "WRITE_SIZE")):
+        vals = {}
+        for r in _rocprof_rows(d, "counter_collection.csv"):
+            if r["Counter_Name"] == ctr:
+                vals.setdefault(r["Kernel_Name"], []).append(float(r["Counter_Value"]))
+        copy = max(vals.get(COPY_KERNEL, [0.0]))
+        if copy <= 0:
+            raise SystemExit(f"{d}: no {COPY_KERNEL} dispatch (run bench.py with --copy-calib)")
+        factor[ctr] = COPY_CALIB_BYTES / (copy * 1024.0)
+        for k, v in vals.items():
+            per.setdefault(k, {})[ctr] = (len(v), sum(v) / len(v))
+    out = ["| kernel | dispatches | FETCH_SIZE KiB/dispatch | WRITE_SIZE KiB/dispatch | "
+           "HBM bytes/dispatch (calibrated) |", "|---|---|---|---|---|"]
+    for k, c in sorted(per.items(), key=lambda kv: -kv[1].get("FETCH_SIZE", (0, 0.0))[1]):
+        if "FETCH_SIZE" not in c or "WRITE_SIZE" not in c or k == COPY_KERNEL:
+            continue
+        if kernel_re and not re.search(kernel_re, k):
+            continue
+        f, w = c["FETCH_SIZE"][1], c["WRITE_SIZE"][1]
+        hbm = f * 1024 * factor["FETCH_SIZE"] + w * 1024 * factor["WRITE_SIZE"]
+        out.append(f"| `{k[:100]}` | {c['FETCH_SIZE'][0]} | {f:.1f} | {w:.1f} | {hbm:.0f} |")
+    out.append("")
+    out.append(f"Calibration (1 GiB `{COPY_KERNEL}`): FETCH_SIZE x{factor['FETCH_SIZE']:.4f}, "
+               f"WRITE_SIZE x{factor['WRITE_SIZE']:.4f} (bytes per KiB-count / 1024).")
+    return "\n".join(out)
+
+
+def summarize_stats(d, kernel_re=None, skip=0):
+    """Markdown table of the `rocprofv3 --kernel-trace --stats` kernel statistics, with the
+    average over the dispatches after the first `skip` of each kernel (bench.py's warmup calls)
+    from the kernel trace, which is what bench.py's HIP-event average covers."""
+    trace = {}
+    for r in _rocprof_rows(d, "kernel_trace.csv"):
+        trace.setdefault(r["Kernel_Name"], []).append(
+            (int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
+    out = [f"| kernel | calls | average us | min us | max us | % of GPU time | average us after {skip} |",
+           "|---|---|---|---|---|---|---|"]
+    for r in _rocprof_rows(d, "kernel_stats.csv"):
+        if kernel_re and not re.search(kernel_re, r["Name"]):
+            continue
+        ds = [t for _, t in sorted(trace.get(r["Name"], []))][skip:]
+        after = f"{sum(ds) / len(ds) / 1e3:.1f}" if ds else "-"
+        out.append(f"| `{r['Name'][:100]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+                   f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
+                   f"{float(r['Percentage']):.2f} | {after} |")
+    return "\n".join(out)
+
+
+# kernel symbols of the measured workloads (one symbol per workload in the PMC runs, which
+# leave out the fwd extras that share the headline's symbol)
+FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128E\w*ELb1ELb0EEEv9FwdParamsi"
+DEC_C4_KERNEL = r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0EEEv9DecParamsiii"
+
+
+def profiled_traffic(kernel_re):
+    """HBM bytes per dispatch of the kernel whose symbol matches `kernel_re`, from the calibrated
+    PMC tables committed under profiles/ (None if no table names it)."""
+    import glob
+    for f in sorted(glob.glob(os.path.join(PROFILES, "*pmc*.md"))):
+        for line in open(f):
+            m = re.match(r"\| `([^`]+)` \| \d+ \| [\d.]+ \| [\d.]+ \| (\d+) \|", line)
+            if m and re.fullmatch(kernel_re, m.group(1)):
+                return int(m.group(2))
+    return None
 
 
 def cpu_baseline(S=16384, H=32, D=128, heads=2, seed=0):
@@ -162,7 +255,19 @@ def main():
     ap.add_argument("--extras", default="fwd,bwd,decode,varlen")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                    help="print the calibrated PMC table of two rocprofv3 --pmc runs and exit")
+    ap.add_argument("--summarize-stats", metavar="DIR",
+                    help="print the rocprofv3 --stats kernel table and exit")
+    ap.add_argument("--kernel-filter", default=None, help="regex on kernel symbols (summaries)")
+    ap.add_argument("--skip", type=int, default=0, help="leading dispatches to skip (summaries)")
     a = ap.parse_args()
+    if a.summarize_pmc:
+        print(summarize_pmc(*a.summarize_pmc, kernel_re=a.kernel_filter))
+        return
+    if a.summarize_stats:
+        print(summarize_stats(a.summarize_stats, a.kernel_filter, a.skip))
+        return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the reference has no multi-GPU "
               "path); run with --gpus 1", file=sys.stderr)
@@ -223,7 +328,7 @@ def main():
                    "causal": True, "flop_per_step": head["flops"]},
         "roofline": {"bound": "mfma", "achieved": round(ach, 2), "peak": PEAK_MFMA_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(ach / PEAK_MFMA_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": profiled_traffic(FWD_C2_KERNEL)},
         "cpu_baseline": cpu,
         "extra": extra,
     }
