@@ -24,6 +24,8 @@ typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
@@ -45,6 +47,11 @@ struct Dt<_Float16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
+  // c + a.x + a.y with the pair's exact products by one (v_dot2c_f32_f16, fp32 accumulate)
+  static __device__ __forceinline__ float sum2(f16x2 a, float c) {
+    return __builtin_amdgcn_fdot2(a, f16x2{(_Float16)1.0f, (_Float16)1.0f}, c, false);
+  }
+  using V2 = f16x2;
 };
 
 template <>
@@ -58,6 +65,10 @@ struct Dt<__bf16> {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
   }
   static __device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
+  static __device__ __forceinline__ float sum2(bf16x2 a, float c) {
+    return __builtin_amdgcn_fdot2_f32_bf16(a, bf16x2{(__bf16)1.0f, (__bf16)1.0f}, c, false);
+  }
+  using V2 = bf16x2;
 };
 
 template <typename V, typename U>

@@ -10,23 +10,34 @@
 //    one query and BC/2 of its keys: the row max needs a single cross-half exchange
 //    (v_permlane32_swap) and the probabilities P^T are already laid out as the B operand of
 //    O^T = V^T . P^T. P never touches LDS.
-//  * K and V tiles of BC keys are double-buffered in LDS with one barrier per tile, both
-//    row-major with a 16-byte-chunk XOR swizzle. V^T, the A operand of the PV product, comes
-//    from transposing LDS reads (ds_read_b64_tr_b16), so nothing is transposed on the way in.
-//  * tile loads go through buffer descriptors (rows past the sequence end read as zeros), so
-//    they carry no per-lane condition and the prefetch of tile t+1 stays in flight during
-//    tile t.
-//  * online softmax in the log2 domain (one FMA + v_exp_f32 per score); rescaling of the O
-//    accumulator is skipped when no lane's running max moved.
-//  * tiles entirely outside the causal / window / chunk range are never loaded; masking code
-//    runs only on tiles that straddle a boundary (template CAUSAL/FEAT split as in the
-//    reference's launch_cfg, fa_forward.hip:409-421).
+//  * software pipeline: iteration j computes S(j+1) = K(j+1) . Q^T, then the PV product of tile
+//    j and the softmax of tile j+1 in one branch-free block, so the VALU work of one tile runs
+//    under the matrix-core work of the other. K and V have their own double buffers in LDS
+//    (K is loaded two tiles ahead, V one) and there is one barrier per tile.
+//  * LDS rows are padded (K by 16 bytes, V by 64 bytes) so that the 16-byte K reads of 16 rows
+//    and the transposing V reads (ds_read_b64_tr_b16, 4 rows x 64 bytes per half-wave) hit
+//    distinct banks, and every read address is a per-lane base plus an immediate offset.
+//  * tile loads go through buffer descriptors (rows past the last needed key read as zeros),
+//    so they carry no per-lane condition and stay in flight across a whole iteration.
+//  * online softmax in the log2 domain (one FMA + v_exp_f32 per score). The running max only
+//    moves when a tile raises it by more than 2^8 (probabilities then stay <= 256, exact in
+//    fp16/bf16 range), so the O rescale is rare; it is skipped when no lane needs it. fp16 row
+//    sums add the rounded probabilities pairwise (v_dot2, fp32 accumulate), the values the PV
+//    product uses.
+//  * tiles entirely outside the causal / window / chunk range are never loaded; the leading
+//    tiles every row of the workgroup sees in full run without mask code (template CAUSAL/FEAT
+//    split as in the reference's launch_cfg, fa_forward.hip:409-421).
 //  * the workgroup -> (q tile, head, batch) map is XCD-aware (consecutive work items of one
 //    head share an XCD's L2) and, for causal, starts with the heaviest q tiles.
+#include <type_traits>
+
 #include "attn_device.hpp"
 #include "status.hpp"
 
 namespace fa {
+
+// the running max (log2 units) moves only when a tile exceeds it by more than this
+constexpr float kLazyMax = 8.0f;
 
 template <int HD_, int BC_, int NW_, int WPE_>
 struct FwdCfg {
@@ -38,13 +49,15 @@ struct FwdCfg {
   static constexpr int NDS = HD / 16;       // Q.K contraction steps
   static constexpr int NDB = HD / 32;       // 32-row blocks of O^T
   static constexpr int DCH = HD / 8;        // 16-byte chunks per K/V row
-  static constexpr int KSW = DCH < 16 ? DCH : 16;
+  static constexpr int KSTR = HD + 8;       // LDS row strides (elements)
+  static constexpr int VSTR = HD + 32;
+  static constexpr int KTILE = BC * KSTR;
+  static constexpr int VTILE = BC * VSTR;
   static constexpr int KCH = BC * DCH;      // chunks per K (or V) tile
-  static constexpr int PER = 2 * KCH / NT;  // chunks each thread loads per tile (K and V)
-  static constexpr int KT = BC * HD;        // elements per K (or V) tile
-  static constexpr int STAGE = 2 * KT;
+  static constexpr int KJ = KCH / NT;       // chunks each thread loads per K (or V) tile
+  static constexpr int RSTEP = NT / DCH;    // rows between a thread's chunks
   static_assert(HD % 32 == 0 && BC % 32 == 0, "shape");
-  static_assert((2 * KCH) % NT == 0 && KCH % NT == 0, "loader split");
+  static_assert(KCH % NT == 0 && NT % DCH == 0, "loader split");
 };
 
 struct SeqView {
@@ -77,7 +90,8 @@ __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
 fwd_kernel(FwdParams p, int nqt) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
-  __shared__ __attribute__((aligned(16))) T lds[2 * C::STAGE];
+  __shared__ __attribute__((aligned(16))) T kl[2 * C::KTILE];
+  __shared__ __attribute__((aligned(16))) T vl[2 * C::VTILE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
@@ -148,157 +162,231 @@ fwd_kernel(FwdParams p, int nqt) {
   const float c_log2 = p.scale * kLog2e;
   const float aslope = (FEAT && p.alibi_slopes) ? p.alibi_slopes[h] : 0.0f;
 
-  // ---- global -> register loads of one tile through buffer descriptors spanning rows
-  // kb..SK-1 of this head: rows past the sequence end read as zeros without a per-lane
-  // condition (a conditional load would make the compiler wait for it at once), and the
-  // per-lane byte offsets are loop invariant. The first KJ chunks of each thread are K.
-  constexpr int KJ = C::KCH / C::NT;
-  int voff[C::PER];
+  // leading tiles that every row of the workgroup sees in full: no mask code for them
+  int nint = 0;
+  if (!FEAT) {
+    int lim = SK;
+    if (CAUSAL) lim = min(lim, qb + delta + 1);
+    nint = min(max((lim - kstart) / C::BC, 0), ntiles);
+  }
+
+  // ---- global -> register loads of one tile through buffer descriptors spanning the rows
+  // kb .. kvalid-1 of this head: rows past the last needed key read as zeros without a
+  // per-lane condition (a conditional load would make the compiler wait for it at once), and
+  // the per-lane byte offsets are loop invariant.
+  const int kvalid = min(SK, kstart + ntiles * C::BC);
+  int koff[C::KJ], voff[C::KJ];
 #pragma unroll
-  for (int j = 0; j < C::PER; j++) {
-    const bool isv = j >= KJ;
-    const int ci = tid + (isv ? j - KJ : j) * C::NT;
+  for (int j = 0; j < C::KJ; j++) {
+    const int ci = tid + j * C::NT;
     const int r = ci / C::DCH, c = ci % C::DCH;
-    voff[j] = r * (int)((isv ? p.sV.s : p.sK.s) * 2) + 16 * c;
+    koff[j] = r * (int)(p.sK.s * 2) + 16 * c;
+    voff[j] = r * (int)(p.sV.s * 2) + 16 * c;
   }
-  u32x4 ld[C::PER];
-  auto gload = [&](int kb) {
-    const auto rk = buf_rsrc(Kg + (long long)kb * p.sK.s, (long long)(SK - kb) * p.sK.s * 2);
-    const auto rv = buf_rsrc(Vg + (long long)kb * p.sV.s, (long long)(SK - kb) * p.sV.s * 2);
+  const int lrow = tid / C::DCH, lch = tid % C::DCH;
+  const int lko = lrow * C::KSTR + 8 * lch, lvo = lrow * C::VSTR + 8 * lch;
+  u32x4 ldk[C::KJ], ldv[C::KJ];
+  auto gload_k = [&](int kb) {
+    const auto r = buf_rsrc(Kg + (long long)kb * p.sK.s, (long long)(kvalid - kb) * p.sK.s * 2);
 #pragma unroll
-    for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(j >= KJ ? rv : rk, voff[j]);
+    for (int j = 0; j < C::KJ; j++) ldk[j] = buf_load16(r, koff[j]);
   };
-  auto lstore = [&](int stage) {
-    T* base = lds + stage * C::STAGE;
+  auto gload_v = [&](int kb) {
+    const auto r = buf_rsrc(Vg + (long long)kb * p.sV.s, (long long)(kvalid - kb) * p.sV.s * 2);
 #pragma unroll
-    for (int j = 0; j < C::PER; j++) {
-      const bool isv = j >= KJ;
-      const int ci = tid + (isv ? j - KJ : j) * C::NT;
-      const int r = ci / C::DCH, c = ci % C::DCH;
-      *(u32x4*)(base + (isv ? C::KT : 0) + kofs(r, c, C::HD, C::KSW)) = ld[j];
-    }
+    for (int j = 0; j < C::KJ; j++) ldv[j] = buf_load16(r, voff[j]);
+  };
+  auto lstore_k = [&](int st) {
+    T* b = kl + st * C::KTILE + lko;
+#pragma unroll
+    for (int j = 0; j < C::KJ; j++) *(u32x4*)(b + j * C::RSTEP * C::KSTR) = ldk[j];
+  };
+  auto lstore_v = [&](int st) {
+    T* b = vl + st * C::VTILE + lvo;
+#pragma unroll
+    for (int j = 0; j < C::KJ; j++) *(u32x4*)(b + j * C::RSTEP * C::VSTR) = ldv[j];
   };
 
-  if (ntiles > 0) {
-    gload(kstart);
-    lstore(0);
-  }
-  __syncthreads();
-
-  for (int t = 0; t < ntiles; t++) {
-    const int kb = kstart + t * C::BC;
-    const int stage = t & 1;
-    gload(kb + C::BC);  // past the last tile the descriptor is empty and the loads return zeros
-
-    const bool active = wave_rows && kb < wk1 && kb + C::BC > wk0;
-    if (active) {
-      const T* ks = lds + stage * C::STAGE;
-      const T* vt = ks + C::KT;
-      // S^T = K . Q^T
-      f32x16 s[C::NB];
+  // S^T = K . Q^T for the K tile in stage st: lane reads key row 32*jb + l32, head-dim
+  // 16*ds + 8*hh .. +7 (the A operand of v_mfma_f32_32x32x16)
+  const int kro = l32 * C::KSTR + 8 * hh;
+  auto qk = [&](int st, f32x16 (&s)[C::NB]) {
+    const T* kp = kl + st * C::KTILE + kro;
 #pragma unroll
-      for (int jb = 0; jb < C::NB; jb++) s[jb] = f32x16{};
+    for (int jb = 0; jb < C::NB; jb++) s[jb] = f32x16{};
 #pragma unroll
-      for (int ds = 0; ds < C::NDS; ds++) {
-#pragma unroll
-        for (int jb = 0; jb < C::NB; jb++) {
-          const int r = jb * 32 + l32;
-          const V8 a = *(const V8*)(ks + kofs(r, 2 * ds + hh, C::HD, C::KSW));
-          s[jb] = Dt<T>::mma32(a, qreg[ds], s[jb]);
-        }
-      }
-      // logits (log2 domain for FEAT; raw dot products for the plain path) + masking
-      const int kq = kb + 4 * hh;  // key of s[jb][r] = kq + jb*32 + 8*(r/4) + (r%4)
-      if (FEAT) {
-#pragma unroll
-        for (int jb = 0; jb < C::NB; jb++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) {
-            const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
-            float x = s[jb][r] * p.scale;
-            if (p.softcap > 0.0f) x = p.softcap * tanh_exp(x / p.softcap);
-            x += aslope * (float)(key - qi);
-            bool ok = key < SK;
-            if (CAUSAL) ok = ok && key <= qi + delta;
-            if (p.win_left >= 0) ok = ok && key >= qi + delta - p.win_left;
-            if (p.win_right >= 0) ok = ok && key <= qi + delta + p.win_right;
-            if (p.attn_chunk > 0) {
-              const int cs = (max(qi + delta, 0) / p.attn_chunk) * p.attn_chunk;
-              ok = ok && key >= cs && key < cs + p.attn_chunk;
-            }
-            s[jb][r] = ok ? x * kLog2e : -INFINITY;
-          }
-      } else {
-        const bool edge = CAUSAL ? (kb + C::BC - 1 > qw + delta) : (kb + C::BC > SK);
-        if (edge) {
-#pragma unroll
-          for (int jb = 0; jb < C::NB; jb++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-              const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
-              const bool ok = CAUSAL ? key <= qi + delta : key < SK;
-              if (!ok) s[jb][r] = -INFINITY;
-            }
-        }
-      }
-      // online softmax
-      float mx = -INFINITY;
+    for (int ds = 0; ds < C::NDS; ds++)
 #pragma unroll
       for (int jb = 0; jb < C::NB; jb++)
+        s[jb] = Dt<T>::mma32(*(const V8*)(kp + jb * 32 * C::KSTR + 16 * ds), qreg[ds], s[jb]);
+  };
+  // O^T += V^T . P^T for the V tile in stage st. A operand by transposing reads: lane j16 of
+  // 16-lane group (mh, hh) addresses key row 16g+8a+4hh+j16/4, head-dim 32db+16mh+4*(j16%4)
+  // and receives head-dim 32db+16mh+j16 of keys 16g+8a+4hh+0..3 (the keys of its P^T items
+  // 4a..4a+3).
+  const int vro = (4 * hh + (j16 >> 2)) * C::VSTR + 16 * mh + 4 * (j16 & 3);
+  auto pv = [&](int st, const V8 (&pb)[C::NG]) {
+    const T* vp = vl + st * C::VTILE + vro;
 #pragma unroll
-        for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[jb][r]);
-      mx = half_max(mx);
-      const float m_new = fmaxf(m_run, FEAT ? mx : mx * c_log2);
-      const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-      const float corr = exp2_fast(m_run - m_use);
-      float rs = 0.0f;
+    for (int db = 0; db < C::NDB; db++)
+#pragma unroll
+      for (int g = 0; g < C::NG; g++) {
+        const V4 lo = lds_read_tr<T>(vp + 16 * g * C::VSTR + 32 * db);
+        const V4 hi = lds_read_tr<T>(vp + (16 * g + 8) * C::VSTR + 32 * db);
+        V8 av;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          av[e] = lo[e];
+          av[4 + e] = hi[e];
+        }
+        oacc[db] = Dt<T>::mma32(av, pb[g], oacc[db]);
+      }
+  };
+  // Softmax of one tile (keys kb..kb+BC-1) in s -> probabilities pb (the B operands of the PV
+  // product), running max/sum update. Returns the factor the O accumulators must be scaled by
+  // once every earlier tile's PV product is in them; `resc` is set when any lane's is not 1.
+  // Branch-free, so the compiler can interleave it with independent matrix-core work.
+  auto softmax = [&](auto masked, f32x16 (&s)[C::NB], int kb, V8 (&pb)[C::NG], bool& resc) {
+    const int kq = kb + 4 * hh;  // key of s[jb][r] = kq + 32*jb + 8*(r/4) + (r%4)
+    if constexpr (FEAT) {
 #pragma unroll
       for (int jb = 0; jb < C::NB; jb++)
 #pragma unroll
         for (int r = 0; r < 16; r++) {
-          const float e = FEAT ? exp2_fast(s[jb][r] - m_use) : exp2_fast(fmaf(s[jb][r], c_log2, -m_use));
-          s[jb][r] = e;
-          rs += e;
+          const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
+          float x = s[jb][r] * p.scale;
+          if (p.softcap > 0.0f) x = p.softcap * tanh_exp(x / p.softcap);
+          x += aslope * (float)(key - qi);
+          bool ok = key < SK;
+          if (CAUSAL) ok = ok && key <= qi + delta;
+          if (p.win_left >= 0) ok = ok && key >= qi + delta - p.win_left;
+          if (p.win_right >= 0) ok = ok && key <= qi + delta + p.win_right;
+          if (p.attn_chunk > 0) {
+            const int cs = (max(qi + delta, 0) / p.attn_chunk) * p.attn_chunk;
+            ok = ok && key >= cs && key < cs + p.attn_chunk;
+          }
+          s[jb][r] = ok ? x * kLog2e : -INFINITY;
         }
-      l_run = l_run * corr + rs;
-      m_run = m_new;
-      if (__builtin_amdgcn_ballot_w64(corr != 1.0f)) {
-#pragma unroll
-        for (int db = 0; db < C::NDB; db++) oacc[db] *= corr;
-      }
-      // P^T as B operands: group g = 2*jb + half covers accumulators 8*half .. 8*half+7
-      V8 pb[C::NG];
+    } else if constexpr (decltype(masked)::value) {
 #pragma unroll
       for (int jb = 0; jb < C::NB; jb++)
 #pragma unroll
-        for (int sh = 0; sh < 2; sh++)
-#pragma unroll
-          for (int e = 0; e < 8; e++) pb[2 * jb + sh][e] = (T)s[jb][8 * sh + e];
-      // O^T += V^T . P^T. A operand by transposing reads: lane j16 of 16-lane group (mh, hh)
-      // addresses key row 16g+8a+4hh+j16/4, head-dim 32db+16mh+4*(j16%4) and receives head-dim
-      // 32db+16mh+j16 of keys 16g+8a+4hh+0..3 (the keys of its P^T items 4a..4a+3).
-#pragma unroll
-      for (int db = 0; db < C::NDB; db++) {
-        const int col = 32 * db + 16 * mh + 4 * (j16 & 3);
-#pragma unroll
-        for (int g = 0; g < C::NG; g++) {
-          V4 part[2];
-#pragma unroll
-          for (int a = 0; a < 2; a++) {
-            const int row = 16 * g + 8 * a + 4 * hh + (j16 >> 2);
-            part[a] = lds_read_tr<T>(vt + kofs(row, col >> 3, C::HD, C::KSW) + (col & 7));
-          }
-          V8 av;
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            av[e] = part[0][e];
-            av[4 + e] = part[1][e];
-          }
-          oacc[db] = Dt<T>::mma32(av, pb[g], oacc[db]);
+        for (int r = 0; r < 16; r++) {
+          const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
+          const bool ok = CAUSAL ? (key < SK && key <= qi + delta) : key < SK;
+          if (!ok) s[jb][r] = -INFINITY;
         }
-      }
     }
-    lstore(stage ^ 1);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int jb = 0; jb < C::NB; jb++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[jb][r]);
+    mx = half_max(mx);
+    const float m_cand = fmaxf(m_run, FEAT ? mx : mx * c_log2);
+    const bool need = m_cand > m_run + kLazyMax;
+    const float corr = need ? exp2_fast(m_run - m_cand) : 1.0f;
+    m_run = need ? m_cand : m_run;
+    resc = __builtin_amdgcn_ballot_w64(need) != 0;
+    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    // fp16 sums the rounded probabilities pairwise (their rounding moves the row sum by at most
+    // 2^-12 relative); bf16 rounding is 8x coarser, so it sums the fp32 values
+    constexpr bool kPairSum = std::is_same<T, _Float16>::value;
+    float r0 = 0.0f, r1 = 0.0f;
+#pragma unroll
+    for (int jb = 0; jb < C::NB; jb++)
+#pragma unroll
+      for (int sh = 0; sh < 2; sh++)
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float x = s[jb][8 * sh + e];
+          const float pe = FEAT ? exp2_fast(x - m_use) : exp2_fast(fmaf(x, c_log2, -m_use));
+          pb[2 * jb + sh][e] = (T)pe;
+          if (!kPairSum) (e & 1 ? r1 : r0) += pe;
+        }
+    if (kPairSum) {
+#pragma unroll
+      for (int g = 0; g < C::NG; g++)
+#pragma unroll
+        for (int e = 0; e < 8; e += 4) {
+          r0 = Dt<T>::sum2(typename Dt<T>::V2{pb[g][e], pb[g][e + 1]}, r0);
+          r1 = Dt<T>::sum2(typename Dt<T>::V2{pb[g][e + 2], pb[g][e + 3]}, r1);
+        }
+    }
+    l_run = l_run * corr + (r0 + r1);
+    return corr;
+  };
+  auto rescale = [&](float corr) {
+#pragma unroll
+    for (int db = 0; db < C::NDB; db++) oacc[db] *= corr;
+  };
+  auto active = [&](int t) {
+    const int kb = kstart + t * C::BC;
+    return wave_rows && kb < wk1 && kb + C::BC > wk0;
+  };
+  using Plain = std::integral_constant<bool, false>;
+  using Masked = std::integral_constant<bool, true>;
+
+  // ---- prologue: K tiles 0 and 1, V tile 0 in LDS; S and P of tile 0
+  V8 pb[C::NG];
+  if (ntiles > 0) {
+    gload_k(kstart);
+    gload_v(kstart);
+    lstore_k(0);
+    lstore_v(0);
+    gload_k(kstart + C::BC);
+    lstore_k(1);
+  }
+  __syncthreads();
+  bool a_cur = false;
+  // a pending O rescale (from the softmax of the tile whose PV product comes next) is applied
+  // at the top of the next iteration, so the softmax shares a basic block with the PV product
+  bool resc = false;
+  float corr = 1.0f;
+  if (ntiles > 0) {
+    f32x16 s[C::NB];
+    if (nint > 0) {
+      a_cur = true;
+      qk(0, s);
+      corr = softmax(Plain{}, s, kstart, pb, resc);
+    } else if ((a_cur = active(0))) {
+      qk(0, s);
+      corr = softmax(Masked{}, s, kstart, pb, resc);
+    }
+  }
+  __syncthreads();  // every wave has read K stage 0 before iteration 0 refills it
+
+  // ---- iteration t: S of tile t+1, PV of tile t, softmax of tile t+1; then K tile t+2 and
+  // V tile t+1 go to the stages tiles t and t-1 used.
+  int t = 0;
+  for (; t + 1 < nint; t++) {
+    if (resc) rescale(corr);
+    const int kb1 = kstart + (t + 1) * C::BC;
+    gload_k(kb1 + C::BC);
+    gload_v(kb1);
+    f32x16 s[C::NB];
+    qk((t + 1) & 1, s);
+    pv(t & 1, pb);
+    corr = softmax(Plain{}, s, kb1, pb, resc);
+    lstore_k(t & 1);
+    lstore_v((t + 1) & 1);
+    __syncthreads();
+  }
+  if (t < ntiles && t > 0) a_cur = active(t);
+  for (; t < ntiles; t++) {
+    if (resc) rescale(corr);
+    resc = false;
+    const int kb1 = kstart + (t + 1) * C::BC;
+    gload_k(kb1 + C::BC);
+    gload_v(kb1);
+    const bool a_next = t + 1 < ntiles && active(t + 1);
+    f32x16 s[C::NB];
+    if (a_next) qk((t + 1) & 1, s);
+    if (a_cur) pv(t & 1, pb);
+    if (a_next) corr = softmax(Masked{}, s, kb1, pb, resc);
+    a_cur = a_next;
+    lstore_k(t & 1);
+    lstore_v((t + 1) & 1);
     __syncthreads();
   }
 
@@ -348,7 +436,7 @@ template <typename T>
 static int dispatch_hd(const FwdParams& p, hipStream_t st) {
   switch (p.HD) {
     case 64: return launch_fwd<T, FwdCfg<64, 64, 4, 2>>(p, st);
-    case 128: return launch_fwd<T, FwdCfg<128, 64, 8, 2>>(p, st);
+    case 128: return launch_fwd<T, FwdCfg<128, 64, 4, 2>>(p, st);
     case 256: return launch_fwd<T, FwdCfg<256, 32, 4, 1>>(p, st);
     default: return fail(FA_ERR_HEADDIM, "fa_forward_launch: head_dim=%d has no kernel (64, 128, 256)", p.HD);
   }
