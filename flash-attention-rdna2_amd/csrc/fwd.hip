@@ -39,11 +39,12 @@ namespace fa {
 // the running max (log2 units) moves only when a tile exceeds it by more than this
 constexpr float kLazyMax = 8.0f;
 
-template <int HD_, int BC_, int NW_, int WPE_>
+template <int HD_, int BC_, int NW_, int WPE_, int QB_ = 1>
 struct FwdCfg {
   static constexpr int HD = HD_, BC = BC_, NW = NW_, WPE = WPE_;
+  static constexpr int QB = QB_;            // 32-query blocks per wave
   static constexpr int NT = NW * 64;
-  static constexpr int BR = NW * 32;
+  static constexpr int BR = NW * 32 * QB;
   static constexpr int NB = BC / 32;        // 32-key blocks per tile
   static constexpr int NG = BC / 16;        // 16-key groups per tile (PV contraction steps)
   static constexpr int NDS = HD / 16;       // Q.K contraction steps
@@ -135,30 +136,39 @@ fwd_kernel(FwdParams p, int nqt) {
   T* Og = (T*)p.O + sv.o0 + (long long)h * p.sO.h;
 
   // ---- block and wave key ranges
+  constexpr int QB = C::QB;
   int bk0, bk1;
   key_range<CAUSAL, FEAT>(p, qb, min(qb + C::BR, SQ) - 1, delta, SK, bk0, bk1);
-  const int qw = qb + wave * 32;
+  const int qw = qb + wave * 32 * QB;  // first row of this wave; block i = rows qw+32i..+31
   const bool wave_rows = qw < SQ;
   int wk0 = 0, wk1 = 0;
-  if (wave_rows) key_range<CAUSAL, FEAT>(p, qw, min(qw + 32, SQ) - 1, delta, SK, wk0, wk1);
+  if (wave_rows) key_range<CAUSAL, FEAT>(p, qw, min(qw + 32 * QB, SQ) - 1, delta, SK, wk0, wk1);
   const int kstart = (bk0 / C::BC) * C::BC;
   const int ntiles = bk1 > bk0 ? (bk1 - kstart + C::BC - 1) / C::BC : 0;
 
-  // ---- Q (B operand) in registers
-  const int qi = qw + l32;
-  V8 qreg[C::NDS];
+  // ---- Q (B operands) in registers: lane holds query qw + 32i + l32, head-dim 16ds + 8hh..+7
+  V8 qreg[QB][C::NDS];
 #pragma unroll
-  for (int ds = 0; ds < C::NDS; ds++) {
-    if (qi < SQ)
-      qreg[ds] = *(const V8*)(Qg + (long long)qi * p.sQ.s + 16 * ds + 8 * hh);
-    else
-      qreg[ds] = bitcast<V8>(u32x4{0, 0, 0, 0});
+  for (int i = 0; i < QB; i++) {
+    const int qi = qw + 32 * i + l32;
+#pragma unroll
+    for (int ds = 0; ds < C::NDS; ds++) {
+      if (qi < SQ)
+        qreg[i][ds] = *(const V8*)(Qg + (long long)qi * p.sQ.s + 16 * ds + 8 * hh);
+      else
+        qreg[i][ds] = bitcast<V8>(u32x4{0, 0, 0, 0});
+    }
   }
 
-  f32x16 oacc[C::NDB];
+  f32x16 oacc[QB][C::NDB];
+  float m_run[QB], l_run[QB];
 #pragma unroll
-  for (int db = 0; db < C::NDB; db++) oacc[db] = f32x16{};
-  float m_run = -INFINITY, l_run = 0.0f;
+  for (int i = 0; i < QB; i++) {
+#pragma unroll
+    for (int db = 0; db < C::NDB; db++) oacc[i][db] = f32x16{};
+    m_run[i] = -INFINITY;
+    l_run[i] = 0.0f;
+  }
   const float c_log2 = p.scale * kLog2e;
   const float aslope = (FEAT && p.alibi_slopes) ? p.alibi_slopes[h] : 0.0f;
 
@@ -207,25 +217,31 @@ fwd_kernel(FwdParams p, int nqt) {
     for (int j = 0; j < C::KJ; j++) *(u32x4*)(b + j * C::RSTEP * C::VSTR) = ldv[j];
   };
 
-  // S^T = K . Q^T for the K tile in stage st: lane reads key row 32*jb + l32, head-dim
-  // 16*ds + 8*hh .. +7 (the A operand of v_mfma_f32_32x32x16)
+  // S^T = K . Q^T for the K tile in stage st, every query block: lane reads key row
+  // 32*jb + l32, head-dim 16*ds + 8*hh .. +7 (the A operand of v_mfma_f32_32x32x16), shared by
+  // the blocks
   const int kro = l32 * C::KSTR + 8 * hh;
-  auto qk = [&](int st, f32x16 (&s)[C::NB]) {
+  auto qk = [&](int st, f32x16 (&s)[QB][C::NB]) {
     const T* kp = kl + st * C::KTILE + kro;
 #pragma unroll
-    for (int jb = 0; jb < C::NB; jb++) s[jb] = f32x16{};
+    for (int i = 0; i < QB; i++)
+#pragma unroll
+      for (int jb = 0; jb < C::NB; jb++) s[i][jb] = f32x16{};
 #pragma unroll
     for (int ds = 0; ds < C::NDS; ds++)
 #pragma unroll
-      for (int jb = 0; jb < C::NB; jb++)
-        s[jb] = Dt<T>::mma32(*(const V8*)(kp + jb * 32 * C::KSTR + 16 * ds), qreg[ds], s[jb]);
+      for (int jb = 0; jb < C::NB; jb++) {
+        const V8 a = *(const V8*)(kp + jb * 32 * C::KSTR + 16 * ds);
+#pragma unroll
+        for (int i = 0; i < QB; i++) s[i][jb] = Dt<T>::mma32(a, qreg[i][ds], s[i][jb]);
+      }
   };
   // O^T += V^T . P^T for the V tile in stage st. A operand by transposing reads: lane j16 of
   // 16-lane group (mh, hh) addresses key row 16g+8a+4hh+j16/4, head-dim 32db+16mh+4*(j16%4)
   // and receives head-dim 32db+16mh+j16 of keys 16g+8a+4hh+0..3 (the keys of its P^T items
   // 4a..4a+3).
   const int vro = (4 * hh + (j16 >> 2)) * C::VSTR + 16 * mh + 4 * (j16 & 3);
-  auto pv = [&](int st, const V8 (&pb)[C::NG]) {
+  auto pv = [&](int st, const V8 (&pb)[QB][C::NG]) {
     const T* vp = vl + st * C::VTILE + vro;
 #pragma unroll
     for (int db = 0; db < C::NDB; db++)
@@ -239,14 +255,17 @@ fwd_kernel(FwdParams p, int nqt) {
           av[e] = lo[e];
           av[4 + e] = hi[e];
         }
-        oacc[db] = Dt<T>::mma32(av, pb[g], oacc[db]);
+#pragma unroll
+        for (int i = 0; i < QB; i++) oacc[i][db] = Dt<T>::mma32(av, pb[i][g], oacc[i][db]);
       }
   };
-  // Softmax of one tile (keys kb..kb+BC-1) in s -> probabilities pb (the B operands of the PV
-  // product), running max/sum update. Returns the factor the O accumulators must be scaled by
-  // once every earlier tile's PV product is in them; `resc` is set when any lane's is not 1.
-  // Branch-free, so the compiler can interleave it with independent matrix-core work.
-  auto softmax = [&](auto masked, f32x16 (&s)[C::NB], int kb, V8 (&pb)[C::NG], bool& resc) {
+  // Softmax of one tile (keys kb..kb+BC-1) of query block i in s -> probabilities pb (the B
+  // operands of the PV product), running max/sum update. Returns the factor the block's O
+  // accumulators must be scaled by once every earlier tile's PV product is in them; `resc` is
+  // set when any lane's is not 1. Branch-free, so the compiler can interleave it with
+  // independent matrix-core work.
+  auto softmax = [&](auto masked, int i, f32x16 (&s)[C::NB], int kb, V8 (&pb)[C::NG], bool& resc) {
+    const int qi = qw + 32 * i + l32;
     const int kq = kb + 4 * hh;  // key of s[jb][r] = kq + 32*jb + 8*(r/4) + (r%4)
     if constexpr (FEAT) {
 #pragma unroll
@@ -283,12 +302,12 @@ fwd_kernel(FwdParams p, int nqt) {
 #pragma unroll
       for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[jb][r]);
     mx = half_max(mx);
-    const float m_cand = fmaxf(m_run, FEAT ? mx : mx * c_log2);
-    const bool need = m_cand > m_run + kLazyMax;
-    const float corr = need ? exp2_fast(m_run - m_cand) : 1.0f;
-    m_run = need ? m_cand : m_run;
+    const float m_cand = fmaxf(m_run[i], FEAT ? mx : mx * c_log2);
+    const bool need = m_cand > m_run[i] + kLazyMax;
+    const float corr = need ? exp2_fast(m_run[i] - m_cand) : 1.0f;
+    m_run[i] = need ? m_cand : m_run[i];
     resc = __builtin_amdgcn_ballot_w64(need) != 0;
-    const float m_use = m_run == -INFINITY ? 0.0f : m_run;
+    const float m_use = m_run[i] == -INFINITY ? 0.0f : m_run[i];
     // fp16 sums the rounded probabilities pairwise (their rounding moves the row sum by at most
     // 2^-12 relative); bf16 rounding is 8x coarser, so it sums the fp32 values
     constexpr bool kPairSum = std::is_same<T, _Float16>::value;
@@ -313,12 +332,8 @@ fwd_kernel(FwdParams p, int nqt) {
           r1 = Dt<T>::sum2(typename Dt<T>::V2{pb[g][e + 2], pb[g][e + 3]}, r1);
         }
     }
-    l_run = l_run * corr + (r0 + r1);
+    l_run[i] = l_run[i] * corr + (r0 + r1);
     return corr;
-  };
-  auto rescale = [&](float corr) {
-#pragma unroll
-    for (int db = 0; db < C::NDB; db++) oacc[db] *= corr;
   };
   auto active = [&](int t) {
     const int kb = kstart + t * C::BC;
@@ -328,7 +343,7 @@ fwd_kernel(FwdParams p, int nqt) {
   using Masked = std::integral_constant<bool, true>;
 
   // ---- prologue: K tiles 0 and 1, V tile 0 in LDS; S and P of tile 0
-  V8 pb[C::NG];
+  V8 pb[QB][C::NG];
   if (ntiles > 0) {
     gload_k(kstart);
     gload_v(kstart);
@@ -341,17 +356,33 @@ fwd_kernel(FwdParams p, int nqt) {
   bool a_cur = false;
   // a pending O rescale (from the softmax of the tile whose PV product comes next) is applied
   // at the top of the next iteration, so the softmax shares a basic block with the PV product
-  bool resc = false;
-  float corr = 1.0f;
+  bool resc[QB];
+  float corr[QB];
+#pragma unroll
+  for (int i = 0; i < QB; i++) {
+    resc[i] = false;
+    corr[i] = 1.0f;
+  }
+  auto rescale = [&]() {
+#pragma unroll
+    for (int i = 0; i < QB; i++)
+      if (resc[i]) {
+#pragma unroll
+        for (int db = 0; db < C::NDB; db++) oacc[i][db] *= corr[i];
+        resc[i] = false;
+      }
+  };
   if (ntiles > 0) {
-    f32x16 s[C::NB];
+    f32x16 s[QB][C::NB];
     if (nint > 0) {
       a_cur = true;
       qk(0, s);
-      corr = softmax(Plain{}, s, kstart, pb, resc);
+#pragma unroll
+      for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, i, s[i], kstart, pb[i], resc[i]);
     } else if ((a_cur = active(0))) {
       qk(0, s);
-      corr = softmax(Masked{}, s, kstart, pb, resc);
+#pragma unroll
+      for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, i, s[i], kstart, pb[i], resc[i]);
     }
   }
   __syncthreads();  // every wave has read K stage 0 before iteration 0 refills it
@@ -360,30 +391,33 @@ fwd_kernel(FwdParams p, int nqt) {
   // V tile t+1 go to the stages tiles t and t-1 used.
   int t = 0;
   for (; t + 1 < nint; t++) {
-    if (resc) rescale(corr);
+    rescale();
     const int kb1 = kstart + (t + 1) * C::BC;
     gload_k(kb1 + C::BC);
     gload_v(kb1);
-    f32x16 s[C::NB];
+    f32x16 s[QB][C::NB];
     qk((t + 1) & 1, s);
     pv(t & 1, pb);
-    corr = softmax(Plain{}, s, kb1, pb, resc);
+#pragma unroll
+    for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, i, s[i], kb1, pb[i], resc[i]);
     lstore_k(t & 1);
     lstore_v((t + 1) & 1);
     __syncthreads();
   }
   if (t < ntiles && t > 0) a_cur = active(t);
   for (; t < ntiles; t++) {
-    if (resc) rescale(corr);
-    resc = false;
+    rescale();
     const int kb1 = kstart + (t + 1) * C::BC;
     gload_k(kb1 + C::BC);
     gload_v(kb1);
     const bool a_next = t + 1 < ntiles && active(t + 1);
-    f32x16 s[C::NB];
+    f32x16 s[QB][C::NB];
     if (a_next) qk((t + 1) & 1, s);
     if (a_cur) pv(t & 1, pb);
-    if (a_next) corr = softmax(Masked{}, s, kb1, pb, resc);
+    if (a_next) {
+#pragma unroll
+      for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, i, s[i], kb1, pb[i], resc[i]);
+    }
     a_cur = a_next;
     lstore_k(t & 1);
     lstore_v((t + 1) & 1);
@@ -391,21 +425,25 @@ fwd_kernel(FwdParams p, int nqt) {
   }
 
   // ---- epilogue: O = acc / l, LSE
-  const float l_tot = half_sum(l_run);
-  const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-  if (qi < SQ) {
-    T* orow = Og + (long long)qi * p.sO.s;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++)
+  for (int i = 0; i < QB; i++) {
+    const int qi = qw + 32 * i + l32;
+    const float l_tot = half_sum(l_run[i]);
+    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (qi < SQ) {
+      T* orow = Og + (long long)qi * p.sO.s;
 #pragma unroll
-      for (int rq = 0; rq < 4; rq++) {
-        V4 v;
+      for (int db = 0; db < C::NDB; db++)
 #pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = (T)(oacc[db][4 * rq + c] * inv);
-        *(V4*)(orow + db * 32 + 8 * rq + 4 * hh) = v;
-      }
-    if (p.LSE && hh == 0)
-      p.LSE[sv.lse0 + qi] = l_tot > 0.0f ? m_run * kLn2 + __logf(l_tot) : -INFINITY;
+        for (int rq = 0; rq < 4; rq++) {
+          V4 v;
+#pragma unroll
+          for (int c = 0; c < 4; c++) v[c] = (T)(oacc[i][db][4 * rq + c] * inv);
+          *(V4*)(orow + db * 32 + 8 * rq + 4 * hh) = v;
+        }
+      if (p.LSE && hh == 0)
+        p.LSE[sv.lse0 + qi] = l_tot > 0.0f ? m_run[i] * kLn2 + __logf(l_tot) : -INFINITY;
+    }
   }
 }
 
