@@ -5,7 +5,9 @@
 Every .hip file under csrc/ is compiled separately (in parallel) with hipcc for gfx950 only and
 linked into fable_attn/libfable_attn_hip.so. Objects go to _build/ (git-ignored).
 Flags: -O3, C++17, packed-fp32 VALU ops disabled (a hard rule for this hardware pool), no
-fast-math (masking relies on IEEE infinities).
+fast-math (masking relies on IEEE infinities). The backward kernels keep MFMA accumulators in
+architectural VGPRs (-amdgpu-mfma-vgpr-form): the compiler's default there parks the dK/dV
+accumulators in AGPRs and copies them back and forth around every MFMA group.
 """
 import argparse
 import concurrent.futures as cf
@@ -25,9 +27,13 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
          "-I" + os.path.join(HERE, "..", "include")]
 
 
+# per-source extra flags
+EXTRA = {"bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def _compile(src):
     obj = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC] + FLAGS + ["-c", src, "-o", obj]
+    cmd = [HIPCC] + FLAGS + EXTRA.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")
