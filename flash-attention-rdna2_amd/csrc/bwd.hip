@@ -76,6 +76,20 @@ __device__ __forceinline__ float bwd_logit2(const BwdParams& p, float s, float c
 }
 
 // ------------------------------------------------------------------------------------ dQ
+// Offset (elements) of row r, 16-byte chunk c of a row-major LDS tile read two ways: by rows
+// (16 consecutive rows at one chunk) and transposed (ds_read_b64_tr_b16: 4 consecutive rows x
+// 4 aligned chunks per half-wave). With 16 chunks per row the chunk is XORed with the row's two
+// low bit-pairs swapped, a bijection over 16 consecutive rows that also sends the 4 rows of a
+// transposed read to 4 different 64-byte bank groups; other widths use the row-modulo swizzle.
+template <int HD>
+__device__ __forceinline__ int bofs(int r, int c) {
+  constexpr int DCH = HD / 8;
+  if constexpr (DCH == 16)
+    return r * HD + 8 * (c ^ (((r & 3) << 2) | ((r >> 2) & 3)));
+  else
+    return kofs(r, c, HD, DCH < 16 ? DCH : 16);
+}
+
 template <int HD_, int BC_, int NW_, int WPE_, int DSPLIT_ = 1>
 struct BwdQCfg {
   static constexpr int HD = HD_, BC = BC_, NW = NW_, WPE = WPE_, DSPLIT = DSPLIT_;
@@ -186,7 +200,7 @@ bwd_dq_kernel(BwdParams p, int nqt) {
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
-      *(u32x4*)(base + kofs(r, c, C::HD, C::KSW)) = ld[j];
+      *(u32x4*)(base + bofs<C::HD>(r, c)) = ld[j];
     }
   };
 
@@ -213,7 +227,7 @@ bwd_dq_kernel(BwdParams p, int nqt) {
       for (int ds = 0; ds < C::NDS; ds++)
 #pragma unroll
         for (int jb = 0; jb < C::NB; jb++) {
-          const int off = kofs(jb * 32 + l32, 2 * ds + hh, C::HD, C::KSW);
+          const int off = bofs<C::HD>(jb * 32 + l32, 2 * ds + hh);
           s[jb] = Dt<T>::mma32(*(const V8*)(ks + off), qreg[ds], s[jb]);
           dp[jb] = Dt<T>::mma32(*(const V8*)(vs + off), doreg[ds], dp[jb]);
         }
@@ -248,7 +262,7 @@ bwd_dq_kernel(BwdParams p, int nqt) {
 #pragma unroll
           for (int a = 0; a < 2; a++) {
             const int row = 16 * g + 8 * a + 4 * hh + (j16 >> 2);
-            part[a] = lds_read_tr<T>(ks + kofs(row, col >> 3, C::HD, C::KSW) + (col & 7));
+            part[a] = lds_read_tr<T>(ks + bofs<C::HD>(row, col >> 3) + (col & 7));
           }
           V8 av;
 #pragma unroll
@@ -380,7 +394,7 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int ci = tid + (j < QJ ? j : j - QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
-      *(u32x4*)(base + (j < QJ ? 0 : C::TT) + kofs(r, c, C::HD, C::KSW)) = ld[j];
+      *(u32x4*)(base + (j < QJ ? 0 : C::TT) + bofs<C::HD>(r, c)) = ld[j];
     }
     if (tid < 2 * C::BQ) {
       // rows past SQ and rows without visible keys (LSE = -inf) get P = 0 through LSE = +inf
@@ -408,7 +422,7 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
       f32x16 s = f32x16{}, dp = f32x16{};
 #pragma unroll
       for (int ds = 0; ds < C::NDS; ds++) {
-        const int off = kofs(l32, 2 * ds + hh, C::HD, C::KSW);
+        const int off = bofs<C::HD>(l32, 2 * ds + hh);
         s = Dt<T>::mma32(*(const V8*)(qs + off), kreg[ds], s);
         dp = Dt<T>::mma32(*(const V8*)(dos + off), vreg[ds], dp);
       }
@@ -441,7 +455,7 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
 #pragma unroll
           for (int a = 0; a < 2; a++) {
             const int row = 16 * st + 8 * a + 4 * hh + (j16 >> 2);
-            const int off = kofs(row, col >> 3, C::HD, C::KSW) + (col & 7);
+            const int off = bofs<C::HD>(row, col >> 3) + (col & 7);
             po[a] = lds_read_tr<T>(dos + off);
             pq[a] = lds_read_tr<T>(qs + off);
           }
