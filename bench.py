@@ -209,7 +209,7 @@ def summarize_stats(d, kernel_re=None, skip=0):
 
 # kernel symbols of the measured workloads (one symbol per workload in the PMC runs, which
 # leave out the fwd extras that share the headline's symbol)
-FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128E\w*ELb1ELb0EEEv9FwdParamsi"
+FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128ELi64ELi4ELi2ELi1EEELb1ELb0EEEv9FwdParamsi"
 DEC_C4_KERNEL = r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0EEEv9DecParamsiii"
 
 
@@ -225,7 +225,7 @@ def profiled_traffic(kernel_re):
     return None
 
 
-def cpu_baseline(S=16384, H=32, D=128, heads=2, seed=0):
+def cpu_baseline(S=16384, H=32, D=128, heads=32, seed=0):
     """Exact fp32 torch reference on the host cores, `heads` of the H heads of the headline
     workload (one head at a time to bound memory), scaled to the full workload's FLOP rate."""
     import torch
@@ -251,7 +251,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=2)
+    ap.add_argument("--cpu-heads", type=int, default=32)
     ap.add_argument("--extras", default="fwd,bwd,decode,varlen")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")

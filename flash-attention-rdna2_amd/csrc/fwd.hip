@@ -396,7 +396,9 @@ fwd_kernel(FwdParams p, int nqt) {
     gload_k(kb1 + C::BC);
     gload_v(kb1);
     f32x16 s[QB][C::NB];
+    __builtin_amdgcn_s_setprio(1);
     qk((t + 1) & 1, s);
+    __builtin_amdgcn_s_setprio(0);
     pv(t & 1, pb);
 #pragma unroll
     for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, i, s[i], kb1, pb[i], resc[i]);
