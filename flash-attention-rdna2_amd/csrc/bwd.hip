@@ -294,6 +294,7 @@ bwd_dq_kernel(BwdParams p, int nqt) {
 // ---------------------------------------------------------------------------------- dK, dV
 template <int HD_, int NW_, int WPE_, int DSPLIT_ = 1>
 struct BwdKVCfg {
+  static constexpr bool PAIR = false;
   static constexpr int HD = HD_, NW = NW_, WPE = WPE_, DSPLIT = DSPLIT_;
   static constexpr int NT = NW * 64;
   static constexpr int BQ = 32;         // queries per stage
@@ -494,6 +495,256 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
   }
 }
 
+// ------------------------------------------------------------------- dK, dV with wave pairs
+// Each 32-key block belongs to a pair of waves on the same SIMD slot pattern (wave w and w+NP):
+// the S-wave holds K and computes S = Q K^T, P, and dV += dO^T P; the dP-wave holds V and, one
+// tile behind, computes dP = dO V^T, dS = P deriv (dP - D) and dK += Q^T dS, taking P deriv
+// (fp32) from the S-wave through LDS. No product is computed twice, and each wave needs about
+// half the registers of a wave that owns both accumulators, so two waves fit per SIMD and
+// one's VALU work overlaps the other's MFMAs. The Q/dO tiles sit in a 4-stage LDS ring (the
+// S-wave reads tile t, the dP-wave tile t-1, tile t+1 is stored) and tiles t+2 .. t+NSET are in
+// flight in registers; one barrier per tile.
+template <int HD_, int NP_, int NSET_>
+struct BwdKVPCfg {
+  static constexpr bool PAIR = true;
+  static constexpr int HD = HD_, NP = NP_, NW = 2 * NP_, WPE = 2, DSPLIT = 1;
+  static constexpr int NSET = NSET_;       // global-load prefetch distance (tiles), 2 or 3
+  static_assert(NSET == 2 || NSET == 3, "prefetch distance");
+  static constexpr int NT = NW * 64;
+  static constexpr int BQ = 32;            // queries per stage
+  static constexpr int BK = NP * 32;       // keys per workgroup
+  static constexpr int NDS = HD / 16;
+  static constexpr int NDB = HD / 32;
+  static constexpr int DCH = HD / 8;
+  static constexpr int TT = BQ * HD;       // elements per Q (or dO) tile
+  static constexpr int STAGE = 2 * TT;
+  static constexpr int CH = 2 * BQ * DCH;  // chunks per stage (Q and dO)
+  static constexpr int PER = CH / NT;
+  static constexpr int QJ = BQ * DCH / NT; // Q chunk slots per thread (the rest are dO)
+  static_assert(CH % NT == 0 && (BQ * DCH) % NT == 0, "loader split");
+};
+
+template <typename T, class C, bool CAUSAL, bool FEAT>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
+                          amdgpu_waves_per_eu(C::WPE, C::WPE))) void
+bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
+  using V8 = typename Dt<T>::V8;
+  using V4 = typename Dt<T>::V4;
+  __shared__ __attribute__((aligned(16))) T lds[4 * C::STAGE];
+  __shared__ __attribute__((aligned(16))) float rowv[4][2][C::BQ];  // [stage][lse2 | D][q]
+  // P deriv hand-over, [buffer][pair][rq][lane] x 4 floats: lane-contiguous 16-byte records
+  __shared__ __attribute__((aligned(16))) f32x4 pdx[2][C::NP][4][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
+  const bool dpw = wave >= C::NP;  // dP-wave (holds V, accumulates dK)
+  const int pair = dpw ? wave - C::NP : wave;
+
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int kt = w % nkt, zh = w / nkt;
+  const int kvh = zh % p.Hk, b = zh / p.Hk;
+  const int SQ = p.SQ, SK = p.SK, delta = SK - SQ;
+  const int kb0 = kt * C::BK;
+  if (kb0 >= SK) return;
+
+  const int kw = kb0 + 32 * pair, key = kw + l32;
+  const bool pair_keys = kw < SK;
+  // B operand rows of this wave's product with the Q (or dO) tile: K for the S-wave, V for the
+  // dP-wave; lane holds key `key`, head-dim 16*ds + 8*hh .. +7
+  const T* Rg = dpw ? (const T*)p.V + (long long)b * p.vs.b + (long long)kvh * p.vs.h
+                    : (const T*)p.K + (long long)b * p.ks.b + (long long)kvh * p.ks.h;
+  const long long rstride = dpw ? p.vs.s : p.ks.s;
+  V8 kv[C::NDS];
+#pragma unroll
+  for (int ds = 0; ds < C::NDS; ds++)
+    kv[ds] = key < SK ? *(const V8*)(Rg + (long long)key * rstride + 16 * ds + 8 * hh)
+                      : bitcast<V8>(u32x4{0, 0, 0, 0});
+  f32x16 acc[C::NDB];  // dV^T (S-wave) or dK^T (dP-wave)
+#pragma unroll
+  for (int db = 0; db < C::NDB; db++) acc[db] = f32x16{};
+
+  int bq0, bq1, wq0 = 0, wq1 = 0;
+  query_range_b<CAUSAL, FEAT>(p, kb0, min(kb0 + C::BK, SK) - 1, delta, SQ, bq0, bq1);
+  if (pair_keys) query_range_b<CAUSAL, FEAT>(p, kw, min(kw + 32, SK) - 1, delta, SQ, wq0, wq1);
+  const int qstart = (max(bq0, 0) / C::BQ) * C::BQ;
+  const int ntq = bq1 > bq0 ? (bq1 - qstart + C::BQ - 1) / C::BQ : 0;
+  const int total = ntq * p.gqa;
+  const float c_log2 = p.scale * kLog2e;
+
+  // Q/dO tiles through buffer descriptors over rows qt0..SQ-1 (rows past SQ read as zeros);
+  // each thread's first QJ chunk slots are Q, the rest dO. LSE/D row values are loaded
+  // unconditionally (clamped row) and turned into log2-domain LSE / D at store time.
+  int voff[C::PER];
+#pragma unroll
+  for (int j = 0; j < C::PER; j++) {
+    const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
+    voff[j] = r * (int)((j < C::QJ ? p.qs.s : p.dos.s) * 2) + 16 * c;
+  }
+  // NSET register sets: tile it+NSET is loaded while tile it+1 (loaded NSET-1 iterations
+  // earlier) is stored, so every global load has NSET iterations to land
+  constexpr int NSET = C::NSET;
+  u32x4 ld[NSET][C::PER];
+  float lraw[NSET];
+  bool lok[NSET];
+  const int rsel = tid % (2 * C::BQ);  // row value slot: [0,BQ) LSE, [BQ,2BQ) D
+  auto gload = [&](auto set, int it) {
+    constexpr int S = decltype(set)::value;
+    const int hg = min(it / max(ntq, 1), p.gqa - 1), qt0 = qstart + (it % max(ntq, 1)) * C::BQ;
+    const int h = kvh * p.gqa + hg;
+    const long long rows = it < total ? (long long)(SQ - qt0) : 0;  // past the end: all zeros
+    const auto rq = buf_rsrc((const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h + (long long)qt0 * p.qs.s,
+                             rows * p.qs.s * 2);
+    const auto rd = buf_rsrc((const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + (long long)qt0 * p.dos.s,
+                             rows * p.dos.s * 2);
+#pragma unroll
+    for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(j < C::QJ ? rq : rd, voff[j]);
+    const int q = qt0 + (rsel % C::BQ);
+    lok[S] = it < total && q < SQ;
+    lraw[S] = 0.0f;
+    if (it < total) {  // (uniform) the loop runs past the last tile; SQ may be 0
+      const long long ri = ((long long)b * p.Hq + h) * SQ + min(q, SQ - 1);
+      lraw[S] = rsel < C::BQ ? p.lse[ri] : p.dsum[ri];
+    }
+  };
+  auto lstore = [&](auto set, int stage) {
+    constexpr int S = decltype(set)::value;
+    T* base = lds + stage * C::STAGE;
+#pragma unroll
+    for (int j = 0; j < C::PER; j++) {
+      const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
+      *(u32x4*)(base + (j < C::QJ ? 0 : C::TT) + bofs<C::HD>(r, c)) = ld[S][j];
+    }
+    if (tid < 2 * C::BQ) {
+      // rows past SQ and rows without visible keys (LSE = -inf) get P = 0 through LSE = +inf
+      const float lv = rsel < C::BQ ? ((lok[S] && lraw[S] != -INFINITY) ? lraw[S] * kLog2e : INFINITY)
+                                    : (lok[S] ? lraw[S] : 0.0f);
+      rowv[stage][rsel / C::BQ][rsel % C::BQ] = lv;
+    }
+  };
+  auto active = [&](int it) {
+    const int qt0 = qstart + (it % ntq) * C::BQ;
+    return pair_keys && qt0 < wq1 && qt0 + C::BQ > wq0;
+  };
+  // this wave's product of a tile with its B rows: S (S-wave, with Q) or dP (dP-wave, with
+  // dO); x[r] is query qt0 + 8*(r/4) + 4*hh + (r%4), key `key`
+  // (two independent accumulation chains, even and odd contraction steps)
+  auto rowprod = [&](const T* tile) {
+    f32x16 x0 = f32x16{}, x1 = f32x16{};
+#pragma unroll
+    for (int ds = 0; ds < C::NDS; ds += 2) {
+      x0 = Dt<T>::mma32(*(const V8*)(tile + bofs<C::HD>(l32, 2 * ds + hh)), kv[ds], x0);
+      x1 = Dt<T>::mma32(*(const V8*)(tile + bofs<C::HD>(l32, 2 * ds + 2 + hh)), kv[ds + 1], x1);
+    }
+    return x0 + x1;
+  };
+  // acc^T += tile^T . B (A operand by transposing reads of the tile; B = P or dS)
+  auto tprod = [&](const T* tile, const V8 (&bop)[2]) {
+#pragma unroll
+    for (int db = 0; db < C::NDB; db++) {
+      const int col = 32 * db + 16 * mh + 4 * (j16 & 3);
+#pragma unroll
+      for (int sq = 0; sq < 2; sq++) {
+        V4 part[2];
+#pragma unroll
+        for (int a = 0; a < 2; a++) {
+          const int row = 16 * sq + 8 * a + 4 * hh + (j16 >> 2);
+          part[a] = lds_read_tr<T>(tile + bofs<C::HD>(row, col >> 3) + (col & 7));
+        }
+        V8 av;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          av[e] = part[0][e];
+          av[4 + e] = part[1][e];
+        }
+        acc[db] = Dt<T>::mma32(av, bop[sq], acc[db]);
+      }
+    }
+  };
+
+  // 4-stage ring (a power of two keeps the stage index cheap; three would do): the S-wave
+  // reads tile it (stage it%4), the dP-wave tile it-1, tile it+1 is stored into the stage tile
+  // it-3 used; tiles it+2 .. it+NSET are in flight in registers
+  if (total > 0) {
+    gload(std::integral_constant<int, 0>{}, 0);
+    lstore(std::integral_constant<int, 0>{}, 0);
+    gload(std::integral_constant<int, 1>{}, 1);
+    if constexpr (NSET > 2) gload(std::integral_constant<int, 2>{}, 2);
+  }
+  __syncthreads();
+  // iteration it (it % NSET == S): the S-wave works on tile it, the dP-wave on tile it-1
+  auto step = [&](auto set, int it) {
+    constexpr int S = decltype(set)::value;
+    gload(set, it + NSET);  // set S held tile it, stored an iteration ago
+    if (!dpw) {
+      if (it < total && active(it)) {
+        const int st = it & 3, hg = it / ntq, qt0 = qstart + (it % ntq) * C::BQ;
+        const float slope = (FEAT && p.alibi) ? p.alibi[kvh * p.gqa + hg] : 0.0f;
+        const T* qs = lds + st * C::STAGE;
+        const f32x16 sv = rowprod(qs);
+        const bool edge = FEAT || (CAUSAL && kw + 31 > qt0 + delta) || qt0 + C::BQ > SQ || kw + 32 > SK;
+        V8 pP[2];
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+          const f32x4 l4 = *(const f32x4*)&rowv[st][0][8 * rq + 4 * hh];
+          f32x4 pd4;
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            const int r = 4 * rq + c, q = qt0 + 8 * rq + 4 * hh + c;
+            float deriv;
+            const float x = bwd_logit2<FEAT>(p, sv[r], c_log2, slope, q, key, deriv);
+            float pr = exp2_fast(x - l4[c]);
+            if (edge && !visible_b<CAUSAL, FEAT>(p, q, key, delta, SQ, SK)) pr = 0.0f;
+            pP[r >> 3][r & 7] = (T)pr;
+            pd4[c] = pr * deriv;
+          }
+          pdx[it & 1][pair][rq][lane] = pd4;
+        }
+        tprod(qs + C::TT, pP);  // dV^T += dO^T . P
+      }
+    } else {
+      const int t = it - 1;
+      if (t >= 0 && active(t)) {
+        const int st = t & 3;
+        const T* qs = lds + st * C::STAGE;
+        const f32x16 dpv = rowprod(qs + C::TT);
+        V8 pS[2];
+#pragma unroll
+        for (int rq = 0; rq < 4; rq++) {
+          const f32x4 d4 = *(const f32x4*)&rowv[st][1][8 * rq + 4 * hh];
+          const f32x4 pd4 = pdx[t & 1][pair][rq][lane];
+#pragma unroll
+          for (int c = 0; c < 4; c++) {
+            const int r = 4 * rq + c;
+            pS[r >> 3][r & 7] = (T)(pd4[c] * (dpv[r] - d4[c]));
+          }
+        }
+        tprod(qs, pS);  // dK^T += Q^T . dS
+      }
+    }
+    lstore(std::integral_constant<int, (S + 1) % NSET>{}, (it + 1) & 3);  // tile it+1
+    __syncthreads();
+  };
+  for (int it = 0; it <= total; it += NSET) {
+    step(std::integral_constant<int, 0>{}, it);
+    if (it + 1 <= total) step(std::integral_constant<int, 1>{}, it + 1);
+    if constexpr (NSET > 2)
+      if (it + 2 <= total) step(std::integral_constant<int, 2>{}, it + 2);
+  }
+  if (key < SK) {
+    T* row = dpw ? (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (long long)key * p.dks.s
+                 : (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (long long)key * p.dvs.s;
+    const float sc = dpw ? p.scale : 1.0f;
+#pragma unroll
+    for (int db = 0; db < C::NDB; db++)
+#pragma unroll
+      for (int rq = 0; rq < 4; rq++) {
+        V4 v;
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = (T)(acc[db][4 * rq + c] * sc);
+        *(V4*)(row + 32 * db + 8 * rq + 4 * hh) = v;
+      }
+  }
+}
+
 template <typename T, class CQ, class CKV, bool CAUSAL, bool FEAT>
 static int launch_bwd2(const BwdParams& p, hipStream_t st) {
   const int nqt = (p.SQ + CQ::BQ - 1) / CQ::BQ;
@@ -506,7 +757,10 @@ static int launch_bwd2(const BwdParams& p, hipStream_t st) {
     if (int rc = launch_status("fable_attn_backward_launch (dq)")) return rc;
   }
   if (gkv > 0) {
-    hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
+    if constexpr (CKV::PAIR)
+      hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
+    else
+      hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
     if (int rc = launch_status("fable_attn_backward_launch (dkdv)")) return rc;
   }
   return FA_OK;
@@ -524,8 +778,8 @@ static int launch_bwd(const BwdParams& p, hipStream_t st) {
 template <typename T>
 static int bwd_dispatch(const BwdParams& p, hipStream_t st) {
   switch (p.D) {
-    case 64: return launch_bwd<T, BwdQCfg<64, 64, 4, 2>, BwdKVCfg<64, 4, 2>>(p, st);
-    case 128: return launch_bwd<T, BwdQCfg<128, 32, 4, 2>, BwdKVCfg<128, 4, 1>>(p, st);
+    case 64: return launch_bwd<T, BwdQCfg<64, 64, 4, 2>, BwdKVPCfg<64, 2, 3>>(p, st);
+    case 128: return launch_bwd<T, BwdQCfg<128, 32, 4, 2>, BwdKVPCfg<128, 4, 2>>(p, st);
     case 256: return launch_bwd<T, BwdQCfg<256, 32, 4, 1, 2>, BwdKVCfg<256, 4, 1, 4>>(p, st);
     default: return fail(FA_ERR_HEADDIM, "fable_attn_backward_launch: head_dim=%d has no kernel (64, 128, 256)", p.D);
   }
