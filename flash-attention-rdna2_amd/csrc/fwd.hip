@@ -264,7 +264,12 @@ fwd_kernel(FwdParams p, int nqt) {
   // accumulators must be scaled by once every earlier tile's PV product is in them; `resc` is
   // set when any lane's is not 1. Branch-free, so the compiler can interleave it with
   // independent matrix-core work.
-  auto softmax = [&](auto masked, int i, f32x16 (&s)[C::NB], int kb, V8 (&pb)[C::NG], bool& resc) {
+  // FEAT logits in log2 units. softcap: c * tanh(x / c) with x = scale * q.k, tanh(y) =
+  // 1 - 2 / (exp(2y) + 1); exp(2y) = exp2(q.k * kcap), so no division per score
+  const float kcap = p.softcap > 0.0f ? 2.0f * kLog2e * p.scale / p.softcap : 0.0f;
+  const float lcap = p.softcap * kLog2e;
+  const float aslope2 = aslope * kLog2e;
+  auto softmax = [&](auto masked, auto cap, int i, f32x16 (&s)[C::NB], int kb, V8 (&pb)[C::NG], bool& resc) {
     const int qi = qw + 32 * i + l32;
     const int kq = kb + 4 * hh;  // key of s[jb][r] = kq + 32*jb + 8*(r/4) + (r%4)
     if constexpr (FEAT) {
@@ -273,18 +278,28 @@ fwd_kernel(FwdParams p, int nqt) {
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
-          float x = s[jb][r] * p.scale;
-          if (p.softcap > 0.0f) x = p.softcap * tanh_exp(x / p.softcap);
-          x += aslope * (float)(key - qi);
-          bool ok = key < SK;
-          if (CAUSAL) ok = ok && key <= qi + delta;
-          if (p.win_left >= 0) ok = ok && key >= qi + delta - p.win_left;
-          if (p.win_right >= 0) ok = ok && key <= qi + delta + p.win_right;
-          if (p.attn_chunk > 0) {
-            const int cs = (max(qi + delta, 0) / p.attn_chunk) * p.attn_chunk;
-            ok = ok && key >= cs && key < cs + p.attn_chunk;
+          float x;
+          if constexpr (decltype(cap)::value) {
+            const float e = exp2_fast(s[jb][r] * kcap);
+            x = fmaf(-2.0f * lcap, __builtin_amdgcn_rcpf(e + 1.0f), lcap);
+          } else {
+            x = s[jb][r] * c_log2;
           }
-          s[jb][r] = ok ? x * kLog2e : -INFINITY;
+          x = fmaf(aslope2, (float)(key - qi), x);
+          if constexpr (decltype(masked)::value) {
+            bool ok = key < SK;
+            if (CAUSAL) ok = ok && key <= qi + delta;
+            if (p.win_left >= 0) ok = ok && key >= qi + delta - p.win_left;
+            if (p.win_right >= 0) ok = ok && key <= qi + delta + p.win_right;
+            if (p.attn_chunk > 0) {
+              const int cs = (max(qi + delta, 0) / p.attn_chunk) * p.attn_chunk;
+              ok = ok && key >= cs && key < cs + p.attn_chunk;
+            }
+            x = ok ? x : -INFINITY;
+          }
+          s[jb][r] = x;
+          // bound how many scores the scheduler transforms at once (register pressure)
+          if ((r & 7) == 7) __builtin_amdgcn_sched_barrier(0);
         }
     } else if constexpr (decltype(masked)::value) {
 #pragma unroll
@@ -339,8 +354,22 @@ fwd_kernel(FwdParams p, int nqt) {
     const int kb = kstart + t * C::BC;
     return wave_rows && kb < wk1 && kb + C::BC > wk0;
   };
+  // FEAT tiles that every row of this wave sees in full (no mask code); chunked attention
+  // always takes the masked path
+  auto interior = [&](int t) {
+    const int kb = kstart + t * C::BC, ke = kb + C::BC - 1;
+    const int r0 = qw + delta, r1 = qw + 32 * QB - 1 + delta;
+    bool ok = ke < SK && p.attn_chunk <= 0;
+    if (CAUSAL) ok = ok && ke <= r0;
+    if (p.win_right >= 0) ok = ok && ke <= r0 + p.win_right;
+    if (p.win_left >= 0) ok = ok && kb >= r1 - p.win_left;
+    return ok;
+  };
   using Plain = std::integral_constant<bool, false>;
   using Masked = std::integral_constant<bool, true>;
+  using Cap0 = std::integral_constant<bool, false>;
+  using Cap1 = std::integral_constant<bool, true>;
+  const bool has_cap = FEAT && p.softcap > 0.0f;
 
   // ---- prologue: K tiles 0 and 1, V tile 0 in LDS; S and P of tile 0
   V8 pb[QB][C::NG];
@@ -378,11 +407,16 @@ fwd_kernel(FwdParams p, int nqt) {
       a_cur = true;
       qk(0, s);
 #pragma unroll
-      for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, i, s[i], kstart, pb[i], resc[i]);
+      for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, Cap0{}, i, s[i], kstart, pb[i], resc[i]);
     } else if ((a_cur = active(0))) {
       qk(0, s);
+      if (has_cap) {
 #pragma unroll
-      for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, i, s[i], kstart, pb[i], resc[i]);
+        for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, Cap1{}, i, s[i], kstart, pb[i], resc[i]);
+      } else {
+#pragma unroll
+        for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, Cap0{}, i, s[i], kstart, pb[i], resc[i]);
+      }
     }
   }
   __syncthreads();  // every wave has read K stage 0 before iteration 0 refills it
@@ -401,7 +435,7 @@ fwd_kernel(FwdParams p, int nqt) {
     __builtin_amdgcn_s_setprio(0);
     pv(t & 1, pb);
 #pragma unroll
-    for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, i, s[i], kb1, pb[i], resc[i]);
+    for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, Cap0{}, i, s[i], kb1, pb[i], resc[i]);
     lstore_k(t & 1);
     lstore_v((t + 1) & 1);
     __syncthreads();
@@ -417,8 +451,16 @@ fwd_kernel(FwdParams p, int nqt) {
     if (a_next) qk((t + 1) & 1, s);
     if (a_cur) pv(t & 1, pb);
     if (a_next) {
+      // FEAT tiles every row of the wave sees in full skip the mask code
+      auto sm = [&](auto masked, auto cap) {
 #pragma unroll
-      for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, i, s[i], kb1, pb[i], resc[i]);
+        for (int i = 0; i < QB; i++) corr[i] = softmax(masked, cap, i, s[i], kb1, pb[i], resc[i]);
+      };
+      if (FEAT && interior(t + 1)) {
+        if (has_cap) sm(Plain{}, Cap1{}); else sm(Plain{}, Cap0{});
+      } else {
+        if (has_cap) sm(Masked{}, Cap1{}); else sm(Masked{}, Cap0{});
+      }
     }
     a_cur = a_next;
     lstore_k(t & 1);
@@ -449,25 +491,28 @@ fwd_kernel(FwdParams p, int nqt) {
   }
 }
 
-template <typename T, class C>
+// C runs the plain masks (causal / sequence end), CF the feature kernels (window, chunk,
+// softcap, alibi), whose extra per-score work needs a different register balance
+template <typename T, class C, class CF = C>
 static int launch_fwd(const FwdParams& p, hipStream_t st) {
-  const int nqt = (p.SQ + C::BR - 1) / C::BR;
+  const bool feat = p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
+                    p.win_left >= 0 || (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
+  const int br = feat ? CF::BR : C::BR;
+  const int nqt = (p.SQ + br - 1) / br;
   const long long nblk = (long long)nqt * p.NH * p.batch;
   if (nblk <= 0) return FA_OK;
   if (nblk > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fa_forward_launch: grid too large");
-  const bool feat = p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
-                    p.win_left >= 0 || (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
-  dim3 grid((unsigned)nblk), block(C::NT);
+  dim3 grid((unsigned)nblk);
   if (p.causal) {
     if (feat)
-      hipLaunchKernelGGL((fwd_kernel<T, C, true, true>), grid, block, 0, st, p, nqt);
+      hipLaunchKernelGGL((fwd_kernel<T, CF, true, true>), grid, dim3(CF::NT), 0, st, p, nqt);
     else
-      hipLaunchKernelGGL((fwd_kernel<T, C, true, false>), grid, block, 0, st, p, nqt);
+      hipLaunchKernelGGL((fwd_kernel<T, C, true, false>), grid, dim3(C::NT), 0, st, p, nqt);
   } else {
     if (feat)
-      hipLaunchKernelGGL((fwd_kernel<T, C, false, true>), grid, block, 0, st, p, nqt);
+      hipLaunchKernelGGL((fwd_kernel<T, CF, false, true>), grid, dim3(CF::NT), 0, st, p, nqt);
     else
-      hipLaunchKernelGGL((fwd_kernel<T, C, false, false>), grid, block, 0, st, p, nqt);
+      hipLaunchKernelGGL((fwd_kernel<T, C, false, false>), grid, dim3(C::NT), 0, st, p, nqt);
   }
   return launch_status("fa_forward_launch");
 }
@@ -476,7 +521,7 @@ template <typename T>
 static int dispatch_hd(const FwdParams& p, hipStream_t st) {
   switch (p.HD) {
     case 64: return launch_fwd<T, FwdCfg<64, 64, 4, 2>>(p, st);
-    case 128: return launch_fwd<T, FwdCfg<128, 64, 4, 2>>(p, st);
+    case 128: return launch_fwd<T, FwdCfg<128, 64, 4, 2>, FwdCfg<128, 32, 4, 2>>(p, st);
     case 256: return launch_fwd<T, FwdCfg<256, 32, 4, 1>>(p, st);
     default: return fail(FA_ERR_HEADDIM, "fa_forward_launch: head_dim=%d has no kernel (64, 128, 256)", p.HD);
   }
