@@ -67,7 +67,8 @@ __device__ __forceinline__ float bwd_logit2(const BwdParams& p, float s, float c
   float x = s * p.scale;
   deriv = 1.0f;
   if (p.softcap > 0.0f) {
-    const float t = tanh_exp(x / p.softcap);
+    // (the reciprocal is uniform: one division per call site after hoisting, not per score)
+    const float t = tanh_exp(x * (1.0f / p.softcap));
     x = p.softcap * t;
     deriv = 1.0f - t * t;
   }
