@@ -76,6 +76,30 @@ __device__ __forceinline__ float bwd_logit2(const BwdParams& p, float s, float c
   return x * kLog2e;
 }
 
+// Lengths and first packed rows of sequence b (dense: the whole [SQ, SK] and row 0; varlen:
+// from cu_q/cu_k, cut by seqused). Pointer bases are base + b*str.b + row*str.s + h*str.h, so
+// varlen callers pass b strides of 0; lse/dsum (b, h, q) is at b*lse_sb + h*lse_sh + qo + q.
+struct BwdSeq {
+  int SQ, SK;
+  long long qo, ko;
+};
+__device__ __forceinline__ BwdSeq bwd_seq(const BwdParams& p, int b) {
+  BwdSeq s;
+  if (p.cu_q) {
+    s.qo = p.cu_q[b];
+    s.ko = p.cu_k[b];
+    s.SQ = p.cu_q[b + 1] - p.cu_q[b];
+    s.SK = p.cu_k[b + 1] - p.cu_k[b];
+    if (p.seqused_q) s.SQ = min(s.SQ, p.seqused_q[b]);
+    if (p.seqused_k) s.SK = min(s.SK, p.seqused_k[b]);
+  } else {
+    s.qo = s.ko = 0;
+    s.SQ = p.SQ;
+    s.SK = p.SK;
+  }
+  return s;
+}
+
 // ------------------------------------------------------------------------------------ dQ
 // Offset (elements) of row r, 16-byte chunk c of a row-major LDS tile read two ways: by rows
 // (16 consecutive rows at one chunk) and transposed (ds_read_b64_tr_b16: 4 consecutive rows x
@@ -126,18 +150,19 @@ bwd_dq_kernel(BwdParams p, int nqt) {
   const int h = zh % p.Hq, b = zh / p.Hq;
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
   const int kvh = h / p.gqa;
-  const int SQ = p.SQ, SK = p.SK, delta = SK - SQ;
+  const BwdSeq sq = bwd_seq(p, b);
+  const int SQ = sq.SQ, SK = sq.SK, delta = SK - SQ;
   const int qb = qt * C::BQ;
   const int dbase = dpass * C::NDB * 32;
   if (qb >= SQ) return;
 
-  const T* Qg = (const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h;
-  const T* dOg = (const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h;
-  const T* Og = (const T*)p.O + (long long)b * p.os.b + (long long)h * p.os.h;
-  const T* Kg = (const T*)p.K + (long long)b * p.ks.b + (long long)kvh * p.ks.h;
-  const T* Vg = (const T*)p.V + (long long)b * p.vs.b + (long long)kvh * p.vs.h;
-  T* dQg = (T*)p.dQ + (long long)b * p.dqs.b + (long long)h * p.dqs.h;
-  const long long row0 = ((long long)b * p.Hq + h) * SQ;
+  const T* Qg = (const T*)p.Q + (long long)b * p.qs.b + sq.qo * p.qs.s + (long long)h * p.qs.h;
+  const T* dOg = (const T*)p.dO + (long long)b * p.dos.b + sq.qo * p.dos.s + (long long)h * p.dos.h;
+  const T* Og = (const T*)p.O + (long long)b * p.os.b + sq.qo * p.os.s + (long long)h * p.os.h;
+  const T* Kg = (const T*)p.K + (long long)b * p.ks.b + sq.ko * p.ks.s + (long long)kvh * p.ks.h;
+  const T* Vg = (const T*)p.V + (long long)b * p.vs.b + sq.ko * p.vs.s + (long long)kvh * p.vs.h;
+  T* dQg = (T*)p.dQ + (long long)b * p.dqs.b + sq.qo * p.dqs.s + (long long)h * p.dqs.h;
+  const long long row0 = (long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo;
 
   const int qw = qb + 32 * wave, qi = qw + l32;
   const bool wave_rows = qw < SQ;
@@ -326,12 +351,13 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
   const int kt = w2 % nkt, zh = w2 / nkt;
   const int kvh = zh % p.Hk, b = zh / p.Hk;
   const int dbase = dpass * C::NDB * 32;
-  const int SQ = p.SQ, SK = p.SK, delta = SK - SQ;
+  const BwdSeq sq = bwd_seq(p, b);
+  const int SQ = sq.SQ, SK = sq.SK, delta = SK - SQ;
   const int kb0 = kt * C::BK;
   if (kb0 >= SK) return;
 
-  const T* Kg = (const T*)p.K + (long long)b * p.ks.b + (long long)kvh * p.ks.h;
-  const T* Vg = (const T*)p.V + (long long)b * p.vs.b + (long long)kvh * p.vs.h;
+  const T* Kg = (const T*)p.K + (long long)b * p.ks.b + sq.ko * p.ks.s + (long long)kvh * p.ks.h;
+  const T* Vg = (const T*)p.V + (long long)b * p.vs.b + sq.ko * p.vs.s + (long long)kvh * p.vs.h;
   const int kw = kb0 + 32 * wave, key = kw + l32;
   const bool wave_keys = kw < SK;
 
@@ -380,15 +406,15 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
     const int hg = min(it / ntq, p.gqa - 1), qt0 = qstart + (it % ntq) * C::BQ;
     const int h = kvh * p.gqa + hg;
     const long long rows = it < total ? (long long)(SQ - qt0) : 0;  // past the end: all zeros
-    const auto rq = buf_rsrc((const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h + (long long)qt0 * p.qs.s,
+    const auto rq = buf_rsrc((const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h + (sq.qo + qt0) * p.qs.s,
                              rows * p.qs.s * 2);
-    const auto rd = buf_rsrc((const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + (long long)qt0 * p.dos.s,
+    const auto rd = buf_rsrc((const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + (sq.qo + qt0) * p.dos.s,
                              rows * p.dos.s * 2);
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(j < QJ ? rq : rd, voff[j]);
     const int q = qt0 + (rsel % C::BQ);
     lok = it < total && q < SQ;
-    const long long ri = ((long long)b * p.Hq + h) * SQ + min(q, SQ - 1);
+    const long long ri = (long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + min(q, SQ - 1);
     lraw = rsel < C::BQ ? p.lse[ri] : p.dsum[ri];
   };
   auto lstore = [&](int stage) {
@@ -478,8 +504,8 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
     __syncthreads();
   }
   if (key < SK) {
-    T* krow = (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (long long)key * p.dks.s;
-    T* vrow = (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (long long)key * p.dvs.s;
+    T* krow = (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (sq.ko + key) * p.dks.s;
+    T* vrow = (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (sq.ko + key) * p.dvs.s;
 #pragma unroll
     for (int db = 0; db < C::NDB; db++)
 #pragma unroll
@@ -543,7 +569,8 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int kt = w % nkt, zh = w / nkt;
   const int kvh = zh % p.Hk, b = zh / p.Hk;
-  const int SQ = p.SQ, SK = p.SK, delta = SK - SQ;
+  const BwdSeq sq = bwd_seq(p, b);
+  const int SQ = sq.SQ, SK = sq.SK, delta = SK - SQ;
   const int kb0 = kt * C::BK;
   if (kb0 >= SK) return;
 
@@ -551,8 +578,8 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   const bool pair_keys = kw < SK;
   // B operand rows of this wave's product with the Q (or dO) tile: K for the S-wave, V for the
   // dP-wave; lane holds key `key`, head-dim 16*ds + 8*hh .. +7
-  const T* Rg = dpw ? (const T*)p.V + (long long)b * p.vs.b + (long long)kvh * p.vs.h
-                    : (const T*)p.K + (long long)b * p.ks.b + (long long)kvh * p.ks.h;
+  const T* Rg = dpw ? (const T*)p.V + (long long)b * p.vs.b + sq.ko * p.vs.s + (long long)kvh * p.vs.h
+                    : (const T*)p.K + (long long)b * p.ks.b + sq.ko * p.ks.s + (long long)kvh * p.ks.h;
   const long long rstride = dpw ? p.vs.s : p.ks.s;
   V8 kv[C::NDS];
 #pragma unroll
@@ -592,9 +619,9 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
     const int hg = min(it / max(ntq, 1), p.gqa - 1), qt0 = qstart + (it % max(ntq, 1)) * C::BQ;
     const int h = kvh * p.gqa + hg;
     const long long rows = it < total ? (long long)(SQ - qt0) : 0;  // past the end: all zeros
-    const auto rq = buf_rsrc((const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h + (long long)qt0 * p.qs.s,
+    const auto rq = buf_rsrc((const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h + (sq.qo + qt0) * p.qs.s,
                              rows * p.qs.s * 2);
-    const auto rd = buf_rsrc((const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + (long long)qt0 * p.dos.s,
+    const auto rd = buf_rsrc((const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + (sq.qo + qt0) * p.dos.s,
                              rows * p.dos.s * 2);
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(j < C::QJ ? rq : rd, voff[j]);
@@ -602,7 +629,7 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
     lok[S] = it < total && q < SQ;
     lraw[S] = 0.0f;
     if (it < total) {  // (uniform) the loop runs past the last tile; SQ may be 0
-      const long long ri = ((long long)b * p.Hq + h) * SQ + min(q, SQ - 1);
+      const long long ri = (long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + min(q, SQ - 1);
       lraw[S] = rsel < C::BQ ? p.lse[ri] : p.dsum[ri];
     }
   };
@@ -731,8 +758,8 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
       if (it + 2 <= total) step(std::integral_constant<int, 2>{}, it + 2);
   }
   if (key < SK) {
-    T* row = dpw ? (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (long long)key * p.dks.s
-                 : (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (long long)key * p.dvs.s;
+    T* row = dpw ? (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (sq.ko + key) * p.dks.s
+                 : (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (sq.ko + key) * p.dvs.s;
     const float sc = dpw ? p.scale : 1.0f;
 #pragma unroll
     for (int db = 0; db < C::NDB; db++)
@@ -795,7 +822,13 @@ extern "C" int fable_attn_backward_launch(BwdParams p, int dtype, void* stream) 
   if (p.Hq <= 0 || p.Hk <= 0 || p.Hq % p.Hk || p.gqa != p.Hq / p.Hk)
     return fail(FA_ERR_ARG, "fable_attn_backward_launch: Hq=%d Hk=%d gqa=%d", p.Hq, p.Hk, p.gqa);
   if (p.dropout) return fail(FA_ERR_UNSUPPORTED, "fable_attn_backward_launch: dropout is not implemented");
+  if ((p.cu_q == nullptr) != (p.cu_k == nullptr))
+    return fail(FA_ERR_ARG, "fable_attn_backward_launch: cu_q and cu_k go together");
   if (p.B <= 0 || p.SQ < 0 || p.SK < 0) return FA_OK;  // empty ranges write zero gradients
+  if (!p.cu_q && p.lse_sb == 0 && p.lse_sh == 0) {  // dense [B,Hq,SQ] LSE / dsum
+    p.lse_sh = p.SQ;
+    p.lse_sb = (int64_t)p.Hq * p.SQ;
+  }
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
     case FA_F16: return bwd_dispatch<_Float16>(p, st);

@@ -6,6 +6,9 @@ bound at :239-268) with the same names, argument order and meaning:
         attn_chunk=0, out=None) -> (out, lse)
     bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, alibi,
         dropout_p, seed) -> (dq, dk, dv)
+    bwd_varlen(dout, q, k, v, out, lse, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left,
+               win_right, softcap, alibi, dropout_p, seed, seqused_q=None, seqused_k=None)
+        -> (dq, dk, dv)   (no counterpart in the reference's _C: native varlen backward)
     fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win_right,
                softcap, alibi, dropout_p, seed, attn_chunk=0, seqused_q=None,
                seqused_k=None, return_lse=False) -> out  (or (out, lse) when return_lse)
@@ -178,8 +181,54 @@ def bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, al
     p.dropout = 1 if dropout_p > 0 else 0
     p.drop_seed, p.dropout_p = int(seed) & ((1 << 64) - 1), float(dropout_p)
     p.keep_scale = 1.0 / (1.0 - dropout_p) if dropout_p > 0 else 1.0
+    p.lse_sb, p.lse_sh = Hq * SQ, SQ
     with torch.cuda.device(q.device):
         _lib.check(_L.fable_attn_backward_launch(p, _dt(q), _stream(q)), "fable_attn_backward_launch")
+    return dq, dk, dv
+
+
+def bwd_varlen(dout, q, k, v, out, lse, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left,
+               win_right, softcap, alibi, dropout_p, seed, seqused_q=None, seqused_k=None):
+    """Packed variable-length backward: dout/q/out (total_q, Hq, D), k/v (total_k, Hk, D),
+    cu_* int32 [batch+1], lse [Hq, total_q] fp32 (fwd_varlen(..., return_lse=True)). One launch
+    of each backward kernel for all sequences; the reference has none and loops over the
+    sequences in Python (flash_attn_interface.py:523-540). Returns (dq, dk, dv) packed; rows
+    outside every sequence (and past seqused) get zero gradient."""
+    _req(q.is_cuda and k.is_cuda and v.is_cuda, "GPU tensors required")
+    for n, t in (("dout", dout), ("q", q), ("k", k), ("v", v), ("out", out)):
+        _req(t.dim() == 3, f"{n}: varlen expects [total, H, D]")
+        _req(t.dtype == q.dtype and t.device == q.device, f"{n}: dtype/device mismatch")
+        _req(_rows_aligned(t), f"{n}: head_dim must be contiguous with 16-byte aligned rows")
+    Hq, D, Hk = q.shape[1], q.shape[2], k.shape[1]
+    _req(Hq % Hk == 0, "Hq must be a multiple of Hk (GQA)")
+    _req(dout.shape == q.shape and out.shape == q.shape and v.shape == k.shape, "shape mismatch")
+    _req(cu_q.dtype == torch.int32 and cu_k.dtype == torch.int32, "cu_seqlens must be int32")
+    _req(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (Hq, q.shape[0]),
+         "lse must be contiguous fp32 [Hq, total_q]")
+    batch = cu_q.numel() - 1
+    dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
+    dsum = torch.empty((Hq, q.shape[0]), dtype=torch.float32, device=q.device)
+    al = alibi.float().contiguous() if alibi is not None else None
+    row = lambda t: Strides(0, t.stride(1), t.stride(0))
+    p = BwdParams()
+    p.Q, p.K, p.V, p.O, p.dO = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr()
+    p.dQ, p.dK, p.dV = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    p.lse, p.dsum = lse.data_ptr(), dsum.data_ptr()
+    p.qs, p.ks, p.vs, p.os, p.dos = row(q), row(k), row(v), row(out), row(dout)
+    p.dqs, p.dks, p.dvs = row(dq), row(dk), row(dv)
+    p.B, p.Hq, p.Hk, p.SQ, p.SK, p.D, p.gqa = batch, Hq, Hk, int(max_sq), int(max_sk), D, Hq // Hk
+    p.scale, p.softcap = float(scale), float(softcap)
+    p.alibi = al.data_ptr() if al is not None else None
+    p.causal, p.win_left, p.win_right = 1 if causal else 0, int(win_left), int(win_right)
+    p.dropout = 1 if dropout_p > 0 else 0
+    p.drop_seed, p.dropout_p = int(seed) & ((1 << 64) - 1), float(dropout_p)
+    p.keep_scale = 1.0 / (1.0 - dropout_p) if dropout_p > 0 else 1.0
+    p.cu_q, p.cu_k = cu_q.data_ptr(), cu_k.data_ptr()
+    p.seqused_q = seqused_q.data_ptr() if seqused_q is not None else None
+    p.seqused_k = seqused_k.data_ptr() if seqused_k is not None else None
+    p.lse_sb, p.lse_sh = 0, q.shape[0]
+    with torch.cuda.device(q.device):
+        _lib.check(_L.fable_attn_backward_launch(p, _dt(q), _stream(q)), "fable_attn_backward_launch (varlen)")
     return dq, dk, dv
 
 

@@ -15,6 +15,8 @@ LIB_PATH = os.path.join(_HERE, "libfable_attn_hip.so")
 FA_F16, FA_BF16, FA_F32 = 0, 1, 2
 FA_OK = 0
 
+ABI_VERSION = 2  # FABLE_ATTN_ABI_VERSION of include/fable_attn_abi.h
+
 c_i32, c_i64, c_u64, c_f32, c_ptr = (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64,
                                      ctypes.c_float, ctypes.c_void_p)
 
@@ -44,7 +46,8 @@ class BwdParams(ctypes.Structure):
                 ("D", c_i32), ("gqa", c_i32), ("scale", c_f32), ("softcap", c_f32),
                 ("alibi", c_ptr), ("causal", c_i32), ("win_left", c_i32), ("win_right", c_i32),
                 ("dropout", c_i32), ("drop_seed", c_u64), ("dropout_p", c_f32),
-                ("keep_scale", c_f32)]
+                ("keep_scale", c_f32), ("cu_q", c_ptr), ("cu_k", c_ptr), ("seqused_q", c_ptr),
+                ("seqused_k", c_ptr), ("lse_sb", c_i64), ("lse_sh", c_i64)]
 
 
 class DecParams(ctypes.Structure):
@@ -96,7 +99,7 @@ def load():
     lib.fable_attn_struct_size.argtypes = [c_i32]
     lib.fable_attn_struct_size.restype = ctypes.c_size_t
     lib.fable_attn_last_error.restype = ctypes.c_char_p
-    if lib.fable_attn_abi_version() != 1:
+    if lib.fable_attn_abi_version() != ABI_VERSION:
         raise ImportError("fable_attn: ABI version mismatch between library and binding")
     for k, st in STRUCTS.items():
         if lib.fable_attn_struct_size(k) != ctypes.sizeof(st):

@@ -151,6 +151,44 @@ class _FableAttnFn(torch.autograd.Function):
         return dq, dk, dv, None, None, None, None, None, None, None, None, None, None
 
 
+class _FableVarlenFn(torch.autograd.Function):
+    """Autograd over the packed variable-length kernels: one forward launch (with LSE) and one
+    launch of each backward kernel for all sequences. The reference has no native varlen
+    backward and differentiates a per-sequence Python loop (:523-540)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, wl, wr, softcap, alibi,
+                dropout_p, attn_chunk, su_q, su_k):
+        seed = random.getrandbits(63) if dropout_p > 0 else 0
+        out, lse = _C.fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, float(scale), bool(causal),
+                                 int(wl), int(wr), float(softcap), alibi, float(dropout_p),
+                                 int(seed), int(attn_chunk), su_q, su_k, return_lse=True)
+        empty = torch.empty(0, device=q.device)
+        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k,
+                              alibi if alibi is not None else empty,
+                              su_q if su_q is not None else empty,
+                              su_k if su_k is not None else empty)
+        ctx.args = (max_sq, max_sk, scale, causal, wl, wr, softcap, dropout_p, seed, attn_chunk,
+                    alibi is not None, su_q is not None, su_k is not None)
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        (max_sq, max_sk, scale, causal, wl, wr, softcap, dropout_p, seed, attn_chunk,
+         has_alibi, has_suq, has_suk) = ctx.args
+        if attn_chunk:
+            raise NotImplementedError(
+                "fable_attn: backward with attention_chunk is not supported (as in FA-3); "
+                "run the chunked forward under torch.no_grad()")
+        q, k, v, out, lse, cu_q, cu_k, alibi, su_q, su_k = ctx.saved_tensors
+        dq, dk, dv = _C.bwd_varlen(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_sq,
+                                   max_sk, float(scale), bool(causal), int(wl), int(wr),
+                                   float(softcap), alibi if has_alibi else None,
+                                   float(dropout_p), int(seed),
+                                   su_q if has_suq else None, su_k if has_suk else None)
+        return (dq, dk, dv) + (None,) * 14
+
+
 def _attn_probs(q, k, lse, scale, causal, wl, wr, softcap, alibi, attn_chunk):
     """Debug path for return_attn_probs: the full [B,Hq,SQ,SK] probability matrix from the
     kernel's LSE, p = exp(s - lse) (reference :266-308). Materialises S x S."""
@@ -294,8 +332,9 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
                            num_splits=1, pack_gqa=None, sm_margin=0,
                            block_table=None):
     """Packed variable-length sequences: q (total_q, nheads, d), k/v (total_k, nheads_k, d),
-    cu_seqlens_* int32 (batch+1). Without grad: one kernel launch over all sequences. With grad:
-    per-sequence dense calls (the backward kernels are dense), as the reference."""
+    cu_seqlens_* int32 (batch+1). One forward launch over all sequences; with grad the
+    backward is one launch of each backward kernel over all sequences as well (the reference
+    loops over the sequences in Python on the grad path, :523-540)."""
     _reject_fp8(q_descale, k_descale, v_descale)
     _accept_hints(num_splits, pack_gqa, sm_margin)
     chunk = _check_chunk(attention_chunk)
@@ -310,34 +349,42 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
     elif softmax_scale is None:
         softmax_scale = 1.0 / math.sqrt(q.shape[-1])
     need_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
-    if not need_grad:
-        if q.dim() != 3:
-            raise ValueError(f"fable_attn: varlen expects (total, nheads, headdim), got {tuple(q.shape)}")
-        if q.shape[-1] > MAX_HEAD_DIM:
-            raise ValueError(f"fable_attn: head_dim={q.shape[-1]} exceeds the maximum {MAX_HEAD_DIM}")
-        if not q.is_cuda:
-            raise ValueError("fable_attn: tensors must be on the GPU (q.is_cuda == False)")
-        d_real = q.shape[-1]
-        d_ker = _kernel_dim(d_real)
-        if d_ker != d_real:
-            q, k, v = _pad_last(q, d_ker), _pad_last(k, d_ker), _pad_last(v, d_ker)
-            if dv_out is None:
-                dv_out = d_real
-        cflag, wl, wr = _map_window(causal, window_size)
-        al = alibi_slopes.float().contiguous() if alibi_slopes is not None else None
+    if q.dim() != 3:
+        raise ValueError(f"fable_attn: varlen expects (total, nheads, headdim), got {tuple(q.shape)}")
+    if q.shape[-1] > MAX_HEAD_DIM:
+        raise ValueError(f"fable_attn: head_dim={q.shape[-1]} exceeds the maximum {MAX_HEAD_DIM}")
+    if not q.is_cuda:
+        raise ValueError("fable_attn: tensors must be on the GPU (q.is_cuda == False)")
+    if q.shape[1] % k.shape[1] != 0:
+        raise ValueError(f"fable_attn: GQA needs nheads_q ({q.shape[1]}) divisible by nheads_k ({k.shape[1]})")
+    d_real = q.shape[-1]
+    d_ker = _kernel_dim(d_real)
+    if d_ker != d_real:
+        q, k, v = _pad_last(q, d_ker), _pad_last(k, d_ker), _pad_last(v, d_ker)
+        if dv_out is None:
+            dv_out = d_real
+    cflag, wl, wr = _map_window(causal, window_size)
+    al = alibi_slopes.float().contiguous() if alibi_slopes is not None else None
+    su_q = seqused_q.to(torch.int32).contiguous() if seqused_q is not None else None
+    su_k = seqused_k.to(torch.int32).contiguous() if seqused_k is not None else None
+    cu_q = cu_seqlens_q.to(torch.int32).contiguous()
+    cu_k = cu_seqlens_k.to(torch.int32).contiguous()
+    if need_grad:
+        out = _FableVarlenFn.apply(q.contiguous(), k.contiguous(), v.contiguous(), cu_q, cu_k,
+                                   int(max_seqlen_q), int(max_seqlen_k), float(softmax_scale),
+                                   bool(cflag), int(wl), int(wr), float(softcap), al,
+                                   float(dropout_p), int(chunk), su_q, su_k)
+    else:
         seed = random.getrandbits(63) if dropout_p > 0 else 0
-        su_q = seqused_q.to(torch.int32).contiguous() if seqused_q is not None else None
-        su_k = seqused_k.to(torch.int32).contiguous() if seqused_k is not None else None
-        out = _C.fwd_varlen(q.contiguous(), k.contiguous(), v.contiguous(),
-                            cu_seqlens_q.to(torch.int32).contiguous(),
-                            cu_seqlens_k.to(torch.int32).contiguous(),
+        out = _C.fwd_varlen(q.contiguous(), k.contiguous(), v.contiguous(), cu_q, cu_k,
                             int(max_seqlen_q), int(max_seqlen_k), float(softmax_scale),
                             bool(cflag), int(wl), int(wr), float(softcap), al, float(dropout_p),
                             int(seed), int(chunk), su_q, su_k)
-        if dv_out is not None:
-            out = out[..., :dv_out]
-        if return_attn_probs:
-            lse_l, probs_l = [], []
+    if dv_out is not None:
+        out = out[..., :dv_out]
+    if return_attn_probs:
+        lse_l, probs_l = [], []
+        with torch.no_grad():
             for i in range(cu_seqlens_q.numel() - 1):
                 a, b = int(cu_seqlens_q[i]), int(cu_seqlens_q[i + 1])
                 c, d = int(cu_seqlens_k[i]), int(cu_seqlens_k[i + 1])
@@ -351,22 +398,8 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
                                             deterministic, True, attention_chunk=chunk)
                 lse_l.append(li.squeeze(0))
                 probs_l.append(pi.squeeze(0))
-            return out, lse_l, probs_l
-        return out
-    outs = []
-    for i in range(cu_seqlens_q.numel() - 1):
-        qs, qe = int(cu_seqlens_q[i]), int(cu_seqlens_q[i + 1])
-        ks, ke = int(cu_seqlens_k[i]), int(cu_seqlens_k[i + 1])
-        if seqused_q is not None:
-            qe = qs + int(seqused_q[i])
-        if seqused_k is not None:
-            ke = ks + int(seqused_k[i])
-        o = flash_attn_func(q[qs:qe].unsqueeze(0), k[ks:ke].unsqueeze(0), v[ks:ke].unsqueeze(0),
-                            dropout_p, softmax_scale, causal, window_size, softcap,
-                            alibi_slopes, deterministic, False, attention_chunk=chunk)
-        outs.append(o.squeeze(0))
-    res = torch.cat(outs, dim=0)
-    return res[..., :dv_out] if dv_out is not None else res
+        return out, lse_l, probs_l
+    return out
 
 
 def flash_attn_varlen_qkvpacked_func(qkv, cu_seqlens, max_seqlen, dropout_p=0.0,

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define FABLE_ATTN_ABI_VERSION 1
+#define FABLE_ATTN_ABI_VERSION 2
 
 /* dtype codes, same values as the reference (fa_forward.hip:403, backward.hip:25) */
 enum { FA_F16 = 0, FA_BF16 = 1, FA_F32 = 2 };
@@ -118,6 +118,18 @@ typedef struct BwdParams {
   int32_t dropout;
   uint64_t drop_seed;
   float dropout_p, keep_scale;
+  /* Packed variable-length sequences (cu_q != NULL; the reference has no native varlen
+   * backward and loops over sequences in Python, flash_attn_interface.py:523-540). Rows of
+   * sequence b start at row cu_q[b] of the packed [total_q, H, D] Q, O, dO, dQ and at row
+   * cu_k[b] of K, V, dK, dV (set the b strides to 0); B is the number of sequences, SQ/SK the
+   * longest lengths (they size the grid); seqused_q/k, when set, cut a sequence short.
+   * lse/dsum element (b, h, q) sits at b*lse_sb + h*lse_sh + (cu_q ? cu_q[b] : 0) + q; with
+   * cu_q == NULL and both strides 0 the dense [B,Hq,SQ] layout is assumed. */
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const int32_t* seqused_q;
+  const int32_t* seqused_k;
+  int64_t lse_sb, lse_sh;
 } BwdParams;
 
 /* Paged-KV decode parameters. Reference: fa_iface.h:42-63 / fa_decode.hip:13-35.

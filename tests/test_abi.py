@@ -56,7 +56,7 @@ def test_library_exports_every_declared_function():
     assert set(declared) == set(_lib.EXPORTS), declared
     for f in declared:
         assert hasattr(lib, f), f
-    assert lib.fable_attn_abi_version() == 1
+    assert lib.fable_attn_abi_version() == _lib.ABI_VERSION == 2
     for k, st in _lib.STRUCTS.items():
         assert lib.fable_attn_struct_size(k) == ctypes.sizeof(st)
 

@@ -37,10 +37,17 @@ class FakeC:
         return torch.ones_like(q), torch.ones_like(k), torch.ones_like(v)
 
     def fwd_varlen(self, q, k, v, cu_q, cu_k, mq, mk, scale, causal, wl, wr, sc, al, dp, seed, chunk,
-                   uq, uk):
+                   uq, uk, return_lse=False):
         self.calls.append(("fwd_varlen", dict(shape=tuple(q.shape), mq=mq, mk=mk, scale=scale,
-                                              causal=causal, wl=wl, wr=wr)))
-        return torch.zeros_like(q)
+                                              causal=causal, wl=wl, wr=wr, return_lse=return_lse)))
+        out = torch.zeros_like(q)
+        return (out, torch.zeros((q.shape[1], q.shape[0]))) if return_lse else out
+
+    def bwd_varlen(self, dout, q, k, v, out, lse, cu_q, cu_k, mq, mk, scale, causal, wl, wr, sc, al,
+                   dp, seed, uq=None, uk=None):
+        self.calls.append(("bwd_varlen", dict(shape=tuple(q.shape), kshape=tuple(k.shape), mq=mq,
+                                              mk=mk, causal=causal, lse=tuple(lse.shape))))
+        return torch.full_like(q, 2.0), torch.full_like(k, 3.0), torch.full_like(v, 4.0)
 
     def dec(self, q, kc, vc, bt, seqlens, nk, nv, cos, sin, inter, scale, window, num_splits,
             lp=None, return_lse=False, softcap=0.0, alibi=None, rdim=0, rpos=None):
@@ -159,6 +166,40 @@ def test_varlen_no_grad_single_launch(fake):
     fai.flash_attn_varlen_func(q, q, q, cu, cu, 7, 7, causal=True, window_size=(3, -1))
     name, a = fake.calls[-1]
     assert name == "fwd_varlen" and a["mq"] == 7 and a["causal"] == 1 and a["wl"] == 3 and a["wr"] == 0
+
+
+def test_varlen_grad_is_one_native_call_each_way(fake):
+    """With grad, varlen runs one forward (with LSE) and one backward over all sequences; the
+    reference differentiated a per-sequence Python loop (flash_attn_interface.py:523-540)."""
+    cu = torch.tensor([0, 5, 12, 20], dtype=torch.int32)
+    q = rnd(20, 4, 64).requires_grad_()
+    k = rnd(20, 2, 64).requires_grad_()
+    v = rnd(20, 2, 64).requires_grad_()
+    out = fai.flash_attn_varlen_func(q, k, v, cu, cu, 8, 8, causal=True)
+    assert [c[0] for c in fake.calls] == ["fwd_varlen"] and fake.calls[0][1]["return_lse"]
+    out.sum().backward()
+    assert [c[0] for c in fake.calls] == ["fwd_varlen", "bwd_varlen"]
+    a = fake.calls[1][1]
+    assert a["shape"] == (20, 4, 64) and a["kshape"] == (20, 2, 64) and a["lse"] == (4, 20)
+    assert a["causal"] is True and a["mq"] == 8
+    assert torch.all(q.grad == 2) and torch.all(k.grad == 3) and torch.all(v.grad == 4)
+
+
+def test_varlen_grad_padded_head_dim(fake):
+    cu = torch.tensor([0, 6, 10], dtype=torch.int32)
+    q, k, v = (rnd(10, 2, 80).requires_grad_() for _ in range(3))
+    out = fai.flash_attn_varlen_func(q, k, v, cu, cu, 6, 6)
+    assert out.shape == (10, 2, 80) and fake.calls[0][1]["shape"] == (10, 2, 128)
+    out.sum().backward()
+    assert q.grad.shape == (10, 2, 80) and torch.all(q.grad == 2)
+
+
+def test_varlen_chunk_backward_rejected(fake):
+    cu = torch.tensor([0, 8], dtype=torch.int32)
+    q, k, v = (rnd(8, 2, 64).requires_grad_() for _ in range(3))
+    out = fai.flash_attn_varlen_func(q, k, v, cu, cu, 8, 8, attention_chunk=4)
+    with pytest.raises(NotImplementedError, match="attention_chunk"):
+        out.sum().backward()
 
 
 def test_kvcache_mapping(fake):
