@@ -20,6 +20,11 @@ from .flash_attn_interface import (
     flash_attn_with_kvcache,
 )
 
+from . import torch_op
+
+# torch.ops.fable_attn.forward, as the reference registers at import (__init__.py:23,29)
+torch_op.register()
+
 __all__ = [
     "flash_attn_func", "flash_attn_qkvpacked_func", "flash_attn_kvpacked_func",
     "flash_attn_varlen_func", "flash_attn_varlen_qkvpacked_func",

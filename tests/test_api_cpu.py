@@ -259,3 +259,16 @@ def test_install_as_flash_attn_names():
 def test_combine_argument_checks():
     with pytest.raises(RuntimeError):
         fai.flash_attn_combine(rnd(2, 1, 4, 2, 64), torch.zeros(2, 1, 2, 4))   # CPU tensors
+
+
+def test_torch_op_registered_and_falls_back_to_empty():
+    """torch.ops.fable_attn.forward exists after import (reference torch_op.py:51-71) and answers
+    shapes it cannot serve with an empty tensor, never an exception (:27-48)."""
+    from fable_attn import torch_op
+    assert torch_op.REGISTERED and torch_op.LAST_ERROR is None
+    assert hasattr(torch.ops.fable_attn, "forward")
+    assert torch_op.register()   # idempotent
+    q = rnd(1, 2, 8, 64)
+    assert torch_op._forward(q, q, q, 0.125, True).numel() == 0                  # CPU tensor
+    assert torch_op._forward(q.float(), q.float(), q.float(), 0.125, True).numel() == 0
+    assert torch_op._forward(q[0], q[0], q[0], 0.125, False).numel() == 0        # 3-D
