@@ -86,6 +86,34 @@ __device__ __forceinline__ float tanh_exp(float y) {
   return 1.0f - 2.0f * __builtin_amdgcn_rcpf(e + 1.0f);
 }
 
+// Philox4x32-10 (Salmon, Moraes, Dror, Shaw, "Parallel random numbers: as easy as 1, 2, 3",
+// SC 2011): word 0 after ten rounds on the counter (idx, 0, 0) under the key `seed`. The
+// reference draws its dropout stream this way (kernels/fa_common.hpp:71-82).
+__device__ __forceinline__ uint32_t philox_w0(uint64_t seed, uint64_t idx) {
+  uint32_t k0 = (uint32_t)seed, k1 = (uint32_t)(seed >> 32);
+  uint32_t c0 = (uint32_t)idx, c1 = (uint32_t)(idx >> 32), c2 = 0u, c3 = 0u;
+#pragma unroll
+  for (int r = 0; r < 10; r++) {
+    const uint32_t hi0 = __umulhi(0xD2511F53u, c0), lo0 = 0xD2511F53u * c0;
+    const uint32_t hi1 = __umulhi(0xCD9E8D57u, c2), lo1 = 0xCD9E8D57u * c2;
+    c0 = hi1 ^ c1 ^ k0;
+    c1 = lo1;
+    c2 = hi0 ^ c3 ^ k1;
+    c3 = lo0;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  return c0;
+}
+
+// Dropout multiplier of one score: keep_scale (= 1/(1-p)) when (word0 >> 8) * 2^-24 >= p,
+// otherwise 0; idx = (h*SQ + q)*SK + key with no batch term (fa_common.hpp:84-88,
+// fa_forward.hip:255-259).
+__device__ __forceinline__ float dropout_z(uint64_t seed, uint64_t idx, float p, float keep_scale) {
+  const float u = (float)(philox_w0(seed, idx) >> 8) * (1.0f / 16777216.0f);
+  return u >= p ? keep_scale : 0.0f;
+}
+
 // Reductions across lanes l and l^32 (the two halves of one MFMA 32x32 C column) with
 // v_permlane32_swap. Swapping a register with itself leaves, in every lane, the pair
 // {x[l], x[l^32]} spread over the two results, so a symmetric op over both results is the

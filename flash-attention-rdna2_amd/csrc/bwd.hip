@@ -134,7 +134,7 @@ struct BwdQCfg {
   static_assert(KCH % HALF == 0, "loader split");
 };
 
-template <typename T, class C, bool CAUSAL, bool FEAT>
+template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
 bwd_dq_kernel(BwdParams p, int nqt) {
@@ -268,7 +268,10 @@ bwd_dq_kernel(BwdParams p, int nqt) {
           const float x = bwd_logit2<FEAT>(p, s[jb][r], c_log2, slope, qi, key, deriv);
           float pr = exp2_fast(x - lse2);
           if (edge && !visible_b<CAUSAL, FEAT>(p, qi, key, delta, SQ, SK)) pr = 0.0f;
-          s[jb][r] = pr * (dp[jb][r] - Di) * deriv;  // dS^T
+          const float z = DROP ? dropout_z(p.drop_seed, ((uint64_t)h * SQ + qi) * SK + key,
+                                                          p.dropout_p, p.keep_scale)
+                                              : 1.0f;
+          s[jb][r] = pr * (z * dp[jb][r] - Di) * deriv;  // dS^T (backward.hip:170-176)
         }
       V8 pb[C::NG];
 #pragma unroll
@@ -335,7 +338,7 @@ struct BwdKVCfg {
   static constexpr int PER = (CH + NT - 1) / NT;
 };
 
-template <typename T, class C, bool CAUSAL, bool FEAT>
+template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
 bwd_dkdv_kernel(BwdParams p, int nkt) {
@@ -468,8 +471,11 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
           const float x = bwd_logit2<FEAT>(p, s[r], c_log2, slope, q, key, deriv);
           float pr = exp2_fast(x - l4[c]);
           if (edge && !visible_b<CAUSAL, FEAT>(p, q, key, delta, SQ, SK)) pr = 0.0f;
-          const float dsv = pr * (dp[r] - d4[c]) * deriv;
-          pP[r >> 3][r & 7] = (T)pr;
+          const float z = DROP ? dropout_z(p.drop_seed, ((uint64_t)h * SQ + q) * SK + key,
+                                                          p.dropout_p, p.keep_scale)
+                                              : 1.0f;
+          const float dsv = pr * (z * dp[r] - d4[c]) * deriv;
+          pP[r >> 3][r & 7] = (T)(z * pr);
           pS[r >> 3][r & 7] = (T)dsv;
         }
       }
@@ -551,7 +557,7 @@ struct BwdKVPCfg {
   static_assert(CH % NT == 0 && (BQ * DCH) % NT == 0, "loader split");
 };
 
-template <typename T, class C, bool CAUSAL, bool FEAT>
+template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
 bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
@@ -721,8 +727,12 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
             const float x = bwd_logit2<FEAT>(p, sv[r], c_log2, slope, q, key, deriv);
             float pr = exp2_fast(x - l4[c]);
             if (edge && !visible_b<CAUSAL, FEAT>(p, q, key, delta, SQ, SK)) pr = 0.0f;
-            pP[r >> 3][r & 7] = (T)pr;
-            pd4[c] = pr * deriv;
+            const float z = DROP ? dropout_z(p.drop_seed, ((uint64_t)(kvh * p.gqa + hg) * SQ + q) * SK + key,
+                                                            p.dropout_p, p.keep_scale)
+                                                : 1.0f;
+            pP[r >> 3][r & 7] = (T)(z * pr);
+            // p * deriv >= 0; a dropped score hands it over negated, so the dP-wave knows z
+            pd4[c] = z == 0.0f ? -(pr * deriv) : pr * deriv;
           }
           pdx[it & 1][pair][rq][lane] = pd4;
         }
@@ -742,7 +752,12 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
 #pragma unroll
           for (int c = 0; c < 4; c++) {
             const int r = 4 * rq + c;
-            pS[r >> 3][r & 7] = (T)(pd4[c] * (dpv[r] - d4[c]));
+            if constexpr (DROP) {  // dS = p (z dP - D) deriv (backward.hip:170-176)
+              const float z = pd4[c] < 0.0f ? 0.0f : p.keep_scale;
+              pS[r >> 3][r & 7] = (T)(fabsf(pd4[c]) * (z * dpv[r] - d4[c]));
+            } else {
+              pS[r >> 3][r & 7] = (T)(pd4[c] * (dpv[r] - d4[c]));
+            }
           }
         }
         tprod(qs, pS);  // dK^T += Q^T . dS
@@ -773,7 +788,7 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   }
 }
 
-template <typename T, class CQ, class CKV, bool CAUSAL, bool FEAT>
+template <typename T, class CQ, class CKV, bool CAUSAL, bool FEAT, bool DROP = false>
 static int launch_bwd2(const BwdParams& p, hipStream_t st) {
   const int nqt = (p.SQ + CQ::BQ - 1) / CQ::BQ;
   const int nkt = (p.SK + CKV::BK - 1) / CKV::BK;
@@ -781,14 +796,14 @@ static int launch_bwd2(const BwdParams& p, hipStream_t st) {
   const long long gkv = (long long)nkt * p.Hk * p.B * CKV::DSPLIT;
   if (gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_backward_launch: grid too large");
   if (gq > 0) {
-    hipLaunchKernelGGL((bwd_dq_kernel<T, CQ, CAUSAL, FEAT>), dim3((unsigned)gq), dim3(CQ::NT), 0, st, p, nqt);
+    hipLaunchKernelGGL((bwd_dq_kernel<T, CQ, CAUSAL, FEAT, DROP>), dim3((unsigned)gq), dim3(CQ::NT), 0, st, p, nqt);
     if (int rc = launch_status("fable_attn_backward_launch (dq)")) return rc;
   }
   if (gkv > 0) {
     if constexpr (CKV::PAIR)
-      hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
+      hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
     else
-      hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
+      hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
     if (int rc = launch_status("fable_attn_backward_launch (dkdv)")) return rc;
   }
   return FA_OK;
@@ -798,6 +813,9 @@ template <typename T, class CQ, class CKV>
 static int launch_bwd(const BwdParams& p, hipStream_t st) {
   const bool feat = p.softcap > 0.0f || p.alibi != nullptr || p.win_left >= 0 ||
                     (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
+  // dropout has kernels of its own (the Philox rounds cost the other features no registers)
+  if (p.dropout)
+    return p.causal ? launch_bwd2<T, CQ, CKV, true, true, true>(p, st) : launch_bwd2<T, CQ, CKV, false, true, true>(p, st);
   if (p.causal)
     return feat ? launch_bwd2<T, CQ, CKV, true, true>(p, st) : launch_bwd2<T, CQ, CKV, true, false>(p, st);
   return feat ? launch_bwd2<T, CQ, CKV, false, true>(p, st) : launch_bwd2<T, CQ, CKV, false, false>(p, st);
@@ -821,7 +839,8 @@ extern "C" int fable_attn_backward_launch(BwdParams p, int dtype, void* stream) 
     return fail(FA_ERR_ARG, "fable_attn_backward_launch: null pointer");
   if (p.Hq <= 0 || p.Hk <= 0 || p.Hq % p.Hk || p.gqa != p.Hq / p.Hk)
     return fail(FA_ERR_ARG, "fable_attn_backward_launch: Hq=%d Hk=%d gqa=%d", p.Hq, p.Hk, p.gqa);
-  if (p.dropout) return fail(FA_ERR_UNSUPPORTED, "fable_attn_backward_launch: dropout is not implemented");
+  if (p.dropout && !(p.dropout_p >= 0.0f && p.dropout_p < 1.0f))
+    return fail(FA_ERR_ARG, "fable_attn_backward_launch: dropout_p=%g", p.dropout_p);
   if ((p.cu_q == nullptr) != (p.cu_k == nullptr))
     return fail(FA_ERR_ARG, "fable_attn_backward_launch: cu_q and cu_k go together");
   if (p.B <= 0 || p.SQ < 0 || p.SK < 0) return FA_OK;  // empty ranges write zero gradients

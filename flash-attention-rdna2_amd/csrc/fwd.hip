@@ -85,7 +85,7 @@ __device__ __forceinline__ void key_range(const FwdParams& p, int r0, int r1, in
   }
 }
 
-template <typename T, class C, bool CAUSAL, bool FEAT>
+template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
 fwd_kernel(FwdParams p, int nqt) {
@@ -269,6 +269,8 @@ fwd_kernel(FwdParams p, int nqt) {
   const float kcap = p.softcap > 0.0f ? 2.0f * kLog2e * p.scale / p.softcap : 0.0f;
   const float lcap = p.softcap * kLog2e;
   const float aslope2 = aslope * kLog2e;
+  // dropout: probabilities are scaled after the row sum, O = sum z p V / sum p
+  const float keep_scale = DROP ? 1.0f / (1.0f - p.dropout_p) : 1.0f;
   auto softmax = [&](auto masked, auto cap, int i, f32x16 (&s)[C::NB], int kb, V8 (&pb)[C::NG], bool& resc) {
     const int qi = qw + 32 * i + l32;
     const int kq = kb + 4 * hh;  // key of s[jb][r] = kq + 32*jb + 8*(r/4) + (r%4)
@@ -324,8 +326,9 @@ fwd_kernel(FwdParams p, int nqt) {
     resc = __builtin_amdgcn_ballot_w64(need) != 0;
     const float m_use = m_run[i] == -INFINITY ? 0.0f : m_run[i];
     // fp16 sums the rounded probabilities pairwise (their rounding moves the row sum by at most
-    // 2^-12 relative); bf16 rounding is 8x coarser, so it sums the fp32 values
-    constexpr bool kPairSum = std::is_same<T, _Float16>::value;
+    // 2^-12 relative); bf16 rounding is 8x coarser, so it sums the fp32 values, and so does
+    // dropout, which scales the probabilities after the sum
+    constexpr bool kPairSum = std::is_same<T, _Float16>::value && !DROP;
     float r0 = 0.0f, r1 = 0.0f;
 #pragma unroll
     for (int jb = 0; jb < C::NB; jb++)
@@ -335,7 +338,12 @@ fwd_kernel(FwdParams p, int nqt) {
         for (int e = 0; e < 8; e++) {
           const float x = s[jb][8 * sh + e];
           const float pe = FEAT ? exp2_fast(x - m_use) : exp2_fast(fmaf(x, c_log2, -m_use));
-          pb[2 * jb + sh][e] = (T)pe;
+          float pz = pe;
+          if constexpr (DROP) {
+            const int r = 8 * sh + e, key = kq + 32 * jb + 8 * (r >> 2) + (r & 3);
+            pz *= dropout_z(p.philox_seed, ((uint64_t)h * SQ + qi) * SK + key, p.dropout_p, keep_scale);
+          }
+          pb[2 * jb + sh][e] = (T)pz;
           if (!kPairSum) (e & 1 ? r1 : r0) += pe;
         }
     if (kPairSum) {
@@ -492,10 +500,12 @@ fwd_kernel(FwdParams p, int nqt) {
 }
 
 // C runs the plain masks (causal / sequence end), CF the feature kernels (window, chunk,
-// softcap, alibi), whose extra per-score work needs a different register balance
+// softcap, alibi, dropout), whose extra per-score work needs a different register balance.
+// Dropout has kernels of its own, so its Philox rounds cost the other features no registers.
 template <typename T, class C, class CF = C>
 static int launch_fwd(const FwdParams& p, hipStream_t st) {
-  const bool feat = p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
+  const bool drop = p.dropout_p > 0.0f;
+  const bool feat = drop || p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
                     p.win_left >= 0 || (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
   const int br = feat ? CF::BR : C::BR;
   const int nqt = (p.SQ + br - 1) / br;
@@ -504,12 +514,16 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
   if (nblk > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fa_forward_launch: grid too large");
   dim3 grid((unsigned)nblk);
   if (p.causal) {
-    if (feat)
+    if (drop)
+      hipLaunchKernelGGL((fwd_kernel<T, CF, true, true, true>), grid, dim3(CF::NT), 0, st, p, nqt);
+    else if (feat)
       hipLaunchKernelGGL((fwd_kernel<T, CF, true, true>), grid, dim3(CF::NT), 0, st, p, nqt);
     else
       hipLaunchKernelGGL((fwd_kernel<T, C, true, false>), grid, dim3(C::NT), 0, st, p, nqt);
   } else {
-    if (feat)
+    if (drop)
+      hipLaunchKernelGGL((fwd_kernel<T, CF, false, true, true>), grid, dim3(CF::NT), 0, st, p, nqt);
+    else if (feat)
       hipLaunchKernelGGL((fwd_kernel<T, CF, false, true>), grid, dim3(CF::NT), 0, st, p, nqt);
     else
       hipLaunchKernelGGL((fwd_kernel<T, C, false, false>), grid, dim3(C::NT), 0, st, p, nqt);
@@ -533,7 +547,7 @@ extern "C" int fa_forward_launch(FwdParams p, int dtype, void* stream) {
   using namespace fa;
   if (!p.Q || !p.K || !p.V || !p.O) return fail(FA_ERR_ARG, "fa_forward_launch: null tensor pointer");
   if (p.NH <= 0 || p.gqa <= 0 || p.NH % p.gqa) return fail(FA_ERR_ARG, "fa_forward_launch: NH=%d gqa=%d", p.NH, p.gqa);
-  if (p.dropout_p > 0.0f) return fail(FA_ERR_UNSUPPORTED, "fa_forward_launch: dropout is not implemented");
+  if (!(p.dropout_p >= 0.0f && p.dropout_p < 1.0f)) return fail(FA_ERR_ARG, "fa_forward_launch: dropout_p=%g", p.dropout_p);
   if ((p.cu_q == nullptr) != (p.cu_k == nullptr)) return fail(FA_ERR_ARG, "fa_forward_launch: cu_q and cu_k go together");
   if (!p.cu_q && p.batch <= 0) return FA_OK;
   hipStream_t st = (hipStream_t)stream;

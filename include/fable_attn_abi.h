@@ -84,6 +84,9 @@ typedef struct FwdParams {
   int32_t win_left, win_right;
   const float* alibi_slopes;
   int32_t causal;
+  /* dropout: Philox4x32-10 word 0 on (idx, 0, 0) under key philox_seed, idx = (h*SQ + q)*SK + key
+   * (per-sequence SQ/SK for varlen); kept iff (word0 >> 8) * 2^-24 >= dropout_p, scaled by
+   * 1/(1-dropout_p) after the row sum (fa_common.hpp:71-88, fa_forward.hip:255-259) */
   float dropout_p;
   uint64_t philox_seed;
   const int32_t* cu_q;
@@ -115,7 +118,7 @@ typedef struct BwdParams {
   float scale, softcap;
   const float* alibi;
   int32_t causal, win_left, win_right;
-  int32_t dropout;
+  int32_t dropout; /* the forward's stream: drop_seed = its philox_seed, keep_scale = 1/(1-p) */
   uint64_t drop_seed;
   float dropout_p, keep_scale;
   /* Packed variable-length sequences (cu_q != NULL; the reference has no native varlen

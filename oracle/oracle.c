@@ -11,8 +11,14 @@
  *                   a row with no visible key gives O = 0 and LSE = -inf.
  *                   Batch/GQA indexing as kernels/fa_forward_gate.inc:33-47.
  *   oracle_bwd      kernels/backward.hip:566-597 (fp64 backward of the gate): recompute P from
- *                   the exact forward, Di = sum(O*dO), dS = P*(dP - Di)*softcap'(.), dQ,dK,dV.
- *                   Dropout is not restated (the kernels here do not implement it).
+ *                   the exact forward, Di = sum(O*dO), dS = P*(z*dP - Di)*softcap'(.), dQ,dK,dV
+ *                   with dropout multiplier z (1 when dropout_p == 0).
+ *   dropout         kernels/fa_common.hpp:71-88: Philox4x32-10 (Salmon, Moraes, Dror, Shaw,
+ *                   "Parallel random numbers: as easy as 1, 2, 3", SC 2011) on counter
+ *                   (idx, 0, 0) and key = seed; u = (word0 >> 8) * 2^-24; kept (z = 1/(1-p))
+ *                   iff u >= p; idx = (h*SQ + i)*SK + j with no batch term
+ *                   (fa_forward.hip:255-259, backward.hip:172). The forward normalises with
+ *                   the undropped sum: O = sum_j z_j p_j V_j, LSE unchanged.
  *   oracle_decode   kernels/fa_decode_gate.inc:19-25 (rot_at) and :66-96 (oracle loop): new
  *                   tokens at ctx+tk, causal among new tokens via append, window lo =
  *                   qpos-window+1, leftpad, softcap, alibi slope*(pos-qpos), rotary (neox /
@@ -35,7 +41,50 @@ typedef struct OracleCfg {
   double scale, softcap;
   int win_left, win_right, causal, attn_chunk;
   const float* alibi; /* [H] or NULL */
+  double dropout_p;   /* 0: no dropout */
+  uint64_t seed;
 } OracleCfg;
+
+/* Philox4x32-10: 10 rounds of the published round function with multipliers 0xD2511F53 and
+ * 0xCD9E8D57 and key bumps 0x9E3779B9, 0xBB67AE85 (Salmon et al. 2011, Random123). */
+void oracle_philox4x32_10(const uint32_t ctr[4], const uint32_t key[2], uint32_t out[4]) {
+  uint32_t c0 = ctr[0], c1 = ctr[1], c2 = ctr[2], c3 = ctr[3], k0 = key[0], k1 = key[1];
+  for (int r = 0; r < 10; r++) {
+    const uint64_t p0 = (uint64_t)0xD2511F53u * c0, p1 = (uint64_t)0xCD9E8D57u * c2;
+    const uint32_t n0 = (uint32_t)(p1 >> 32) ^ c1 ^ k0, n1 = (uint32_t)p1;
+    const uint32_t n2 = (uint32_t)(p0 >> 32) ^ c3 ^ k1, n3 = (uint32_t)p0;
+    c0 = n0; c1 = n1; c2 = n2; c3 = n3;
+    k0 += 0x9E3779B9u;
+    k1 += 0xBB67AE85u;
+  }
+  out[0] = c0; out[1] = c1; out[2] = c2; out[3] = c3;
+}
+
+/* dropout multiplier of (h, i, j): 0 or 1/(1-p) — fa_common.hpp:84-88 */
+double oracle_drop_mul(uint64_t seed, uint64_t idx, double p) {
+  const uint32_t ctr[4] = {(uint32_t)idx, (uint32_t)(idx >> 32), 0u, 0u};
+  const uint32_t key[2] = {(uint32_t)seed, (uint32_t)(seed >> 32)};
+  uint32_t out[4];
+  oracle_philox4x32_10(ctr, key, out);
+  const float u = (float)(out[0] >> 8) * (1.0f / 16777216.0f);
+  return u >= (float)p ? 1.0 / (1.0 - p) : 0.0;
+}
+
+/* z[h][i][j] for h < H, i < SQ, j < SK (the dropout multipliers of one sequence) */
+void oracle_dropout_mask(uint64_t seed, double p, int H, int SQ, int SK, double* z) {
+  for (int h = 0; h < H; h++)
+    for (int i = 0; i < SQ; i++)
+      for (int j = 0; j < SK; j++) {
+        const uint64_t idx = ((uint64_t)h * (uint64_t)SQ + (uint64_t)i) * (uint64_t)SK + (uint64_t)j;
+        z[((size_t)h * SQ + i) * SK + j] = oracle_drop_mul(seed, idx, p);
+      }
+}
+
+static double drop_mul(const OracleCfg* c, int h, int i, int j) {
+  if (c->dropout_p <= 0) return 1.0;
+  const uint64_t idx = ((uint64_t)h * (uint64_t)c->SQ + (uint64_t)i) * (uint64_t)c->SK + (uint64_t)j;
+  return oracle_drop_mul(c->seed, idx, c->dropout_p);
+}
 
 /* visibility of key j to query i — fa_common.hpp:111-118 */
 static int visible(const OracleCfg* c, int i, int j) {
@@ -100,6 +149,8 @@ void oracle_fwd(const float* Q, const float* K, const float* V, float* O, float*
           pr[j] = exp(pr[j] - mx);
           sum += pr[j];
         }
+        if (c->dropout_p > 0)
+          for (int j = 0; j < c->SK; j++) pr[j] *= drop_mul(c, h, i, j);  /* after the sum */
         float* o = O + (((size_t)b * c->H + h) * c->SQ + i) * c->D;
         for (int d = 0; d < c->D; d++) {
           double acc = 0.0;
@@ -155,22 +206,24 @@ void oracle_bwd(const float* Q, const float* K, const float* V, const float* dO,
             sum += P[j];
           }
           for (int j = 0; j < c->SK; j++) P[j] /= sum;
-          /* O (exact) and Di = sum_d O*dO — backward.hip:576-579 */
+          /* O (exact, with dropout) and Di = sum_d O*dO — backward.hip:576-579 */
           double Di = 0.0;
           for (int d = 0; d < c->D; d++) {
             double acc = 0.0;
-            for (int j = 0; j < c->SK; j++) acc += P[j] * (double)Vb[(size_t)j * c->D + d];
+            for (int j = 0; j < c->SK; j++)
+              acc += P[j] * drop_mul(c, h, i, j) * (double)Vb[(size_t)j * c->D + d];
             o[d] = acc;
             Di += acc * (double)g[d];
           }
           double* dq = dQ + qo;
           for (int j = 0; j < c->SK; j++) {
             if (P[j] == 0.0 && !visible(c, i, j)) continue;
+            const double z = drop_mul(c, h, i, j);
             double dp = 0.0;
             for (int d = 0; d < c->D; d++) dp += (double)g[d] * (double)Vb[(size_t)j * c->D + d];
-            const double dS = P[j] * (dp - Di) * Dv[j]; /* backward.hip:585 */
+            const double dS = P[j] * (z * dp - Di) * Dv[j]; /* backward.hip:170-176 */
             for (int d = 0; d < c->D; d++) {
-              dVb[(size_t)j * c->D + d] += P[j] * (double)g[d];
+              dVb[(size_t)j * c->D + d] += z * P[j] * (double)g[d];
               dKb[(size_t)j * c->D + d] += c->scale * dS * (double)q[d];
               dq[d] += c->scale * dS * (double)Kb[(size_t)j * c->D + d];
             }

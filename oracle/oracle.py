@@ -2,9 +2,10 @@
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import this module; the
 shipped library never does. It wraps oracle/liboracle.so (oracle.c, a restatement of the
-reference's fp64 oracles) and, when it was built, oracle/_ref/libref.so (the reference's own
-ref_attention compiled from kernels/fa_common.hpp), plus the dtype rounding and the seeded
-input generator the reference's gates use.
+reference's fp64 oracles) and, when they were built, oracle/_ref/libref.so (the reference's own
+ref_attention compiled from kernels/fa_common.hpp) and oracle/_ref/librefdrop.so (the
+reference's host replica of its dropout multiplier, from kernels/backward.hip), plus the dtype
+rounding and the seeded input generator the reference's gates use.
 
 Array layouts follow oracle.c: [B, H, S, D] float32 for the forward/backward,
 [B, nq, H, D] / [nblocks, page, Hk, D] for decode.
@@ -18,6 +19,7 @@ import numpy as np
 _HERE = os.path.dirname(os.path.abspath(__file__))
 _LIB = None
 _REF = None
+_REFDROP = None
 
 
 class OracleCfg(ctypes.Structure):
@@ -26,7 +28,8 @@ class OracleCfg(ctypes.Structure):
                 ("scale", ctypes.c_double), ("softcap", ctypes.c_double),
                 ("win_left", ctypes.c_int), ("win_right", ctypes.c_int),
                 ("causal", ctypes.c_int), ("attn_chunk", ctypes.c_int),
-                ("alibi", ctypes.c_void_p)]
+                ("alibi", ctypes.c_void_p), ("dropout_p", ctypes.c_double),
+                ("seed", ctypes.c_uint64)]
 
 
 class OracleDecCfg(ctypes.Structure):
@@ -130,10 +133,52 @@ def randn(shape, seed, dtype="f16"):
 
 
 # ----------------------------------------------------------------------------- oracles
+def philox4x32_10(ctr, key):
+    """Philox4x32-10 of a 4-word counter and a 2-word key (oracle.c, Salmon et al. 2011)."""
+    c = (ctypes.c_uint32 * 4)(*[int(x) & 0xFFFFFFFF for x in ctr])
+    k = (ctypes.c_uint32 * 2)(*[int(x) & 0xFFFFFFFF for x in key])
+    out = (ctypes.c_uint32 * 4)()
+    lib().oracle_philox4x32_10(c, k, out)
+    return tuple(out)
+
+
+def oracle_drop_mul(seed, idx, p):
+    """One dropout multiplier (oracle.c oracle_drop_mul): 0 or 1/(1-p)."""
+    f = lib().oracle_drop_mul
+    f.restype = ctypes.c_double
+    f.argtypes = [ctypes.c_uint64, ctypes.c_uint64, ctypes.c_double]
+    return f(int(seed) & ((1 << 64) - 1), int(idx), float(p))
+
+
+def keep_mask(seed, p, H, SQ, SK):
+    """Dropout multipliers z[h, i, j] (0 or 1/(1-p)) of the reference's scheme: Philox on
+    idx = (h*SQ + i)*SK + j, key = seed, kept iff (word0 >> 8) * 2^-24 >= p (fa_common.hpp:84-88)."""
+    z = np.zeros((H, SQ, SK))
+    lib().oracle_dropout_mask(ctypes.c_uint64(int(seed) & ((1 << 64) - 1)), ctypes.c_double(p),
+                              H, SQ, SK, _p(z))
+    return z
+
+
+def ref_drop_lib():
+    """The reference's host replica of its dropout multiplier (hdrop), or None when
+    oracle/_ref/librefdrop.so was not built (e.g. on a GPU box)."""
+    global _REFDROP
+    if _REFDROP is None:
+        path = os.path.join(_HERE, "_ref", "librefdrop.so")
+        if not os.path.exists(path):
+            return None
+        _REFDROP = ctypes.CDLL(path)
+        _REFDROP.ref_drop_mul.restype = ctypes.c_float
+        _REFDROP.ref_drop_mul.argtypes = [ctypes.c_ulonglong, ctypes.c_ulonglong, ctypes.c_float,
+                                          ctypes.c_float]
+    return _REFDROP
+
+
 def fwd(q, k, v, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0, alibi=None,
-        chunk=0, rows=None, want_lse=True):
+        chunk=0, rows=None, want_lse=True, dropout_p=0.0, seed=0):
     """fp64 forward oracle. q [B,H,SQ,D], k/v [B,Hk,SK,D] float32 (already dtype-rounded).
-    rows: optional list of query indices to evaluate (others stay 0 / -inf)."""
+    rows: optional list of query indices to evaluate (others stay 0 / -inf). dropout_p > 0
+    applies the reference's Philox dropout with `seed`."""
     q, k, v = _f32(q), _f32(k), _f32(v)
     B, H, SQ, D = q.shape
     Hk, SK = k.shape[1], k.shape[2]
@@ -142,7 +187,8 @@ def fwd(q, k, v, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0, al
     al = _f32(alibi) if alibi is not None else None
     cfg = OracleCfg(B, H, Hk, SQ, SK, D, _f32s(scale), _f32s(softcap), int(win_left),
                     int(win_right), int(bool(causal)), int(chunk),
-                    al.ctypes.data if al is not None else None)
+                    al.ctypes.data if al is not None else None, _f32s(dropout_p),
+                    int(seed) & ((1 << 64) - 1))
     r = np.ascontiguousarray(rows, dtype=np.int32) if rows is not None else None
     lib().oracle_fwd(_p(q), _p(k), _p(v), _p(o), _p(lse), ctypes.byref(cfg), _p(r),
                      ctypes.c_int(len(r) if r is not None else 0))
@@ -150,7 +196,7 @@ def fwd(q, k, v, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0, al
 
 
 def bwd(q, k, v, do, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0, alibi=None,
-        chunk=0):
+        chunk=0, dropout_p=0.0, seed=0):
     """fp64 backward oracle: returns (dq, dk, dv) float64 with the layouts of q, k, v."""
     q, k, v, do = _f32(q), _f32(k), _f32(v), _f32(do)
     B, H, SQ, D = q.shape
@@ -161,7 +207,8 @@ def bwd(q, k, v, do, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0
     al = _f32(alibi) if alibi is not None else None
     cfg = OracleCfg(B, H, Hk, SQ, SK, D, _f32s(scale), _f32s(softcap), int(win_left),
                     int(win_right), int(bool(causal)), int(chunk),
-                    al.ctypes.data if al is not None else None)
+                    al.ctypes.data if al is not None else None, _f32s(dropout_p),
+                    int(seed) & ((1 << 64) - 1))
     lib().oracle_bwd(_p(q), _p(k), _p(v), _p(do), _p(dq), _p(dk), _p(dv), ctypes.byref(cfg))
     return dq, dk, dv
 

@@ -73,8 +73,9 @@ def test_launchers_validate_before_device_work():
     assert b"head_dim=72" in lib.fable_attn_last_error()
     p.HD = 64
     assert lib.fa_forward_launch(p, 7, None) == 1          # unknown dtype
-    p.dropout_p = 0.1
-    assert lib.fa_forward_launch(p, 0, None) == 4          # dropout not implemented
+    p.dropout_p = 1.0                                      # keeps nothing: rejected
+    assert lib.fa_forward_launch(p, 0, None) == 3
+    assert b"dropout_p" in lib.fable_attn_last_error()
     c = _lib.CombineParams()
     assert lib.fa_combine_launch(c, None) == 3
 

@@ -11,7 +11,11 @@ The oracle is trusted only after these checks:
     windows;
   * decode: the forward oracle on gathered pages (no append, append, window, leftpad, nq > 1),
     rotary against a complex-multiplication rotation, invariance under page permutation;
-  * combine: merging two key halves equals attention over all keys.
+  * combine: merging two key halves equals attention over all keys;
+  * dropout: Philox4x32-10 against the Random123 known-answer vectors, the keep mask against
+    the reference's own host replica of its dropout multiplier (oracle/_ref, compiled from
+    kernels/backward.hip) where that is built, the keep rate, a one-hot V that reads the mask
+    back out of the forward, and finite differences of the dropout backward under a fixed mask.
 """
 import math
 import os
@@ -138,9 +142,9 @@ def test_softcap_limit():
     assert np.abs(o1 - o2).max() < 1e-5 and np.abs(l1 - l2).max() < 1e-5
 
 
-def _np_attention(q, k, v, scale, causal, wl=-1, wr=-1, softcap=0.0):
+def _np_attention(q, k, v, scale, causal, wl=-1, wr=-1, softcap=0.0, z=None):
     """fp64 numpy attention (a textbook softmax(QK^T)V with the mask contract), for finite
-    differences only."""
+    differences only. z [H, SQ, SK]: fixed multipliers applied to the probabilities (dropout)."""
     H, Hk = q.shape[1], k.shape[1]
     k = np.repeat(k, H // Hk, axis=1).astype(np.float64)
     v = np.repeat(v, H // Hk, axis=1).astype(np.float64)
@@ -162,6 +166,8 @@ def _np_attention(q, k, v, scale, causal, wl=-1, wr=-1, softcap=0.0):
     mx = s.max(-1, keepdims=True)
     p = np.exp(s - mx)
     p /= p.sum(-1, keepdims=True)
+    if z is not None:
+        p = p * z[None]
     return np.einsum("bhij,bhjd->bhid", p, v)
 
 
@@ -358,3 +364,90 @@ def test_c_rounding_matches_numpy():
         orc.lib().oracle_round(x.ctypes.data_as(ctypes.c_void_p), y.ctypes.data_as(ctypes.c_void_p),
                                ctypes.c_size_t(x.size), mode)
         assert np.array_equal(y, ref), mode
+
+
+# ----------------------------------------------------------------------------- dropout
+# Random123's published known-answer vectors for philox4x32_10 (kat_vectors): counter, key,
+# expected output words.
+PHILOX_KAT = [
+    ((0, 0, 0, 0), (0, 0), (0x6627E8D5, 0xE169C58D, 0xBC57AC4C, 0x9B00DBD8)),
+    ((0xFFFFFFFF,) * 4, (0xFFFFFFFF,) * 2, (0x408F276D, 0x41C83B0E, 0xA20BC7C6, 0x6D5451FD)),
+    ((0x243F6A88, 0x85A308D3, 0x13198A2E, 0x03707344), (0xA4093822, 0x299F31D0),
+     (0xD16CFE09, 0x94FDCCEB, 0x5001E420, 0x24126EA1)),
+]
+
+
+@pytest.mark.parametrize("ctr,key,want", PHILOX_KAT)
+def test_philox_known_answers(ctr, key, want):
+    assert orc.philox4x32_10(ctr, key) == want
+
+
+@pytest.mark.skipif(orc.ref_drop_lib() is None, reason="oracle/_ref not built (reference tree absent)")
+def test_dropout_mask_matches_reference_replica():
+    """Every multiplier equals the reference's hdrop (kernels/backward.hip:530-537) bit for bit,
+    over seeds that use both key words and indices past 2^32 (both counter words)."""
+    ref = orc.ref_drop_lib()
+    for seed in (0, 777, (1 << 63) - 1, 0x123456789ABCDEF0):
+        for p in (0.1, 0.2, 0.5, 0.9):
+            H, SQ, SK = 3, 7, 41
+            z = orc.keep_mask(seed, p, H, SQ, SK)
+            pf = float(np.float32(p))
+            ks = float(np.float32(1.0) / (np.float32(1.0) - np.float32(pf)))
+            want = np.array([ref.ref_drop_mul(seed, i, pf, ks) for i in range(H * SQ * SK)])
+            assert np.array_equal(z.reshape(-1) > 0, want > 0), (seed, p)
+            assert np.allclose(z.reshape(-1)[want > 0], ks, rtol=1e-6)
+        for base in (1 << 32, (1 << 40) + 12345):  # idx high word in play
+            for i in range(base - 20, base + 20):
+                assert (orc.oracle_drop_mul(seed, i, 0.3) > 0) == (ref.ref_drop_mul(seed, i, 0.3, 1.0) > 0)
+
+
+def test_dropout_keep_rate():
+    for p in (0.1, 0.5):
+        z = orc.keep_mask(11, p, 4, 64, 256)
+        n = z.size
+        kept = (z > 0).mean()
+        assert abs(kept - (1 - p)) <= 5 * math.sqrt(p * (1 - p) / n)
+        assert np.allclose(z[z > 0], 1.0 / (1.0 - np.float32(p)))
+
+
+def test_dropout_forward_reads_back_the_mask():
+    """V = identity (one-hot rows): O[b,h,i,j] = z[h,i,j] * P[b,h,i,j] with P the undropped
+    softmax, so the forward with dropout returns the mask times the probabilities; the
+    multiplier has no batch term (both batches see the same mask); the row sum (and LSE) is
+    that of the undropped probabilities."""
+    B, H, SQ, SK = 2, 3, 9, 16
+    rng = np.random.default_rng(5)
+    q = rng.standard_normal((B, H, SQ, SK)).astype(np.float32)
+    k = rng.standard_normal((B, H, SK, SK)).astype(np.float32)
+    v = np.broadcast_to(np.eye(SK, dtype=np.float32), (B, H, SK, SK)).copy()
+    seed, p = 99, 0.3
+    o, lse = orc.fwd(q, k, v, 0.25, False, dropout_p=p, seed=seed)
+    o0, lse0 = orc.fwd(q, k, v, 0.25, False)
+    z = orc.keep_mask(seed, float(np.float32(p)), H, SQ, SK)
+    assert np.allclose(o, z[None] * o0, rtol=1e-6, atol=1e-7)
+    assert np.array_equal(lse, lse0)
+    assert ((o == 0) == (z[None] == 0)).all()
+
+
+def test_dropout_backward_finite_differences():
+    B, H, Hk, SQ, SK, D = 1, 4, 2, 7, 12, 8
+    rng = np.random.default_rng(6)
+    q = rng.standard_normal((B, H, SQ, D)).astype(np.float32)
+    k = rng.standard_normal((B, Hk, SK, D)).astype(np.float32)
+    v = rng.standard_normal((B, Hk, SK, D)).astype(np.float32)
+    do = rng.standard_normal((B, H, SQ, D)).astype(np.float32)
+    seed, p, scale = 1234, 0.25, np.float32(0.4)
+    for causal, sc in ((True, 0.0), (False, 4.0)):
+        dq, dk, dv = orc.bwd(q, k, v, do, scale, causal, -1, -1, sc, dropout_p=p, seed=seed)
+        z = orc.keep_mask(seed, p, H, SQ, SK)
+        loss = lambda q_, k_, v_: (_np_attention(q_, k_, v_, float(scale), causal, softcap=sc, z=z) * do).sum()
+        eps = 1e-3
+        base = [a.astype(np.float64) for a in (q, k, v)]
+        for pos, g in enumerate((dq, dk, dv)):
+            for idx in [tuple(rng.integers(0, s_) for s_ in base[pos].shape) for _ in range(8)]:
+                ap = [a.copy() for a in base]
+                am = [a.copy() for a in base]
+                ap[pos][idx] += eps
+                am[pos][idx] -= eps
+                fd = (loss(*ap) - loss(*am)) / (2 * eps)
+                assert abs(fd - g[idx]) <= 1e-5 + 1e-4 * abs(fd), ("qkv"[pos], idx, fd, g[idx])
