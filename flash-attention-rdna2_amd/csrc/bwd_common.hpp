@@ -1,0 +1,91 @@
+// bwd_common.hpp — the backward's mask ranges, logit transform and sequence views, shared by
+// the fp16/bf16 kernels (bwd.hip) and the fp32 kernels (bwd_f32.hip). Mask contract and math of
+// the reference backward (kernels/backward.hip:109-202, BwdParams in include/fable_attn_abi.h).
+#pragma once
+#include "attn_device.hpp"
+
+namespace fa {
+
+template <bool CAUSAL, bool FEAT>
+__device__ __forceinline__ bool visible_b(const BwdParams& p, int q, int key, int delta, int SQ, int SK) {
+  if (key >= SK || q >= SQ) return false;
+  if (CAUSAL && key > q + delta) return false;
+  if (FEAT) {
+    if (p.win_left >= 0 && key < q + delta - p.win_left) return false;
+    if (p.win_right >= 0 && key > q + delta + p.win_right) return false;
+  }
+  return true;
+}
+
+// keys visible to query rows [r0, r1]: [k0, k1)
+template <bool CAUSAL, bool FEAT>
+__device__ __forceinline__ void key_range_b(const BwdParams& p, int r0, int r1, int delta, int SK, int& k0, int& k1) {
+  k0 = 0;
+  k1 = SK;
+  if (CAUSAL) k1 = min(k1, r1 + delta + 1);
+  if (FEAT) {
+    if (p.win_left >= 0) k0 = max(k0, r0 + delta - p.win_left);
+    if (p.win_right >= 0) k1 = min(k1, r1 + delta + p.win_right + 1);
+  }
+}
+
+// queries that see some key in [k0, k1]: [q0, q1)
+template <bool CAUSAL, bool FEAT>
+__device__ __forceinline__ void query_range_b(const BwdParams& p, int k0, int k1, int delta, int SQ, int& q0, int& q1) {
+  q0 = 0;
+  q1 = SQ;
+  if (CAUSAL) q0 = max(q0, k0 - delta);
+  if (FEAT) {
+    if (p.win_right >= 0) q0 = max(q0, k0 - delta - p.win_right);
+    if (p.win_left >= 0) q1 = min(q1, k1 - delta + p.win_left + 1);
+  }
+}
+
+// logit transform of one score: returns log2-domain logit, and d(logit)/d(scale*q.k)
+template <bool FEAT>
+__device__ __forceinline__ float bwd_logit2(const BwdParams& p, float s, float c_log2, float slope, int q,
+                                            int key, float& deriv) {
+  if (!FEAT) {
+    deriv = 1.0f;
+    return s * c_log2;
+  }
+  float x = s * p.scale;
+  deriv = 1.0f;
+  if (p.softcap > 0.0f) {
+    // (the reciprocal is uniform: one division per call site after hoisting, not per score)
+    const float t = tanh_exp(x * (1.0f / p.softcap));
+    x = p.softcap * t;
+    deriv = 1.0f - t * t;
+  }
+  x += slope * (float)(key - q);
+  return x * kLog2e;
+}
+
+// Lengths and first packed rows of sequence b (dense: the whole [SQ, SK] and row 0; varlen:
+// from cu_q/cu_k, cut by seqused). Pointer bases are base + b*str.b + row*str.s + h*str.h, so
+// varlen callers pass b strides of 0; lse/dsum (b, h, q) is at b*lse_sb + h*lse_sh + qo + q.
+struct BwdSeq {
+  int SQ, SK;
+  long long qo, ko;
+};
+__device__ __forceinline__ BwdSeq bwd_seq(const BwdParams& p, int b) {
+  BwdSeq s;
+  if (p.cu_q) {
+    s.qo = p.cu_q[b];
+    s.ko = p.cu_k[b];
+    s.SQ = p.cu_q[b + 1] - p.cu_q[b];
+    s.SK = p.cu_k[b + 1] - p.cu_k[b];
+    if (p.seqused_q) s.SQ = min(s.SQ, p.seqused_q[b]);
+    if (p.seqused_k) s.SK = min(s.SK, p.seqused_k[b]);
+  } else {
+    s.qo = s.ko = 0;
+    s.SQ = p.SQ;
+    s.SK = p.SK;
+  }
+  return s;
+}
+
+// the fp32 backward (bwd_f32.hip), dispatched from fable_attn_backward_launch
+int launch_bwd_f32(const BwdParams& p, hipStream_t st);
+
+}  // namespace fa

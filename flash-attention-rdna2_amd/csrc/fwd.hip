@@ -32,12 +32,10 @@
 #include <type_traits>
 
 #include "attn_device.hpp"
+#include "fwd_common.hpp"
 #include "status.hpp"
 
 namespace fa {
-
-// the running max (log2 units) moves only when a tile exceeds it by more than this
-constexpr float kLazyMax = 8.0f;
 
 template <int HD_, int BC_, int NW_, int WPE_, int QB_ = 1>
 struct FwdCfg {
@@ -61,30 +59,6 @@ struct FwdCfg {
   static_assert(KCH % NT == 0 && NT % DCH == 0, "loader split");
 };
 
-struct SeqView {
-  int SQ, SK;
-  long long q0, k0, v0, o0;  // element offsets of row 0 of this sequence (batch folded in)
-  long long lse0;            // element offset of row 0 in LSE
-};
-
-// visible key range [k0, k1) for query rows [r0, r1] (reference mask contract)
-template <bool CAUSAL, bool FEAT>
-__device__ __forceinline__ void key_range(const FwdParams& p, int r0, int r1, int delta, int SK,
-                                          int& k0, int& k1) {
-  k0 = 0;
-  k1 = SK;
-  if (CAUSAL) k1 = min(k1, r1 + delta + 1);
-  if (FEAT) {
-    if (p.win_left >= 0) k0 = max(k0, r0 + delta - p.win_left);
-    if (p.win_right >= 0) k1 = min(k1, r1 + delta + p.win_right + 1);
-    if (p.attn_chunk > 0) {
-      const int a = max(r0 + delta, 0), b = max(r1 + delta, 0);
-      k0 = max(k0, (a / p.attn_chunk) * p.attn_chunk);
-      k1 = min(k1, (b / p.attn_chunk + 1) * p.attn_chunk);
-    }
-  }
-}
-
 template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
@@ -104,27 +78,7 @@ fwd_kernel(FwdParams p, int nqt) {
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
   const int kvh = h / p.gqa;
 
-  SeqView sv;
-  if (p.cu_q) {
-    const int qs = p.cu_q[z], ks = p.cu_k[z];
-    sv.SQ = p.cu_q[z + 1] - qs;
-    sv.SK = p.cu_k[z + 1] - ks;
-    if (p.seqused_q) sv.SQ = min(sv.SQ, p.seqused_q[z]);
-    if (p.seqused_k) sv.SK = min(sv.SK, p.seqused_k[z]);
-    sv.q0 = (long long)qs * p.sQ.s;
-    sv.k0 = (long long)ks * p.sK.s;
-    sv.v0 = (long long)ks * p.sV.s;
-    sv.o0 = (long long)qs * p.sO.s;
-    sv.lse0 = (long long)h * p.lse_sh + qs;
-  } else {
-    sv.SQ = p.SQ;
-    sv.SK = p.SK;
-    sv.q0 = (long long)z * p.sQ.b;
-    sv.k0 = (long long)z * p.sK.b;
-    sv.v0 = (long long)z * p.sV.b;
-    sv.o0 = (long long)z * p.sO.b;
-    sv.lse0 = (long long)z * p.lse_sb + (long long)h * p.lse_sh;
-  }
+  const SeqView sv = seq_view(p, z, h);
   const int SQ = sv.SQ, SK = sv.SK;
   const int qb = qt * C::BR;
   if (qb >= SQ) return;
@@ -554,6 +508,7 @@ extern "C" int fa_forward_launch(FwdParams p, int dtype, void* stream) {
   switch (dtype) {
     case FA_F16: return dispatch_hd<_Float16>(p, st);
     case FA_BF16: return dispatch_hd<__bf16>(p, st);
-    default: return fail(FA_ERR_DTYPE, "fa_forward_launch: dtype %d not implemented (fp16/bf16)", dtype);
+    case FA_F32: return launch_fwd_f32(p, st);
+    default: return fail(FA_ERR_DTYPE, "fa_forward_launch: dtype %d not implemented (fp16/bf16/fp32)", dtype);
   }
 }

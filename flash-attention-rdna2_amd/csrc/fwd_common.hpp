@@ -1,0 +1,82 @@
+// fwd_common.hpp — the forward's sequence views and mask ranges, shared by the fp16/bf16
+// kernels (fwd.hip) and the fp32 kernels (fwd_f32.hip). Mask contract of the reference
+// (kernels/fa_forward.hip:224-233, FwdParams in include/fable_attn_abi.h).
+#pragma once
+#include "attn_device.hpp"
+
+namespace fa {
+
+// the running max (log2 units) moves only when a tile exceeds it by more than this
+constexpr float kLazyMax = 8.0f;
+
+struct SeqView {
+  int SQ, SK;
+  long long q0, k0, v0, o0;  // element offsets of row 0 of this sequence (batch folded in)
+  long long lse0;            // element offset of row 0 in LSE
+};
+
+// lengths and row-0 offsets of sequence z, head h (dense: batch element z; varlen: packed rows
+// cu_q[z].. / cu_k[z].., cut by seqused)
+__device__ __forceinline__ SeqView seq_view(const FwdParams& p, int z, int h) {
+  SeqView sv;
+  if (p.cu_q) {
+    const int qs = p.cu_q[z], ks = p.cu_k[z];
+    sv.SQ = p.cu_q[z + 1] - qs;
+    sv.SK = p.cu_k[z + 1] - ks;
+    if (p.seqused_q) sv.SQ = min(sv.SQ, p.seqused_q[z]);
+    if (p.seqused_k) sv.SK = min(sv.SK, p.seqused_k[z]);
+    sv.q0 = (long long)qs * p.sQ.s;
+    sv.k0 = (long long)ks * p.sK.s;
+    sv.v0 = (long long)ks * p.sV.s;
+    sv.o0 = (long long)qs * p.sO.s;
+    sv.lse0 = (long long)h * p.lse_sh + qs;
+  } else {
+    sv.SQ = p.SQ;
+    sv.SK = p.SK;
+    sv.q0 = (long long)z * p.sQ.b;
+    sv.k0 = (long long)z * p.sK.b;
+    sv.v0 = (long long)z * p.sV.b;
+    sv.o0 = (long long)z * p.sO.b;
+    sv.lse0 = (long long)z * p.lse_sb + (long long)h * p.lse_sh;
+  }
+  return sv;
+}
+
+// visible key range [k0, k1) for query rows [r0, r1] (reference mask contract)
+template <bool CAUSAL, bool FEAT>
+__device__ __forceinline__ void key_range(const FwdParams& p, int r0, int r1, int delta, int SK,
+                                          int& k0, int& k1) {
+  k0 = 0;
+  k1 = SK;
+  if (CAUSAL) k1 = min(k1, r1 + delta + 1);
+  if (FEAT) {
+    if (p.win_left >= 0) k0 = max(k0, r0 + delta - p.win_left);
+    if (p.win_right >= 0) k1 = min(k1, r1 + delta + p.win_right + 1);
+    if (p.attn_chunk > 0) {
+      const int a = max(r0 + delta, 0), b = max(r1 + delta, 0);
+      k0 = max(k0, (a / p.attn_chunk) * p.attn_chunk);
+      k1 = min(k1, (b / p.attn_chunk + 1) * p.attn_chunk);
+    }
+  }
+}
+
+// key j visible to query i (delta = SK - SQ, bottom-right alignment)
+template <bool CAUSAL, bool FEAT>
+__device__ __forceinline__ bool fwd_visible(const FwdParams& p, int i, int j, int delta, int SK) {
+  bool ok = j < SK;
+  if (CAUSAL) ok = ok && j <= i + delta;
+  if (FEAT) {
+    if (p.win_left >= 0) ok = ok && j >= i + delta - p.win_left;
+    if (p.win_right >= 0) ok = ok && j <= i + delta + p.win_right;
+    if (p.attn_chunk > 0) {
+      const int cs = (max(i + delta, 0) / p.attn_chunk) * p.attn_chunk;
+      ok = ok && j >= cs && j < cs + p.attn_chunk;
+    }
+  }
+  return ok;
+}
+
+// the fp32 forward (fwd_f32.hip), dispatched from fa_forward_launch
+int launch_fwd_f32(const FwdParams& p, hipStream_t st);
+
+}  // namespace fa

@@ -82,8 +82,8 @@ def _check_supported(q, k):
         raise ValueError("fable_attn: tensors must be on the GPU (q.is_cuda == False)")
     if q.shape[-1] > MAX_HEAD_DIM:
         raise ValueError(f"fable_attn: head_dim={q.shape[-1]} exceeds the maximum {MAX_HEAD_DIM}")
-    if q.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"fable_attn: dtype {q.dtype} is not supported; use fp16 or bf16")
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"fable_attn: dtype {q.dtype} is not supported; use fp16, bf16 or fp32")
     if q.shape[2] % k.shape[2] != 0:
         raise ValueError(f"fable_attn: nheads_q={q.shape[2]} is not a multiple of "
                          f"nheads_k={k.shape[2]} (GQA)")

@@ -101,7 +101,7 @@ def test_rejections_before_any_launch(fake):
     with pytest.raises(NotImplementedError, match="256"):
         fai.flash_attn_func(rnd(1, 8, 2, 192), rnd(1, 8, 2, 192), rnd(1, 8, 2, 192), qv=rnd(1, 8, 2, 192))
     with pytest.raises(ValueError, match="dtype"):
-        x = rnd(1, 8, 2, 64, dt=torch.float32)
+        x = rnd(1, 8, 2, 64, dt=torch.float64)   # fp16, bf16 and fp32 are served (reference :149)
         fai.flash_attn_func(x, x, x)
     assert fake.calls == []
 
