@@ -17,6 +17,8 @@
 //  * appending new_k/new_v (with rotary on k) is a kernel earlier in the same stream: the
 //    reference's hipDeviceSynchronize() after the append (fa_decode.hip:348-351) is gone.
 // Scores are handled in the log2 domain; partial maxima are stored in log2 units.
+#include <type_traits>
+
 #include "attn_device.hpp"
 #include "status.hpp"
 
@@ -307,6 +309,170 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
   }
 }
 
+// fp32 caches (the reference's decode serves fp16/bf16/fp32, fa_decode.hip:4,360): the same
+// workgroup and wave split, on v_mfma_f32_16x16x4_f32. Lane (head lh, group lg) holds q dims
+// lg*HD/4 + t as the B operand of S^T = K . Q^T, whose A operand is loaded straight from the
+// paged cache (16 bytes of one key row per lane); P^T is the B operand of O^T = V^T . P^T,
+// whose A operand is one float per lane (V[key 16kb + 4lg + j][16db + lh]), read from the cache
+// as well (four 64-byte row segments per load). Rotation of q stays exact in fp32.
+template <int HD, bool FEAT>
+__global__ __launch_bounds__(256) void dec_partial_f32_kernel(DecParams p, int page_shift, int ngrp, int append) {
+  constexpr int NQ = HD / 4;    // S^T contraction steps (q floats per lane)
+  constexpr int NDB = HD / 16;  // 16-row blocks of O^T
+  constexpr int QSTR = HD + 4;
+  constexpr int QBYTES = 16 * QSTR * 4, OBYTES = kDecWaves * 16 * HD * 4;
+  __shared__ __attribute__((aligned(16))) char raw[QBYTES > OBYTES ? QBYTES : OBYTES];
+  __shared__ float red_m[kDecWaves][16], red_l[kDecWaves][16];
+  float (*qsh)[QSTR] = (float (*)[QSTR])raw;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lg = lane >> 4, lh = lane & 15;
+  const int b = blockIdx.y / p.nq, tk = blockIdx.y % p.nq;
+  const int kvh = blockIdx.x / ngrp, hgi = blockIdx.x % ngrp;
+  const int h0 = kvh * p.gqa + 16 * hgi, hg = min(16, p.gqa - 16 * hgi);
+  const int sp = blockIdx.z;
+  const int NKV = p.NH / p.gqa;
+  const DecRange rg = dec_range(p, b, tk, sp, append);
+
+  const float* qg = (const float*)p.q + ((long long)(b * p.nq + tk) * p.NH + h0) * HD;
+  for (int i = tid; i < 16 * NQ; i += 256) {
+    const int g = i / NQ, c = i % NQ;
+    const f32x4 v = *(const f32x4*)(qg + (long long)min(g, hg - 1) * HD + 4 * c);
+#pragma unroll
+    for (int e = 0; e < 4; e++) qsh[g][4 * c + e] = g < hg ? v[e] : 0.0f;
+  }
+  __syncthreads();
+  if (p.rotary) {
+    const int rdim = p.rotary_dim > 0 ? p.rotary_dim : HD, half = rdim / 2;
+    const int rp = (p.rotary_pos ? p.rotary_pos[b] : p.ctx_len[b]) + tk;
+    for (int i = tid; i < hg * half; i += 256) {
+      const int g = i / half, j = i % half;
+      const float c = p.cos[(long long)rp * half + j], s = p.sin[(long long)rp * half + j];
+      const int ia = p.rotary == 1 ? j : 2 * j, ib = p.rotary == 1 ? j + half : 2 * j + 1;
+      const float x = qsh[g][ia], y = qsh[g][ib];
+      qsh[g][ia] = x * c - y * s;
+      qsh[g][ib] = y * c + x * s;
+    }
+    __syncthreads();
+  }
+  float qreg[NQ];
+#pragma unroll
+  for (int t = 0; t < NQ; t++) qreg[t] = qsh[lh][lg * NQ + t];
+
+  f32x4 oacc[NDB];
+#pragma unroll
+  for (int db = 0; db < NDB; db++) oacc[db] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.0f;
+  const float c_log2 = p.scale * kLog2e;
+  const float slope = (FEAT && p.alibi && lh < hg) ? p.alibi[h0 + lh] : 0.0f;
+  const float inv_cap = p.softcap > 0.0f ? 1.0f / p.softcap : 0.0f;
+  const float* Kc = (const float*)p.Kc;
+  const float* Vc = (const float*)p.Vc;
+  const int* bt = p.block_table + (long long)b * p.max_blocks;
+  const int pmask = p.page - 1;
+  const int last = rg.end - 1;
+  auto row_off = [&](int key) -> long long {
+    return (((long long)bt[key >> page_shift] * p.page + (key & pmask)) * NKV + kvh) * HD;
+  };
+  constexpr int kStep = kDecChunk * kDecWaves;
+  for (int kc0 = rg.start + kDecChunk * wave; kc0 < rg.end; kc0 += kStep) {
+    // keys past the end clamp to the last one (masked below), so every load is unconditional
+    f32x4 s[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++) {
+      const float* kr = Kc + row_off(min(kc0 + 16 * kb + lh, last)) + lg * NQ;
+      s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int u = 0; u < NQ / 4; u++) {
+        const f32x4 a = *(const f32x4*)(kr + 4 * u);
+#pragma unroll
+        for (int e = 0; e < 4; e++) s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], qreg[4 * u + e], s[kb], 0, 0, 0);
+      }
+    }
+    // s[kb][r] is key kc0 + 16*kb + 4*lg + r, head lh
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int key = kc0 + 16 * kb + 4 * lg + r;
+        float t;
+        if (FEAT) {
+          float x = s[kb][r] * p.scale;
+          if (p.softcap > 0.0f) x = p.softcap * tanhf(x * inv_cap);
+          x += slope * (float)(key - rg.qpos);
+          t = x * kLog2e;
+        } else {
+          t = s[kb][r] * c_log2;
+        }
+        t = key < rg.end ? t : -INFINITY;
+        s[kb][r] = t;
+        mx = fmaxf(mx, t);
+      }
+    mx = half_max(xor16_max(mx));
+    const float m_new = fmaxf(m_run, mx);
+    const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+    const float corr = exp2_fast(m_run - m_use);
+    float rs = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float e = exp2_fast(s[kb][r] - m_use);
+        rs += e;
+        s[kb][r] = e;
+      }
+    l_run = l_run * corr + rs;
+    m_run = m_new;
+#pragma unroll
+    for (int db = 0; db < NDB; db++) oacc[db] *= corr;
+#pragma unroll
+    for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const float* vr = Vc + row_off(min(kc0 + 16 * kb + 4 * lg + r, last)) + lh;
+#pragma unroll
+        for (int db = 0; db < NDB; db++)
+          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * db], s[kb][r], oacc[db], 0, 0, 0);
+      }
+  }
+
+  // ---- merge the four waves (as the fp16/bf16 kernel)
+  const float l_grp = half_sum(xor16_sum(l_run));
+  __syncthreads();  // q staging is dead: the region holds the accumulators
+  float* red_o = (float*)raw;  // [wave][16 heads][HD]
+  if (lg == 0) {
+    red_m[wave][lh] = m_run;
+    red_l[wave][lh] = l_grp;
+  }
+#pragma unroll
+  for (int db = 0; db < NDB; db++)
+#pragma unroll
+    for (int r = 0; r < 4; r++) red_o[(wave * 16 + lh) * HD + 16 * db + 4 * lg + r] = oacc[db][r];
+  __syncthreads();
+  for (int i = tid; i < hg * HD; i += 256) {
+    const int g = i / HD, d = i % HD;
+    float gm = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kDecWaves; w++) gm = fmaxf(gm, red_m[w][g]);
+    float l = 0.0f, acc = 0.0f;
+    if (gm != -INFINITY) {
+#pragma unroll
+      for (int w = 0; w < kDecWaves; w++) {
+        const float f = exp2_fast(red_m[w][g] - gm);
+        l += f * red_l[w][g];
+        acc += f * red_o[(w * 16 + g) * HD + d];
+      }
+    }
+    float* out = p.scratch + (((long long)(b * p.nq + tk) * p.NH + h0 + g) * p.nsplit + sp) * (HD + 2);
+    if (d == 0) {
+      out[0] = gm;
+      out[1] = l;
+    }
+    out[2 + d] = acc;
+  }
+}
+
 // merge nsplit partials of one (token, head): grid (batch*nq, NH), block HD
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void dec_combine_kernel(DecParams p) {
@@ -377,10 +543,17 @@ static int launch_dec(const DecParams& p, hipStream_t st, const void* nk, const 
   }
   const bool feat = p.softcap > 0.0f || p.alibi != nullptr;
   dim3 grid(NKV * ngrp, p.batch * p.nq, p.nsplit);
-  if (feat)
-    hipLaunchKernelGGL((dec_partial_kernel<T, HD, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
-  else
-    hipLaunchKernelGGL((dec_partial_kernel<T, HD, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+  if constexpr (std::is_same<T, float>::value) {
+    if (feat)
+      hipLaunchKernelGGL((dec_partial_f32_kernel<HD, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+    else
+      hipLaunchKernelGGL((dec_partial_f32_kernel<HD, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+  } else {
+    if (feat)
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+    else
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+  }
   if (int rc = launch_status("fa_decode_launch (partial)")) return rc;
   hipLaunchKernelGGL((dec_combine_kernel<T, HD>), dim3(p.batch * p.nq, p.NH), dim3(HD), 0, st, p);
   return launch_status("fa_decode_launch (combine)");
@@ -445,6 +618,7 @@ extern "C" int fa_decode_launch(DecParams p, int dtype, void* stream, const void
   switch (dtype) {
     case FA_F16: return dec_dispatch<_Float16>(p, st, new_k, new_v);
     case FA_BF16: return dec_dispatch<__bf16>(p, st, new_k, new_v);
-    default: return fail(FA_ERR_DTYPE, "fa_decode_launch: dtype %d not implemented (fp16/bf16)", dtype);
+    case FA_F32: return dec_dispatch<float>(p, st, new_k, new_v);
+    default: return fail(FA_ERR_DTYPE, "fa_decode_launch: dtype %d not implemented (fp16/bf16/fp32)", dtype);
   }
 }

@@ -497,8 +497,8 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None,
     d_real = q.shape[-1]
     if not q.is_cuda:
         raise ValueError("fable_attn: tensors must be on the GPU (q.is_cuda == False)")
-    if q.dtype not in (torch.float16, torch.bfloat16):
-        raise ValueError(f"fable_attn: dtype {q.dtype} is not supported; use fp16 or bf16")
+    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+        raise ValueError(f"fable_attn: dtype {q.dtype} is not supported; use fp16, bf16 or fp32")
     if qv is not None:
         # same concatenation as the prefill qv path, applied to the whole cache (compat path)
         if qv.shape[-1] != v_cache.shape[-1]:

@@ -238,7 +238,7 @@ def decode(q, k_cache, v_cache, block_table, ctx_len, scale, new_k=None, new_v=N
     cfg = OracleDecCfg(B, nq, H, Hk, D, page, bt.shape[1], _f32s(scale), _f32s(softcap),
                        int(window), int(rotary), int(rotary_dim), int(nk is not None),
                        al.ctypes.data if al is not None else None,
-                       {None: 0, "f16": 1, "bf16": 2}[append_dtype])
+                       {None: 0, "f32": 0, "f16": 1, "bf16": 2}[append_dtype])
     lib().oracle_decode(_p(q), _p(kc), _p(vc), _p(bt), _p(cl), _p(nk), _p(nv), _p(cs), _p(sn),
                         _p(lp), _p(rp), _p(o), _p(lse), ctypes.byref(cfg))
     return o, lse
