@@ -209,7 +209,7 @@ def summarize_stats(d, kernel_re=None, skip=0):
 
 # kernel symbols of the measured workloads (one symbol per workload in the PMC runs, which
 # leave out the fwd extras that share the headline's symbol)
-FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128ELi64ELi4ELi2ELi1EEELb1ELb0EEEv9FwdParamsi"
+FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128ELi64ELi8ELi2ELi1EEELb1ELb0ELb0EEEv9FwdParamsi"
 DEC_C4_KERNEL = r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0EEEv9DecParamsiii"
 
 

@@ -488,8 +488,8 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
 template <typename T>
 static int dispatch_hd(const FwdParams& p, hipStream_t st) {
   switch (p.HD) {
-    case 64: return launch_fwd<T, FwdCfg<64, 64, 4, 2>>(p, st);
-    case 128: return launch_fwd<T, FwdCfg<128, 64, 4, 2>, FwdCfg<128, 32, 4, 2>>(p, st);
+    case 64: return launch_fwd<T, FwdCfg<64, 64, 8, 2>>(p, st);
+    case 128: return launch_fwd<T, FwdCfg<128, 64, 8, 2>, FwdCfg<128, 32, 4, 2>>(p, st);
     case 256: return launch_fwd<T, FwdCfg<256, 32, 4, 1>>(p, st);
     default: return fail(FA_ERR_HEADDIM, "fa_forward_launch: head_dim=%d has no kernel (64, 128, 256)", p.HD);
   }
