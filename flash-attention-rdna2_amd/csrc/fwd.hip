@@ -235,13 +235,13 @@ fwd_kernel(FwdParams p, int nqt) {
         for (int r = 0; r < 16; r++) {
           const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
           float x;
-          if constexpr (decltype(cap)::value) {
+          if constexpr ((decltype(cap)::value & 1) != 0) {
             const float e = exp2_fast(s[jb][r] * kcap);
             x = fmaf(-2.0f * lcap, __builtin_amdgcn_rcpf(e + 1.0f), lcap);
           } else {
             x = s[jb][r] * c_log2;
           }
-          x = fmaf(aslope2, (float)(key - qi), x);
+          if constexpr ((decltype(cap)::value & 2) != 0) x = fmaf(aslope2, (float)(key - qi), x);
           if constexpr (decltype(masked)::value) {
             bool ok = key < SK;
             if (CAUSAL) ok = ok && key <= qi + delta;
@@ -254,8 +254,10 @@ fwd_kernel(FwdParams p, int nqt) {
             x = ok ? x : -INFINITY;
           }
           s[jb][r] = x;
-          // bound how many scores the scheduler transforms at once (register pressure)
-          if ((r & 7) == 7) __builtin_amdgcn_sched_barrier(0);
+          // bound how many scores the scheduler transforms at once (the softcap transform's
+          // register pressure); plain logits are left to the scheduler
+          if constexpr ((decltype(cap)::value & 1) != 0)
+            if ((r & 7) == 7) __builtin_amdgcn_sched_barrier(0);
         }
     } else if constexpr (decltype(masked)::value) {
 #pragma unroll
@@ -329,9 +331,17 @@ fwd_kernel(FwdParams p, int nqt) {
   };
   using Plain = std::integral_constant<bool, false>;
   using Masked = std::integral_constant<bool, true>;
-  using Cap0 = std::integral_constant<bool, false>;
-  using Cap1 = std::integral_constant<bool, true>;
-  const bool has_cap = FEAT && p.softcap > 0.0f;
+  // logit transform of the feature kernels: bit 0 softcap, bit 1 alibi
+  using Cap0 = std::integral_constant<int, 0>;
+  const int fmode = FEAT ? (p.softcap > 0.0f ? 1 : 0) | (p.alibi_slopes ? 2 : 0) : 0;
+  auto with_fmode = [&](auto f) {
+    switch (fmode) {
+      case 1: f(std::integral_constant<int, 1>{}); break;
+      case 2: f(std::integral_constant<int, 2>{}); break;
+      case 3: f(std::integral_constant<int, 3>{}); break;
+      default: f(Cap0{}); break;
+    }
+  };
 
   // ---- prologue: K tiles 0 and 1, V tile 0 in LDS; S and P of tile 0
   V8 pb[QB][C::NG];
@@ -372,13 +382,10 @@ fwd_kernel(FwdParams p, int nqt) {
       for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, Cap0{}, i, s[i], kstart, pb[i], resc[i]);
     } else if ((a_cur = active(0))) {
       qk(0, s);
-      if (has_cap) {
+      with_fmode([&](auto cap) {
 #pragma unroll
-        for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, Cap1{}, i, s[i], kstart, pb[i], resc[i]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, Cap0{}, i, s[i], kstart, pb[i], resc[i]);
-      }
+        for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, cap, i, s[i], kstart, pb[i], resc[i]);
+      });
     }
   }
   __syncthreads();  // every wave has read K stage 0 before iteration 0 refills it
@@ -418,11 +425,10 @@ fwd_kernel(FwdParams p, int nqt) {
 #pragma unroll
         for (int i = 0; i < QB; i++) corr[i] = softmax(masked, cap, i, s[i], kb1, pb[i], resc[i]);
       };
-      if (FEAT && interior(t + 1)) {
-        if (has_cap) sm(Plain{}, Cap1{}); else sm(Plain{}, Cap0{});
-      } else {
-        if (has_cap) sm(Masked{}, Cap1{}); else sm(Masked{}, Cap0{});
-      }
+      if (FEAT && interior(t + 1))
+        with_fmode([&](auto cap) { sm(Plain{}, cap); });
+      else
+        with_fmode([&](auto cap) { sm(Masked{}, cap); });
     }
     a_cur = a_next;
     lstore_k(t & 1);
@@ -453,35 +459,41 @@ fwd_kernel(FwdParams p, int nqt) {
   }
 }
 
-// C runs the plain masks (causal / sequence end), CF the feature kernels (window, chunk,
-// softcap, alibi, dropout), whose extra per-score work needs a different register balance.
-// Dropout has kernels of its own, so its Philox rounds cost the other features no registers.
+// C runs the plain masks (causal / sequence end) and wide-window / alibi feature kernels; CF
+// the softcap, dropout and narrow-mask kernels. Dropout has kernels of its own, so its Philox
+// rounds cost the other features no registers.
 template <typename T, class C, class CF = C>
 static int launch_fwd(const FwdParams& p, hipStream_t st) {
   const bool drop = p.dropout_p > 0.0f;
   const bool feat = drop || p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
                     p.win_left >= 0 || (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
-  const int br = feat ? CF::BR : C::BR;
+  // CF (128-row workgroups) for softcap and dropout, whose per-score work needs its register
+  // balance, and for narrow masks (a window or chunk under 2048 keys), where most of a 256-row
+  // workgroup's key span would be masked; C (256-row workgroups) otherwise
+  auto narrow = [](int w) { return w >= 0 && w < 2048; };
+  const bool heavy = drop || p.softcap > 0.0f || narrow(p.win_left) || (p.attn_chunk > 0 && p.attn_chunk < 2048) ||
+                     (narrow(p.win_right) && !(p.win_right == 0 && p.causal));
+  const int br = heavy ? CF::BR : C::BR;
   const int nqt = (p.SQ + br - 1) / br;
   const long long nblk = (long long)nqt * p.NH * p.batch;
   if (nblk <= 0) return FA_OK;
   if (nblk > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fa_forward_launch: grid too large");
   dim3 grid((unsigned)nblk);
-  if (p.causal) {
+  auto go = [&](auto causal) {
+    constexpr bool CA = decltype(causal)::value;
     if (drop)
-      hipLaunchKernelGGL((fwd_kernel<T, CF, true, true, true>), grid, dim3(CF::NT), 0, st, p, nqt);
+      hipLaunchKernelGGL((fwd_kernel<T, CF, CA, true, true>), grid, dim3(CF::NT), 0, st, p, nqt);
+    else if (heavy)
+      hipLaunchKernelGGL((fwd_kernel<T, CF, CA, true>), grid, dim3(CF::NT), 0, st, p, nqt);
     else if (feat)
-      hipLaunchKernelGGL((fwd_kernel<T, CF, true, true>), grid, dim3(CF::NT), 0, st, p, nqt);
+      hipLaunchKernelGGL((fwd_kernel<T, C, CA, true>), grid, dim3(C::NT), 0, st, p, nqt);
     else
-      hipLaunchKernelGGL((fwd_kernel<T, C, true, false>), grid, dim3(C::NT), 0, st, p, nqt);
-  } else {
-    if (drop)
-      hipLaunchKernelGGL((fwd_kernel<T, CF, false, true, true>), grid, dim3(CF::NT), 0, st, p, nqt);
-    else if (feat)
-      hipLaunchKernelGGL((fwd_kernel<T, CF, false, true>), grid, dim3(CF::NT), 0, st, p, nqt);
-    else
-      hipLaunchKernelGGL((fwd_kernel<T, C, false, false>), grid, dim3(C::NT), 0, st, p, nqt);
-  }
+      hipLaunchKernelGGL((fwd_kernel<T, C, CA, false>), grid, dim3(C::NT), 0, st, p, nqt);
+  };
+  if (p.causal)
+    go(std::integral_constant<bool, true>{});
+  else
+    go(std::integral_constant<bool, false>{});
   return launch_status("fa_forward_launch");
 }
 
