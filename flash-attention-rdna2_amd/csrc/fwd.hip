@@ -1,508 +1,17 @@
-// fwd.hip — exact attention forward for gfx950 (MI355X), fp16 and bf16.
-//
-// Replaces the reference forward (kernels/fa_forward.hip:52-313 kernel, :424-451 launcher);
-// same math and masking contract (FwdParams in include/fable_attn_abi.h), new design:
-//
-//  * workgroup = NW waves; wave w owns 32 query rows, so a workgroup covers BR = 32*NW rows of
-//    one (batch, head). Q for those rows lives in registers for the whole kernel, laid out as
-//    the B operand of v_mfma_f32_32x32x16 (lane l holds query l%32, 8 head-dim values).
-//  * scores are computed transposed, S^T = K . Q^T (A = K rows from LDS), so each lane holds
-//    one query and BC/2 of its keys: the row max needs a single cross-half exchange
-//    (v_permlane32_swap) and the probabilities P^T are already laid out as the B operand of
-//    O^T = V^T . P^T. P never touches LDS.
-//  * software pipeline: iteration j computes S(j+1) = K(j+1) . Q^T, then the PV product of tile
-//    j and the softmax of tile j+1 in one branch-free block, so the VALU work of one tile runs
-//    under the matrix-core work of the other. K and V have their own double buffers in LDS
-//    (K is loaded two tiles ahead, V one) and there is one barrier per tile.
-//  * LDS rows are padded (K by 16 bytes, V by 64 bytes) so that the 16-byte K reads of 16 rows
-//    and the transposing V reads (ds_read_b64_tr_b16, 4 rows x 64 bytes per half-wave) hit
-//    distinct banks, and every read address is a per-lane base plus an immediate offset.
-//  * tile loads go through buffer descriptors (rows past the last needed key read as zeros),
-//    so they carry no per-lane condition and stay in flight across a whole iteration.
-//  * online softmax in the log2 domain (one FMA + v_exp_f32 per score). The running max only
-//    moves when a tile raises it by more than 2^8 (probabilities then stay <= 256, exact in
-//    fp16/bf16 range), so the O rescale is rare; it is skipped when no lane needs it. fp16 row
-//    sums add the rounded probabilities pairwise (v_dot2, fp32 accumulate), the values the PV
-//    product uses.
-//  * tiles entirely outside the causal / window / chunk range are never loaded; the leading
-//    tiles every row of the workgroup sees in full run without mask code (template CAUSAL/FEAT
-//    split as in the reference's launch_cfg, fa_forward.hip:409-421).
-//  * the workgroup -> (q tile, head, batch) map is XCD-aware (consecutive work items of one
-//    head share an XCD's L2) and, for causal, starts with the heaviest q tiles.
-#include <type_traits>
-
+// fwd.hip — fa_forward_launch, the forward's C-ABI entry point: argument checks and dispatch to
+// the per-head-dim fp16/bf16 kernels (fwd_d64/128/256.hip, kernel in fwd_kernel.hpp) and the
+// fp32 kernels (fwd_f32.hip). Reference launcher: kernels/fa_forward.hip:424-451.
 #include "attn_device.hpp"
 #include "fwd_common.hpp"
 #include "status.hpp"
 
 namespace fa {
 
-template <int HD_, int BC_, int NW_, int WPE_, int QB_ = 1>
-struct FwdCfg {
-  static constexpr int HD = HD_, BC = BC_, NW = NW_, WPE = WPE_;
-  static constexpr int QB = QB_;            // 32-query blocks per wave
-  static constexpr int NT = NW * 64;
-  static constexpr int BR = NW * 32 * QB;
-  static constexpr int NB = BC / 32;        // 32-key blocks per tile
-  static constexpr int NG = BC / 16;        // 16-key groups per tile (PV contraction steps)
-  static constexpr int NDS = HD / 16;       // Q.K contraction steps
-  static constexpr int NDB = HD / 32;       // 32-row blocks of O^T
-  static constexpr int DCH = HD / 8;        // 16-byte chunks per K/V row
-  static constexpr int KSTR = HD + 8;       // LDS row strides (elements)
-  static constexpr int VSTR = HD + 32;
-  static constexpr int KTILE = BC * KSTR;
-  static constexpr int VTILE = BC * VSTR;
-  static constexpr int KCH = BC * DCH;      // chunks per K (or V) tile
-  static constexpr int KJ = KCH / NT;       // chunks each thread loads per K (or V) tile
-  static constexpr int RSTEP = NT / DCH;    // rows between a thread's chunks
-  static_assert(HD % 32 == 0 && BC % 32 == 0, "shape");
-  static_assert(KCH % NT == 0 && NT % DCH == 0, "loader split");
-};
-
-template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
-                          amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-fwd_kernel(FwdParams p, int nqt) {
-  using V8 = typename Dt<T>::V8;
-  using V4 = typename Dt<T>::V4;
-  __shared__ __attribute__((aligned(16))) T kl[2 * C::KTILE];
-  __shared__ __attribute__((aligned(16))) T vl[2 * C::VTILE];
-
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
-
-  // ---- work item -> (sequence z, head h, q tile)
-  const int w = xcd_remap(blockIdx.x, gridDim.x);
-  const int qti = w % nqt, zh = w / nqt;
-  const int h = zh % p.NH, z = zh / p.NH;
-  const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
-  const int kvh = h / p.gqa;
-
-  const SeqView sv = seq_view(p, z, h);
-  const int SQ = sv.SQ, SK = sv.SK;
-  const int qb = qt * C::BR;
-  if (qb >= SQ) return;
-  const int delta = SK - SQ;
-
-  const T* Qg = (const T*)p.Q + sv.q0 + (long long)h * p.sQ.h;
-  const T* Kg = (const T*)p.K + sv.k0 + (long long)kvh * p.sK.h;
-  const T* Vg = (const T*)p.V + sv.v0 + (long long)kvh * p.sV.h;
-  T* Og = (T*)p.O + sv.o0 + (long long)h * p.sO.h;
-
-  // ---- block and wave key ranges
-  constexpr int QB = C::QB;
-  int bk0, bk1;
-  key_range<CAUSAL, FEAT>(p, qb, min(qb + C::BR, SQ) - 1, delta, SK, bk0, bk1);
-  const int qw = qb + wave * 32 * QB;  // first row of this wave; block i = rows qw+32i..+31
-  const bool wave_rows = qw < SQ;
-  int wk0 = 0, wk1 = 0;
-  if (wave_rows) key_range<CAUSAL, FEAT>(p, qw, min(qw + 32 * QB, SQ) - 1, delta, SK, wk0, wk1);
-  const int kstart = (bk0 / C::BC) * C::BC;
-  const int ntiles = bk1 > bk0 ? (bk1 - kstart + C::BC - 1) / C::BC : 0;
-
-  // ---- Q (B operands) in registers: lane holds query qw + 32i + l32, head-dim 16ds + 8hh..+7
-  V8 qreg[QB][C::NDS];
-#pragma unroll
-  for (int i = 0; i < QB; i++) {
-    const int qi = qw + 32 * i + l32;
-#pragma unroll
-    for (int ds = 0; ds < C::NDS; ds++) {
-      if (qi < SQ)
-        qreg[i][ds] = *(const V8*)(Qg + (long long)qi * p.sQ.s + 16 * ds + 8 * hh);
-      else
-        qreg[i][ds] = bitcast<V8>(u32x4{0, 0, 0, 0});
-    }
-  }
-
-  f32x16 oacc[QB][C::NDB];
-  float m_run[QB], l_run[QB];
-#pragma unroll
-  for (int i = 0; i < QB; i++) {
-#pragma unroll
-    for (int db = 0; db < C::NDB; db++) oacc[i][db] = f32x16{};
-    m_run[i] = -INFINITY;
-    l_run[i] = 0.0f;
-  }
-  const float c_log2 = p.scale * kLog2e;
-  const float aslope = (FEAT && p.alibi_slopes) ? p.alibi_slopes[h] : 0.0f;
-
-  // leading tiles that every row of the workgroup sees in full: no mask code for them
-  int nint = 0;
-  if (!FEAT) {
-    int lim = SK;
-    if (CAUSAL) lim = min(lim, qb + delta + 1);
-    nint = min(max((lim - kstart) / C::BC, 0), ntiles);
-  }
-
-  // ---- global -> register loads of one tile through buffer descriptors spanning the rows
-  // kb .. kvalid-1 of this head: rows past the last needed key read as zeros without a
-  // per-lane condition (a conditional load would make the compiler wait for it at once), and
-  // the per-lane byte offsets are loop invariant.
-  const int kvalid = min(SK, kstart + ntiles * C::BC);
-  int koff[C::KJ], voff[C::KJ];
-#pragma unroll
-  for (int j = 0; j < C::KJ; j++) {
-    const int ci = tid + j * C::NT;
-    const int r = ci / C::DCH, c = ci % C::DCH;
-    koff[j] = r * (int)(p.sK.s * 2) + 16 * c;
-    voff[j] = r * (int)(p.sV.s * 2) + 16 * c;
-  }
-  const int lrow = tid / C::DCH, lch = tid % C::DCH;
-  const int lko = lrow * C::KSTR + 8 * lch, lvo = lrow * C::VSTR + 8 * lch;
-  u32x4 ldk[C::KJ], ldv[C::KJ];
-  auto gload_k = [&](int kb) {
-    const auto r = buf_rsrc(Kg + (long long)kb * p.sK.s, (long long)(kvalid - kb) * p.sK.s * 2);
-#pragma unroll
-    for (int j = 0; j < C::KJ; j++) ldk[j] = buf_load16(r, koff[j]);
-  };
-  auto gload_v = [&](int kb) {
-    const auto r = buf_rsrc(Vg + (long long)kb * p.sV.s, (long long)(kvalid - kb) * p.sV.s * 2);
-#pragma unroll
-    for (int j = 0; j < C::KJ; j++) ldv[j] = buf_load16(r, voff[j]);
-  };
-  auto lstore_k = [&](int st) {
-    T* b = kl + st * C::KTILE + lko;
-#pragma unroll
-    for (int j = 0; j < C::KJ; j++) *(u32x4*)(b + j * C::RSTEP * C::KSTR) = ldk[j];
-  };
-  auto lstore_v = [&](int st) {
-    T* b = vl + st * C::VTILE + lvo;
-#pragma unroll
-    for (int j = 0; j < C::KJ; j++) *(u32x4*)(b + j * C::RSTEP * C::VSTR) = ldv[j];
-  };
-
-  // S^T = K . Q^T for the K tile in stage st, every query block: lane reads key row
-  // 32*jb + l32, head-dim 16*ds + 8*hh .. +7 (the A operand of v_mfma_f32_32x32x16), shared by
-  // the blocks
-  const int kro = l32 * C::KSTR + 8 * hh;
-  auto qk = [&](int st, f32x16 (&s)[QB][C::NB]) {
-    const T* kp = kl + st * C::KTILE + kro;
-#pragma unroll
-    for (int i = 0; i < QB; i++)
-#pragma unroll
-      for (int jb = 0; jb < C::NB; jb++) s[i][jb] = f32x16{};
-#pragma unroll
-    for (int ds = 0; ds < C::NDS; ds++)
-#pragma unroll
-      for (int jb = 0; jb < C::NB; jb++) {
-        const V8 a = *(const V8*)(kp + jb * 32 * C::KSTR + 16 * ds);
-#pragma unroll
-        for (int i = 0; i < QB; i++) s[i][jb] = Dt<T>::mma32(a, qreg[i][ds], s[i][jb]);
-      }
-  };
-  // O^T += V^T . P^T for the V tile in stage st. A operand by transposing reads: lane j16 of
-  // 16-lane group (mh, hh) addresses key row 16g+8a+4hh+j16/4, head-dim 32db+16mh+4*(j16%4)
-  // and receives head-dim 32db+16mh+j16 of keys 16g+8a+4hh+0..3 (the keys of its P^T items
-  // 4a..4a+3).
-  const int vro = (4 * hh + (j16 >> 2)) * C::VSTR + 16 * mh + 4 * (j16 & 3);
-  auto pv = [&](int st, const V8 (&pb)[QB][C::NG]) {
-    const T* vp = vl + st * C::VTILE + vro;
-#pragma unroll
-    for (int db = 0; db < C::NDB; db++)
-#pragma unroll
-      for (int g = 0; g < C::NG; g++) {
-        const V4 lo = lds_read_tr<T>(vp + 16 * g * C::VSTR + 32 * db);
-        const V4 hi = lds_read_tr<T>(vp + (16 * g + 8) * C::VSTR + 32 * db);
-        V8 av;
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-          av[e] = lo[e];
-          av[4 + e] = hi[e];
-        }
-#pragma unroll
-        for (int i = 0; i < QB; i++) oacc[i][db] = Dt<T>::mma32(av, pb[i][g], oacc[i][db]);
-      }
-  };
-  // Softmax of one tile (keys kb..kb+BC-1) of query block i in s -> probabilities pb (the B
-  // operands of the PV product), running max/sum update. Returns the factor the block's O
-  // accumulators must be scaled by once every earlier tile's PV product is in them; `resc` is
-  // set when any lane's is not 1. Branch-free, so the compiler can interleave it with
-  // independent matrix-core work.
-  // FEAT logits in log2 units. softcap: c * tanh(x / c) with x = scale * q.k, tanh(y) =
-  // 1 - 2 / (exp(2y) + 1); exp(2y) = exp2(q.k * kcap), so no division per score
-  const float kcap = p.softcap > 0.0f ? 2.0f * kLog2e * p.scale / p.softcap : 0.0f;
-  const float lcap = p.softcap * kLog2e;
-  const float aslope2 = aslope * kLog2e;
-  // dropout: probabilities are scaled after the row sum, O = sum z p V / sum p
-  const float keep_scale = DROP ? 1.0f / (1.0f - p.dropout_p) : 1.0f;
-  auto softmax = [&](auto masked, auto cap, int i, f32x16 (&s)[C::NB], int kb, V8 (&pb)[C::NG], bool& resc) {
-    const int qi = qw + 32 * i + l32;
-    const int kq = kb + 4 * hh;  // key of s[jb][r] = kq + 32*jb + 8*(r/4) + (r%4)
-    if constexpr (FEAT) {
-#pragma unroll
-      for (int jb = 0; jb < C::NB; jb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
-          float x;
-          if constexpr ((decltype(cap)::value & 1) != 0) {
-            const float e = exp2_fast(s[jb][r] * kcap);
-            x = fmaf(-2.0f * lcap, __builtin_amdgcn_rcpf(e + 1.0f), lcap);
-          } else {
-            x = s[jb][r] * c_log2;
-          }
-          if constexpr ((decltype(cap)::value & 2) != 0) x = fmaf(aslope2, (float)(key - qi), x);
-          if constexpr (decltype(masked)::value) {
-            bool ok = key < SK;
-            if (CAUSAL) ok = ok && key <= qi + delta;
-            if (p.win_left >= 0) ok = ok && key >= qi + delta - p.win_left;
-            if (p.win_right >= 0) ok = ok && key <= qi + delta + p.win_right;
-            if (p.attn_chunk > 0) {
-              const int cs = (max(qi + delta, 0) / p.attn_chunk) * p.attn_chunk;
-              ok = ok && key >= cs && key < cs + p.attn_chunk;
-            }
-            x = ok ? x : -INFINITY;
-          }
-          s[jb][r] = x;
-          // bound how many scores the scheduler transforms at once (the softcap transform's
-          // register pressure); plain logits are left to the scheduler
-          if constexpr ((decltype(cap)::value & 1) != 0)
-            if ((r & 7) == 7) __builtin_amdgcn_sched_barrier(0);
-        }
-    } else if constexpr (decltype(masked)::value) {
-#pragma unroll
-      for (int jb = 0; jb < C::NB; jb++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) {
-          const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
-          const bool ok = CAUSAL ? (key < SK && key <= qi + delta) : key < SK;
-          if (!ok) s[jb][r] = -INFINITY;
-        }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int jb = 0; jb < C::NB; jb++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[jb][r]);
-    mx = half_max(mx);
-    const float m_cand = fmaxf(m_run[i], FEAT ? mx : mx * c_log2);
-    const bool need = m_cand > m_run[i] + kLazyMax;
-    const float corr = need ? exp2_fast(m_run[i] - m_cand) : 1.0f;
-    m_run[i] = need ? m_cand : m_run[i];
-    resc = __builtin_amdgcn_ballot_w64(need) != 0;
-    const float m_use = m_run[i] == -INFINITY ? 0.0f : m_run[i];
-    // fp16 sums the rounded probabilities pairwise (their rounding moves the row sum by at most
-    // 2^-12 relative); bf16 rounding is 8x coarser, so it sums the fp32 values, and so does
-    // dropout, which scales the probabilities after the sum
-    constexpr bool kPairSum = std::is_same<T, _Float16>::value && !DROP;
-    float r0 = 0.0f, r1 = 0.0f;
-#pragma unroll
-    for (int jb = 0; jb < C::NB; jb++)
-#pragma unroll
-      for (int sh = 0; sh < 2; sh++)
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float x = s[jb][8 * sh + e];
-          const float pe = FEAT ? exp2_fast(x - m_use) : exp2_fast(fmaf(x, c_log2, -m_use));
-          float pz = pe;
-          if constexpr (DROP) {
-            const int r = 8 * sh + e, key = kq + 32 * jb + 8 * (r >> 2) + (r & 3);
-            pz *= dropout_z(p.philox_seed, ((uint64_t)h * SQ + qi) * SK + key, p.dropout_p, keep_scale);
-          }
-          pb[2 * jb + sh][e] = (T)pz;
-          if (!kPairSum) (e & 1 ? r1 : r0) += pe;
-        }
-    if (kPairSum) {
-#pragma unroll
-      for (int g = 0; g < C::NG; g++)
-#pragma unroll
-        for (int e = 0; e < 8; e += 4) {
-          r0 = Dt<T>::sum2(typename Dt<T>::V2{pb[g][e], pb[g][e + 1]}, r0);
-          r1 = Dt<T>::sum2(typename Dt<T>::V2{pb[g][e + 2], pb[g][e + 3]}, r1);
-        }
-    }
-    l_run[i] = l_run[i] * corr + (r0 + r1);
-    return corr;
-  };
-  auto active = [&](int t) {
-    const int kb = kstart + t * C::BC;
-    return wave_rows && kb < wk1 && kb + C::BC > wk0;
-  };
-  // FEAT tiles that every row of this wave sees in full (no mask code); chunked attention
-  // always takes the masked path
-  auto interior = [&](int t) {
-    const int kb = kstart + t * C::BC, ke = kb + C::BC - 1;
-    const int r0 = qw + delta, r1 = qw + 32 * QB - 1 + delta;
-    bool ok = ke < SK && p.attn_chunk <= 0;
-    if (CAUSAL) ok = ok && ke <= r0;
-    if (p.win_right >= 0) ok = ok && ke <= r0 + p.win_right;
-    if (p.win_left >= 0) ok = ok && kb >= r1 - p.win_left;
-    return ok;
-  };
-  using Plain = std::integral_constant<bool, false>;
-  using Masked = std::integral_constant<bool, true>;
-  // logit transform of the feature kernels: bit 0 softcap, bit 1 alibi
-  using Cap0 = std::integral_constant<int, 0>;
-  const int fmode = FEAT ? (p.softcap > 0.0f ? 1 : 0) | (p.alibi_slopes ? 2 : 0) : 0;
-  auto with_fmode = [&](auto f) {
-    switch (fmode) {
-      case 1: f(std::integral_constant<int, 1>{}); break;
-      case 2: f(std::integral_constant<int, 2>{}); break;
-      case 3: f(std::integral_constant<int, 3>{}); break;
-      default: f(Cap0{}); break;
-    }
-  };
-
-  // ---- prologue: K tiles 0 and 1, V tile 0 in LDS; S and P of tile 0
-  V8 pb[QB][C::NG];
-  if (ntiles > 0) {
-    gload_k(kstart);
-    gload_v(kstart);
-    lstore_k(0);
-    lstore_v(0);
-    gload_k(kstart + C::BC);
-    lstore_k(1);
-  }
-  __syncthreads();
-  bool a_cur = false;
-  // a pending O rescale (from the softmax of the tile whose PV product comes next) is applied
-  // at the top of the next iteration, so the softmax shares a basic block with the PV product
-  bool resc[QB];
-  float corr[QB];
-#pragma unroll
-  for (int i = 0; i < QB; i++) {
-    resc[i] = false;
-    corr[i] = 1.0f;
-  }
-  auto rescale = [&]() {
-#pragma unroll
-    for (int i = 0; i < QB; i++)
-      if (resc[i]) {
-#pragma unroll
-        for (int db = 0; db < C::NDB; db++) oacc[i][db] *= corr[i];
-        resc[i] = false;
-      }
-  };
-  if (ntiles > 0) {
-    f32x16 s[QB][C::NB];
-    if (nint > 0) {
-      a_cur = true;
-      qk(0, s);
-#pragma unroll
-      for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, Cap0{}, i, s[i], kstart, pb[i], resc[i]);
-    } else if ((a_cur = active(0))) {
-      qk(0, s);
-      with_fmode([&](auto cap) {
-#pragma unroll
-        for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, cap, i, s[i], kstart, pb[i], resc[i]);
-      });
-    }
-  }
-  __syncthreads();  // every wave has read K stage 0 before iteration 0 refills it
-
-  // ---- iteration t: S of tile t+1, PV of tile t, softmax of tile t+1; then K tile t+2 and
-  // V tile t+1 go to the stages tiles t and t-1 used.
-  int t = 0;
-  for (; t + 1 < nint; t++) {
-    rescale();
-    const int kb1 = kstart + (t + 1) * C::BC;
-    gload_k(kb1 + C::BC);
-    gload_v(kb1);
-    f32x16 s[QB][C::NB];
-    __builtin_amdgcn_s_setprio(1);
-    qk((t + 1) & 1, s);
-    __builtin_amdgcn_s_setprio(0);
-    pv(t & 1, pb);
-#pragma unroll
-    for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, Cap0{}, i, s[i], kb1, pb[i], resc[i]);
-    lstore_k(t & 1);
-    lstore_v((t + 1) & 1);
-    __syncthreads();
-  }
-  if (t < ntiles && t > 0) a_cur = active(t);
-  for (; t < ntiles; t++) {
-    rescale();
-    const int kb1 = kstart + (t + 1) * C::BC;
-    gload_k(kb1 + C::BC);
-    gload_v(kb1);
-    const bool a_next = t + 1 < ntiles && active(t + 1);
-    f32x16 s[QB][C::NB];
-    if (a_next) qk((t + 1) & 1, s);
-    if (a_cur) pv(t & 1, pb);
-    if (a_next) {
-      // FEAT tiles every row of the wave sees in full skip the mask code
-      auto sm = [&](auto masked, auto cap) {
-#pragma unroll
-        for (int i = 0; i < QB; i++) corr[i] = softmax(masked, cap, i, s[i], kb1, pb[i], resc[i]);
-      };
-      if (FEAT && interior(t + 1))
-        with_fmode([&](auto cap) { sm(Plain{}, cap); });
-      else
-        with_fmode([&](auto cap) { sm(Masked{}, cap); });
-    }
-    a_cur = a_next;
-    lstore_k(t & 1);
-    lstore_v((t + 1) & 1);
-    __syncthreads();
-  }
-
-  // ---- epilogue: O = acc / l, LSE
-#pragma unroll
-  for (int i = 0; i < QB; i++) {
-    const int qi = qw + 32 * i + l32;
-    const float l_tot = half_sum(l_run[i]);
-    const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    if (qi < SQ) {
-      T* orow = Og + (long long)qi * p.sO.s;
-#pragma unroll
-      for (int db = 0; db < C::NDB; db++)
-#pragma unroll
-        for (int rq = 0; rq < 4; rq++) {
-          V4 v;
-#pragma unroll
-          for (int c = 0; c < 4; c++) v[c] = (T)(oacc[i][db][4 * rq + c] * inv);
-          *(V4*)(orow + db * 32 + 8 * rq + 4 * hh) = v;
-        }
-      if (p.LSE && hh == 0)
-        p.LSE[sv.lse0 + qi] = l_tot > 0.0f ? m_run[i] * kLn2 + __logf(l_tot) : -INFINITY;
-    }
-  }
-}
-
-// C runs the plain masks (causal / sequence end) and wide-window / alibi feature kernels; CF
-// the softcap, dropout and narrow-mask kernels. Dropout has kernels of its own, so its Philox
-// rounds cost the other features no registers.
-template <typename T, class C, class CF = C>
-static int launch_fwd(const FwdParams& p, hipStream_t st) {
-  const bool drop = p.dropout_p > 0.0f;
-  const bool feat = drop || p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
-                    p.win_left >= 0 || (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
-  // CF (128-row workgroups) for softcap and dropout, whose per-score work needs its register
-  // balance, and for narrow masks (a window or chunk under 2048 keys), where most of a 256-row
-  // workgroup's key span would be masked; C (256-row workgroups) otherwise
-  auto narrow = [](int w) { return w >= 0 && w < 2048; };
-  const bool heavy = drop || p.softcap > 0.0f || narrow(p.win_left) || (p.attn_chunk > 0 && p.attn_chunk < 2048) ||
-                     (narrow(p.win_right) && !(p.win_right == 0 && p.causal));
-  const int br = heavy ? CF::BR : C::BR;
-  const int nqt = (p.SQ + br - 1) / br;
-  const long long nblk = (long long)nqt * p.NH * p.batch;
-  if (nblk <= 0) return FA_OK;
-  if (nblk > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fa_forward_launch: grid too large");
-  dim3 grid((unsigned)nblk);
-  auto go = [&](auto causal) {
-    constexpr bool CA = decltype(causal)::value;
-    if (drop)
-      hipLaunchKernelGGL((fwd_kernel<T, CF, CA, true, true>), grid, dim3(CF::NT), 0, st, p, nqt);
-    else if (heavy)
-      hipLaunchKernelGGL((fwd_kernel<T, CF, CA, true>), grid, dim3(CF::NT), 0, st, p, nqt);
-    else if (feat)
-      hipLaunchKernelGGL((fwd_kernel<T, C, CA, true>), grid, dim3(C::NT), 0, st, p, nqt);
-    else
-      hipLaunchKernelGGL((fwd_kernel<T, C, CA, false>), grid, dim3(C::NT), 0, st, p, nqt);
-  };
-  if (p.causal)
-    go(std::integral_constant<bool, true>{});
-  else
-    go(std::integral_constant<bool, false>{});
-  return launch_status("fa_forward_launch");
-}
-
-template <typename T>
-static int dispatch_hd(const FwdParams& p, hipStream_t st) {
+static int dispatch_hd(const FwdParams& p, int dtype, hipStream_t st) {
   switch (p.HD) {
-    case 64: return launch_fwd<T, FwdCfg<64, 64, 8, 2>>(p, st);
-    case 128: return launch_fwd<T, FwdCfg<128, 64, 8, 2>, FwdCfg<128, 32, 4, 2>>(p, st);
-    case 256: return launch_fwd<T, FwdCfg<256, 32, 4, 1>>(p, st);
+    case 64: return launch_fwd_d64(p, dtype, st);
+    case 128: return launch_fwd_d128(p, dtype, st);
+    case 256: return launch_fwd_d256(p, dtype, st);
     default: return fail(FA_ERR_HEADDIM, "fa_forward_launch: head_dim=%d has no kernel (64, 128, 256)", p.HD);
   }
 }
@@ -518,8 +27,8 @@ extern "C" int fa_forward_launch(FwdParams p, int dtype, void* stream) {
   if (!p.cu_q && p.batch <= 0) return FA_OK;
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
-    case FA_F16: return dispatch_hd<_Float16>(p, st);
-    case FA_BF16: return dispatch_hd<__bf16>(p, st);
+    case FA_F16:
+    case FA_BF16: return dispatch_hd(p, dtype, st);
     case FA_F32: return launch_fwd_f32(p, st);
     default: return fail(FA_ERR_DTYPE, "fa_forward_launch: dtype %d not implemented (fp16/bf16/fp32)", dtype);
   }

@@ -1,5 +1,5 @@
 // fwd_common.hpp — the forward's sequence views and mask ranges, shared by the fp16/bf16
-// kernels (fwd.hip) and the fp32 kernels (fwd_f32.hip). Mask contract of the reference
+// kernels (fwd_kernel.hpp) and the fp32 kernels (fwd_f32.hip). Mask contract of the reference
 // (kernels/fa_forward.hip:224-233, FwdParams in include/fable_attn_abi.h).
 #pragma once
 #include "attn_device.hpp"
@@ -76,7 +76,11 @@ __device__ __forceinline__ bool fwd_visible(const FwdParams& p, int i, int j, in
   return ok;
 }
 
-// the fp32 forward (fwd_f32.hip), dispatched from fa_forward_launch
+// the fp16/bf16 forward per head dim (fwd_d64/128/256.hip) and the fp32 forward (fwd_f32.hip),
+// dispatched from fa_forward_launch
+int launch_fwd_d64(const FwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_d128(const FwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_d256(const FwdParams& p, int dtype, hipStream_t st);
 int launch_fwd_f32(const FwdParams& p, hipStream_t st);
 
 }  // namespace fa
