@@ -40,6 +40,14 @@ CASES = [
     ("chunk 128 full", 1, 256, 256, 128, 16, 4, False, -1, -1, 0.0, False, 128),
     ("chunk 64 SQ<SK", 1, 128, 320, 128, 16, 4, True, -1, -1, 0.0, False, 64),
     ("d256 window+softcap (C5 features)", 1, 300, 300, 256, 16, 1, True, 64, 0, 30.0, False, 0),
+    # workgroup shapes of the launcher: wide windows / chunks (>= 2048 keys) and alibi run on the
+    # plain shape's feature kernel, narrow masks on the short shape, softcap on its own shape
+    ("d128 wide window (2100,0)", 1, 2400, 2400, 128, 4, 1, True, 2100, 0, 0.0, False, 0),
+    ("d64 wide window (2050,9) GQA", 1, 2300, 2300, 64, 4, 2, False, 2050, 9, 0.0, False, 0),
+    ("d256 chunk 2048 causal", 1, 2200, 2200, 256, 2, 1, True, -1, -1, 0.0, False, 2048),
+    ("d128 wide window + alibi", 1, 2300, 2300, 128, 4, 1, True, 2048, 0, 0.0, True, 0),
+    ("d128 narrow window + softcap", 1, 300, 300, 128, 8, 2, True, 100, 0, 20.0, False, 0),
+    ("d64 narrow window + alibi", 1, 300, 300, 64, 8, 1, False, 40, 40, 0.0, True, 0),
 ]
 
 
