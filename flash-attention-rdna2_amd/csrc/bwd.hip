@@ -14,8 +14,14 @@
 //     Q/dO tiles (and their LSE/D rows) of every q head sharing the kv head, in a fixed order:
 //     S = Q.K^T and dP = dO.V^T; P and dS stay in registers as B operands of
 //     dV^T += dO^T.P and dK^T += Q^T.dS (dO^T/Q^T by transposing LDS reads).
-// S and dP are computed in both kernels (the price of no atomics, as in the reference).
+// On that recomputing path S and dP are computed in both kernels (the price of no atomics, as in
+// the reference). With a dS workspace (BwdParams.ds_ws, fp16/bf16 at head_dim 64/128) the order
+// is instead: a rowsum kernel for D, the dK/dV kernel, which also stores each dS tile once, and
+// a dQ kernel that forms dQ = dS.K from the stored tiles; every product is computed once, still
+// without atomics and in a fixed order.
 // Probabilities are evaluated as exp2(s*scale*log2e - LSE*log2e).
+#include <utility>
+
 #include "attn_device.hpp"
 #include "bwd_common.hpp"
 #include "status.hpp"
@@ -479,7 +485,7 @@ struct BwdKVPCfg {
   static_assert(CH % NT == 0 && (BQ * DCH) % NT == 0, "loader split");
 };
 
-template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
+template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false, bool DSW = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
 bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
@@ -683,6 +689,14 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
           }
         }
         tprod(qs, pS);  // dK^T += Q^T . dS
+        if constexpr (DSW) {  // dS tile (32 queries x this pair's 32 keys) to the workspace
+          const int hg = t / ntq, qt0 = qstart + (t % ntq) * C::BQ;
+          T* dst = ds_tile<T>(p, b, kvh * p.gqa + hg, kw >> 5, qt0 >> 5) + 16 * l32 + 8 * hh;
+          // streaming stores: the tiles are read once, by the dQ kernel, and must not push the
+          // Q/dO tiles this kernel re-reads out of L2
+          __builtin_nontemporal_store(pS[0], (V8*)dst);
+          __builtin_nontemporal_store(pS[1], (V8*)(dst + 512));
+        }
       }
     }
     lstore(std::integral_constant<int, (S + 1) % NSET>{}, (it + 1) & 3);  // tile it+1
@@ -710,6 +724,266 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   }
 }
 
+// ------------------------------------------------------------ dQ from a dS workspace
+// D = rowsum(O*dO) for every (b, h, q) row: HD/8 lanes per row, one 16-byte chunk each.
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void bwd_dsum_kernel(BwdParams p, int rblocks) {
+  constexpr int LPR = HD / 8, RPB = 256 / LPR;
+  using V8 = typename Dt<T>::V8;
+  const int tid = threadIdx.x;
+  const int rb = blockIdx.x % rblocks, zh = blockIdx.x / rblocks;
+  const int h = zh % p.Hq, b = zh / p.Hq;
+  const BwdSeq sq = bwd_seq(p, b);
+  const int q = rb * RPB + tid / LPR, c = tid % LPR;
+  float acc = 0.0f;
+  if (q < sq.SQ) {
+    const V8 o = *(const V8*)((const T*)p.O + (long long)b * p.os.b + (sq.qo + q) * p.os.s +
+                              (long long)h * p.os.h + 8 * c);
+    const V8 d = *(const V8*)((const T*)p.dO + (long long)b * p.dos.b + (sq.qo + q) * p.dos.s +
+                              (long long)h * p.dos.h + 8 * c);
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc += (float)o[e] * (float)d[e];
+  }
+#pragma unroll
+  for (int m = LPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m);
+  if (c == 0 && q < sq.SQ) p.dsum[(long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + q] = acc;
+}
+
+template <int HD_, int NW_, int WPE_, int NS_>
+struct BwdDsQCfg {
+  static constexpr int HD = HD_, NW = NW_, WPE = WPE_;
+  static constexpr int NS = NS_;       // register sets: K and dS loaded NS-1 tiles ahead
+  static constexpr int NT = NW * 64;
+  static constexpr int BQ = NW * 32;   // queries per workgroup (32 per wave)
+  static constexpr int BC = 64;        // keys per K tile (two workspace tiles)
+  static constexpr int NDB = HD / 32;  // 32-row blocks of dQ^T
+  static constexpr int DCH = HD / 8;
+  static constexpr int KCH = BC * DCH;
+  static constexpr int PER = KCH / NT;
+  static constexpr int KT = BC * HD;
+  static constexpr int DSTR = 32;      // LDS row of a wave's dS block: 32 query slots (64 B)
+  static_assert(KCH % NT == 0, "loader split");
+};
+
+// f(integral_constant<int, I>) for I in the sequence, in order (compile-time register-set index)
+template <int... I, typename F>
+__device__ __forceinline__ void for_sets(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+
+// Element offset of (key row r, query slot n) in a wave's dS block: 64-byte rows of four 16-byte
+// chunks, chunk n/8 stored at position (n/8) ^ (2*r.bit2 + r.bit3). The transposing reads
+// (rows R..R+3 and R+4..R+7 of the two half-waves, R a multiple of 8) then use disjoint chunk
+// pairs, and the 16-byte writes of 16 consecutive rows land in 16 distinct 16-byte slots of a
+// 256-byte bank cycle.
+__device__ __forceinline__ int dsl_ofs(int r, int n) {
+  return r * 32 + 8 * ((n >> 3) ^ (2 * ((r >> 2) & 1) + ((r >> 3) & 1))) + (n & 7);
+}
+
+// dQ^T = K^T . dS^T over the dS tiles the pair kernel wrote for this wave's 32 queries. K tiles
+// are double-buffered through LDS and read transposed (A operand). K and dS tiles are loaded
+// NS-1 K tiles ahead (16-byte loads into NS rotating register sets); the dS chunks are staged in
+// a per-wave LDS block with keys as rows and read back transposed, so each lane gets 8 keys of
+// one query slot (B operand), in the contraction order of the K^T reads. Column n of the product
+// is query slot n, i.e. query ds_slot_query(n). A (key block, query block) tile is read exactly
+// when the pair kernel wrote it: the same query range of the key block, intersected with the
+// wave's rows.
+template <typename T, class C, bool CAUSAL, bool FEAT>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
+                          amdgpu_waves_per_eu(C::WPE, C::WPE))) void
+bwd_dq_ds_kernel(BwdParams p, int nqt) {
+  using V8 = typename Dt<T>::V8;
+  using V4 = typename Dt<T>::V4;
+  __shared__ __attribute__((aligned(16))) T lds[2 * C::KT];
+  __shared__ __attribute__((aligned(16))) T dsl[C::NW][C::BC * C::DSTR];
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
+
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int qti = w % nqt, zh = w / nqt;
+  const int h = zh % p.Hq, b = zh / p.Hq;
+  const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
+  const int kvh = h / p.gqa;
+  const BwdSeq sq = bwd_seq(p, b);
+  const int SQ = sq.SQ, SK = sq.SK, delta = SK - SQ;
+  const int qb = qt * C::BQ;
+  if (qb >= SQ) return;
+
+  const T* Kg = (const T*)p.K + (long long)b * p.ks.b + sq.ko * p.ks.s + (long long)kvh * p.ks.h;
+  T* dQg = (T*)p.dQ + (long long)b * p.dqs.b + sq.qo * p.dqs.s + (long long)h * p.dqs.h;
+  const int qw = qb + 32 * wave;
+  const bool wave_rows = qw < SQ;
+  int bk0, bk1;
+  key_range_b<CAUSAL, FEAT>(p, qb, min(qb + C::BQ, SQ) - 1, delta, SK, bk0, bk1);
+  const int kstart = (bk0 / C::BC) * C::BC;
+  const int ntiles = bk1 > bk0 ? (bk1 - kstart + C::BC - 1) / C::BC : 0;
+
+  // the pair kernel wrote tile (key block kb32, this wave's query block) iff it is inside the
+  // key range, and the queries that see some key of the block meet the wave's rows
+  auto written = [&](int kb32) {
+    const int k0 = 32 * kb32;
+    if (!wave_rows || k0 >= SK) return false;
+    int q0, q1;
+    query_range_b<CAUSAL, FEAT>(p, k0, min(k0 + 32, SK) - 1, delta, SQ, q0, q1);
+    return qw < q1 && qw + 32 > q0;
+  };
+  // Loads are issued unconditionally (from a clamped tile address when the tile was not written;
+  // such data is never used), so the memory waits stay exact and the prefetch stays in flight.
+  const int nqb = (p.SQ + 31) >> 5, nkb = (p.SK + 31) >> 5;
+  const T* dsw = ds_tile<T>(p, b, h, 0, min(qw >> 5, nqb - 1)) + 16 * l32 + 8 * hh;
+  const long long kstep = (long long)nqb * 1024;  // elements between key blocks
+  constexpr int NS = C::NS;
+  V8 dsr[NS][4];  // [register set][key block jb, query half sh] chunks of one K tile
+  bool dact[NS][2];
+  auto dsload = [&](auto set, int t) {
+    constexpr int S = decltype(set)::value;
+    const int kb = kstart + t * C::BC;
+#pragma unroll
+    for (int jb = 0; jb < 2; jb++) {
+      const int kb32 = (kb >> 5) + jb;
+      dact[S][jb] = t < ntiles && written(kb32);
+      const T* src = dsw + min(kb32, nkb - 1) * kstep;
+      dsr[S][2 * jb] = __builtin_nontemporal_load((const V8*)src);
+      dsr[S][2 * jb + 1] = __builtin_nontemporal_load((const V8*)(src + 512));
+    }
+  };
+
+  int voff[C::PER];
+#pragma unroll
+  for (int j = 0; j < C::PER; j++) {
+    const int idx = tid + j * C::NT, r = idx / C::DCH, c = idx % C::DCH;
+    voff[j] = r * (int)(p.ks.s * 2) + 16 * c;
+  }
+  u32x4 ld[NS][C::PER];
+  auto gload = [&](auto set, int t) {
+    constexpr int S = decltype(set)::value;
+    const int kb = kstart + t * C::BC;  // past the last tile the descriptor is empty: zeros
+    const auto rs = buf_rsrc(Kg + (long long)kb * p.ks.s, (long long)(SK - kb) * p.ks.s * 2);
+#pragma unroll
+    for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(rs, voff[j]);
+  };
+  auto lstore = [&](auto set, int stage) {
+    constexpr int S = decltype(set)::value;
+    T* base = lds + stage * C::KT;
+#pragma unroll
+    for (int j = 0; j < C::PER; j++) {
+      const int idx = tid + j * C::NT, r = idx / C::DCH, c = idx % C::DCH;
+      *(u32x4*)(base + bofs<C::HD>(r, c)) = ld[S][j];
+    }
+  };
+
+  f32x16 dqacc[C::NDB];
+#pragma unroll
+  for (int db = 0; db < C::NDB; db++) dqacc[db] = f32x16{};
+  T* my = dsl[wave];
+  // tile t: K in LDS stage t&1, dS in register set S; tile t+1 goes from set (S+1)%NS to LDS,
+  // tile t+NS-1 is loaded into set (S+NS-1)%NS
+  auto step = [&](auto set, int t) {
+    constexpr int S = decltype(set)::value;
+    gload(std::integral_constant<int, (S + NS - 1) % NS>{}, t + NS - 1);
+    dsload(std::integral_constant<int, (S + NS - 1) % NS>{}, t + NS - 1);
+    // this wave's dS chunks (key rows 32jb + l32, query slots 16sh + 8hh ..) into its LDS block
+#pragma unroll
+    for (int jb = 0; jb < 2; jb++)
+#pragma unroll
+      for (int sh = 0; sh < 2; sh++) *(V8*)(my + dsl_ofs(32 * jb + l32, 16 * sh + 8 * hh)) = dsr[S][2 * jb + sh];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const T* ks = lds + (t & 1) * C::KT;
+#pragma unroll
+    for (int jb = 0; jb < 2; jb++) {
+      if (!dact[S][jb]) continue;
+#pragma unroll
+      for (int g2 = 0; g2 < 2; g2++) {
+        const int g = 2 * jb + g2;
+        // B: keys 16g + 8(e/4) + 4hh + e%4 (e = 0..7) of query slot l32
+        V8 bop;
+        {
+          const int row = 16 * g + 4 * hh + (j16 >> 2), col = 16 * mh + 4 * (j16 & 3);
+          const V4 lo = lds_read_tr<T>(my + dsl_ofs(row, col)), hi = lds_read_tr<T>(my + dsl_ofs(row + 8, col));
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            bop[e] = lo[e];
+            bop[4 + e] = hi[e];
+          }
+        }
+#pragma unroll
+        for (int db = 0; db < C::NDB; db++) {
+          // A: K^T, head-dim 32db + l32, the same keys
+          const int col = 32 * db + 16 * mh + 4 * (j16 & 3);
+          V4 part[2];
+#pragma unroll
+          for (int a = 0; a < 2; a++) {
+            const int row = 16 * g + 8 * a + 4 * hh + (j16 >> 2);
+            part[a] = lds_read_tr<T>(ks + bofs<C::HD>(row, col >> 3) + (col & 7));
+          }
+          V8 av;
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            av[e] = part[0][e];
+            av[4 + e] = part[1][e];
+          }
+          dqacc[db] = Dt<T>::mma32(av, bop, dqacc[db]);
+        }
+      }
+    }
+    lstore(std::integral_constant<int, (S + 1) % NS>{}, (t + 1) & 1);
+    __syncthreads();
+  };
+
+  if (ntiles > 0) {
+    for_sets(std::make_integer_sequence<int, NS - 1>{}, [&](auto set) {
+      gload(set, decltype(set)::value);
+      dsload(set, decltype(set)::value);
+    });
+    lstore(std::integral_constant<int, 0>{}, 0);
+  }
+  __syncthreads();
+  // whole groups of NS steps (a step past the last tile multiplies nothing): no branch around a
+  // step, so the waits for each register set's loads are exact
+  for (int t = 0; t < ntiles; t += NS)
+    for_sets(std::make_integer_sequence<int, NS>{}, [&](auto set) { step(set, t + decltype(set)::value); });
+  const int qi = qw + ds_slot_query(l32);
+  if (qi < SQ) {
+    T* row = dQg + (long long)qi * p.dqs.s;
+#pragma unroll
+    for (int db = 0; db < C::NDB; db++)
+#pragma unroll
+      for (int rq = 0; rq < 4; rq++) {
+        V4 v;
+#pragma unroll
+        for (int c = 0; c < 4; c++) v[c] = (T)(dqacc[db][4 * rq + c] * p.scale);
+        *(V4*)(row + 32 * db + 8 * rq + 4 * hh) = v;
+      }
+  }
+}
+
+#ifndef DSQ_NS
+#define DSQ_NS 3
+#endif
+// bytes of dS workspace for the fp16/bf16 path (2-byte elements)
+static long long ds_bytes(const BwdParams& p) {
+  return p.SQ > 0 && p.SK > 0 ? (long long)p.B * p.Hq * ds_tiles_per_head(p.SQ, p.SK) * 2048 : 0;
+}
+
+// backward through the dS workspace: D rows, then dK/dV (writing dS), then dQ = dS.K
+template <typename T, class CKV, bool CAUSAL, bool FEAT, bool DROP>
+static int launch_bwd_ds(const BwdParams& p, hipStream_t st, int nkt) {
+  using CD = BwdDsQCfg<CKV::HD, 8, 2, DSQ_NS>;
+  constexpr int RPB = 256 / (CKV::HD / 8);
+  const long long gd = (long long)((p.SQ + RPB - 1) / RPB) * p.Hq * p.B;
+  const int nqt = (p.SQ + CD::BQ - 1) / CD::BQ;
+  const long long gq = (long long)nqt * p.Hq * p.B;
+  const long long gkv = (long long)nkt * p.Hk * p.B;
+  if (gd > 0x7FFFFFFF || gq > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_backward_launch: grid too large");
+  hipLaunchKernelGGL((bwd_dsum_kernel<T, CKV::HD>), dim3((unsigned)gd), dim3(256), 0, st, p, (p.SQ + RPB - 1) / RPB);
+  if (int rc = launch_status("fable_attn_backward_launch (dsum)")) return rc;
+  hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
+  if (int rc = launch_status("fable_attn_backward_launch (dkdv)")) return rc;
+  hipLaunchKernelGGL((bwd_dq_ds_kernel<T, CD, CAUSAL, FEAT>), dim3((unsigned)gq), dim3(CD::NT), 0, st, p, nqt);
+  return launch_status("fable_attn_backward_launch (dq)");
+}
+
 template <typename T, class CQ, class CKV, bool CAUSAL, bool FEAT, bool DROP = false>
 static int launch_bwd2(const BwdParams& p, hipStream_t st) {
   const int nqt = (p.SQ + CQ::BQ - 1) / CQ::BQ;
@@ -717,6 +991,10 @@ static int launch_bwd2(const BwdParams& p, hipStream_t st) {
   const long long gq = (long long)nqt * p.Hq * p.B * CQ::DSPLIT;
   const long long gkv = (long long)nkt * p.Hk * p.B * CKV::DSPLIT;
   if (gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_backward_launch: grid too large");
+  if constexpr (CKV::PAIR) {
+    const long long need = ds_bytes(p);
+    if (p.ds_ws && need > 0 && p.ds_ws_bytes >= need) return launch_bwd_ds<T, CKV, CAUSAL, FEAT, DROP>(p, st, nkt);
+  }
   if (gq > 0) {
     hipLaunchKernelGGL((bwd_dq_kernel<T, CQ, CAUSAL, FEAT, DROP>), dim3((unsigned)gq), dim3(CQ::NT), 0, st, p, nqt);
     if (int rc = launch_status("fable_attn_backward_launch (dq)")) return rc;
@@ -754,6 +1032,11 @@ static int bwd_dispatch(const BwdParams& p, hipStream_t st) {
 }
 
 }  // namespace fa
+
+extern "C" int64_t fable_attn_bwd_ds_bytes(BwdParams p, int dtype) {
+  if ((dtype != FA_F16 && dtype != FA_BF16) || (p.D != 64 && p.D != 128) || p.B <= 0 || p.Hq <= 0) return 0;
+  return fa::ds_bytes(p);
+}
 
 extern "C" int fable_attn_backward_launch(BwdParams p, int dtype, void* stream) {
   using namespace fa;

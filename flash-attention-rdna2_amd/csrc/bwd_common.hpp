@@ -85,6 +85,26 @@ __device__ __forceinline__ BwdSeq bwd_seq(const BwdParams& p, int b) {
   return s;
 }
 
+// With a dS workspace the pair kernel stores each dS tile it computes (32 queries x 32 keys,
+// 2 KiB) and dQ = dS.K is one product per tile, instead of recomputing S, P and dP.
+// Workspace layout: tile (b, h, kb32, qb32) at ((b*Hq + h)*nkb + kb32)*nqb + qb32 (in 1024-element
+// tiles; nkb = ceil(SK/32), nqb = ceil(SQ/32) of the longest sequence). A tile is the pair
+// kernel's register layout, written with two 16-byte stores per lane: half sh (512 elements)
+// holds, for key k, the 16 query slots 16*k .. 16*k+15, and slot 8*hh + e is query
+// 16*sh + 8*(e/4) + 4*hh + e%4 (the MFMA C-row order of the S = Q.K^T product). Slot n of the
+// 32 in a tile (n = 16*sh + 8*hh + e) is therefore query ds_slot_query(n).
+__host__ __device__ inline long long ds_tiles_per_head(int SQ, int SK) {
+  return (long long)((SK + 31) >> 5) * ((SQ + 31) >> 5);
+}
+template <typename T>
+__device__ __forceinline__ T* ds_tile(const BwdParams& p, int b, int h, int kb32, int qb32) {
+  const long long nqb = (p.SQ + 31) >> 5, nkb = (p.SK + 31) >> 5;
+  return (T*)p.ds_ws + ((((long long)b * p.Hq + h) * nkb + kb32) * nqb + qb32) * 1024;
+}
+__device__ __forceinline__ int ds_slot_query(int n) {
+  return 16 * (n >> 4) + 8 * ((n >> 2) & 1) + 4 * ((n >> 3) & 1) + (n & 3);
+}
+
 // the fp32 backward (bwd_f32.hip), dispatched from fable_attn_backward_launch
 int launch_bwd_f32(const BwdParams& p, hipStream_t st);
 

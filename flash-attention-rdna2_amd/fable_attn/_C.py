@@ -5,9 +5,10 @@ bound at :239-268) with the same names, argument order and meaning:
     fwd(q, k, v, scale, causal, win_left, win_right, softcap, alibi, dropout_p, seed,
         attn_chunk=0, out=None) -> (out, lse)
     bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, alibi,
-        dropout_p, seed) -> (dq, dk, dv)
+        dropout_p, seed, ds_max_bytes=None) -> (dq, dk, dv)
     bwd_varlen(dout, q, k, v, out, lse, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left,
-               win_right, softcap, alibi, dropout_p, seed, seqused_q=None, seqused_k=None)
+               win_right, softcap, alibi, dropout_p, seed, seqused_q=None, seqused_k=None,
+               ds_max_bytes=None)
         -> (dq, dk, dv)   (no counterpart in the reference's _C: native varlen backward)
     fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win_right,
                softcap, alibi, dropout_p, seed, attn_chunk=0, seqused_q=None,
@@ -19,8 +20,15 @@ bound at :239-268) with the same names, argument order and meaning:
 Tensor checks raise RuntimeError as TORCH_CHECK does there. torch only allocates outputs and
 workspaces and supplies the current stream; all compute is in libfable_attn_hip.so. There is
 no fallback: if the library is missing, importing this module raises ImportError.
+
+Backward dS workspace: for fp16/bf16 at head_dim 64/128 the backward can store dS once and
+form dQ = dS.K from it (BwdParams.ds_ws) instead of recomputing S and dP in its dQ kernel. The
+workspace is B*Hq*SQ*SK*2 bytes (rounded up to 32x32 tiles); bwd/bwd_varlen allocate it when it
+is at most `ds_max_bytes` (default BWD_DS_MAX_BYTES, 4 GiB, or the environment variable
+FABLE_ATTN_BWD_DS_MAX_BYTES). Both paths give the same gradients to rounding.
 """
 import ctypes
+import os
 
 import torch
 
@@ -28,6 +36,20 @@ from . import _lib
 from ._lib import BwdParams, CombineParams, DecParams, FwdParams, Strides
 
 _L = _lib.load()
+
+BWD_DS_MAX_BYTES = int(os.environ.get("FABLE_ATTN_BWD_DS_MAX_BYTES", 4 << 30))
+
+
+def _ds_workspace(p, dtype, device, ds_max_bytes):
+    """Attach a dS workspace to BwdParams p when the library has a path for it and it fits the
+    cap; returns the tensor (kept alive by the caller until the launch is enqueued)."""
+    cap = BWD_DS_MAX_BYTES if ds_max_bytes is None else int(ds_max_bytes)
+    need = int(_L.fable_attn_bwd_ds_bytes(p, dtype))
+    if need <= 0 or need > cap:
+        return None
+    ws = torch.empty(need, dtype=torch.uint8, device=device)
+    p.ds_ws, p.ds_ws_bytes = ws.data_ptr(), need
+    return ws
 
 
 def _req(cond, msg):
@@ -153,7 +175,7 @@ def fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win
 
 
 def bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, alibi, dropout_p,
-        seed):
+        seed, ds_max_bytes=None):
     """All tensors [B,H,S,D] views (D contiguous); lse [B,Hq,SQ] fp32. Returns (dq, dk, dv)
     with the (B,S,H,D)-dense memory of the public API, viewed as [B,H,S,D].
     Reference: dispatch.cpp:83-111 (no bf16 .item() host syncs here)."""
@@ -182,13 +204,15 @@ def bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, al
     p.drop_seed, p.dropout_p = int(seed) & ((1 << 64) - 1), float(dropout_p)
     p.keep_scale = 1.0 / (1.0 - dropout_p) if dropout_p > 0 else 1.0
     p.lse_sb, p.lse_sh = Hq * SQ, SQ
+    ws = _ds_workspace(p, _dt(q), q.device, ds_max_bytes)  # noqa: F841  (alive through the launch)
     with torch.cuda.device(q.device):
         _lib.check(_L.fable_attn_backward_launch(p, _dt(q), _stream(q)), "fable_attn_backward_launch")
     return dq, dk, dv
 
 
 def bwd_varlen(dout, q, k, v, out, lse, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left,
-               win_right, softcap, alibi, dropout_p, seed, seqused_q=None, seqused_k=None):
+               win_right, softcap, alibi, dropout_p, seed, seqused_q=None, seqused_k=None,
+               ds_max_bytes=None):
     """Packed variable-length backward: dout/q/out (total_q, Hq, D), k/v (total_k, Hk, D),
     cu_* int32 [batch+1], lse [Hq, total_q] fp32 (fwd_varlen(..., return_lse=True)). One launch
     of each backward kernel for all sequences; the reference has none and loops over the
@@ -227,6 +251,7 @@ def bwd_varlen(dout, q, k, v, out, lse, cu_q, cu_k, max_sq, max_sk, scale, causa
     p.seqused_q = seqused_q.data_ptr() if seqused_q is not None else None
     p.seqused_k = seqused_k.data_ptr() if seqused_k is not None else None
     p.lse_sb, p.lse_sh = 0, q.shape[0]
+    ws = _ds_workspace(p, _dt(q), q.device, ds_max_bytes)  # noqa: F841  (alive through the launch)
     with torch.cuda.device(q.device):
         _lib.check(_L.fable_attn_backward_launch(p, _dt(q), _stream(q)), "fable_attn_backward_launch (varlen)")
     return dq, dk, dv

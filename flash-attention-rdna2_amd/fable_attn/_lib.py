@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(_HERE, "libfable_attn_hip.so")
 FA_F16, FA_BF16, FA_F32 = 0, 1, 2
 FA_OK = 0
 
-ABI_VERSION = 2  # FABLE_ATTN_ABI_VERSION of include/fable_attn_abi.h
+ABI_VERSION = 3  # FABLE_ATTN_ABI_VERSION of include/fable_attn_abi.h
 
 c_i32, c_i64, c_u64, c_f32, c_ptr = (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64,
                                      ctypes.c_float, ctypes.c_void_p)
@@ -47,7 +47,8 @@ class BwdParams(ctypes.Structure):
                 ("alibi", c_ptr), ("causal", c_i32), ("win_left", c_i32), ("win_right", c_i32),
                 ("dropout", c_i32), ("drop_seed", c_u64), ("dropout_p", c_f32),
                 ("keep_scale", c_f32), ("cu_q", c_ptr), ("cu_k", c_ptr), ("seqused_q", c_ptr),
-                ("seqused_k", c_ptr), ("lse_sb", c_i64), ("lse_sh", c_i64)]
+                ("seqused_k", c_ptr), ("lse_sb", c_i64), ("lse_sh", c_i64),
+                ("ds_ws", c_ptr), ("ds_ws_bytes", c_i64)]
 
 
 class DecParams(ctypes.Structure):
@@ -72,8 +73,8 @@ STRUCTS = {0: FwdParams, 1: BwdParams, 2: DecParams, 3: CombineParams, 4: Stride
 
 # exported symbols of libfable_attn_hip.so (the C-ABI surface)
 EXPORTS = ("fa_forward_launch", "fable_attn_backward_launch", "fa_decode_launch",
-           "fa_decode_num_splits", "fa_combine_launch", "fable_attn_abi_version",
-           "fable_attn_struct_size", "fable_attn_last_error")
+           "fa_decode_num_splits", "fa_combine_launch", "fable_attn_bwd_ds_bytes",
+           "fable_attn_abi_version", "fable_attn_struct_size", "fable_attn_last_error")
 
 _lib = None
 
@@ -96,6 +97,8 @@ def load():
     for f in ("fa_forward_launch", "fable_attn_backward_launch", "fa_decode_launch",
               "fa_decode_num_splits", "fa_combine_launch", "fable_attn_abi_version"):
         getattr(lib, f).restype = c_i32
+    lib.fable_attn_bwd_ds_bytes.argtypes = [BwdParams, c_i32]
+    lib.fable_attn_bwd_ds_bytes.restype = c_i64
     lib.fable_attn_struct_size.argtypes = [c_i32]
     lib.fable_attn_struct_size.restype = ctypes.c_size_t
     lib.fable_attn_last_error.restype = ctypes.c_char_p

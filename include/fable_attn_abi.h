@@ -27,7 +27,9 @@
  *     consumes bf16 natively, so no host-side `.item()` synchronisation is needed;
  *   - the forward writes LSE for every batch element in one launch (lse_sb/lse_sh strides), so
  *     the host no longer loops over the batch (reference dispatch.cpp:61-78), and the varlen
- *     forward can return LSE too (the reference passed LSE=nullptr, dispatch.cpp:139).
+ *     forward can return LSE too (the reference passed LSE=nullptr, dispatch.cpp:139);
+ *   - the backward takes packed variable-length batches natively (cu_q/cu_k, ABI version 2)
+ *     and an optional dS workspace that removes the dQ kernel's recomputation (ABI version 3).
  */
 #ifndef FABLE_ATTN_ABI_H
 #define FABLE_ATTN_ABI_H
@@ -39,7 +41,7 @@
 extern "C" {
 #endif
 
-#define FABLE_ATTN_ABI_VERSION 2
+#define FABLE_ATTN_ABI_VERSION 3
 
 /* dtype codes, same values as the reference (fa_forward.hip:403, backward.hip:25) */
 enum { FA_F16 = 0, FA_BF16 = 1, FA_F32 = 2 };
@@ -133,6 +135,12 @@ typedef struct BwdParams {
   const int32_t* seqused_q;
   const int32_t* seqused_k;
   int64_t lse_sb, lse_sh;
+  /* dS workspace (no reference counterpart; ABI version 3). When ds_ws is set and ds_ws_bytes
+   * >= fable_attn_bwd_ds_bytes(p, dtype) > 0, the dK/dV kernel writes every dS tile it computes
+   * once, and dQ = dS.K becomes one product per tile; otherwise a dQ kernel recomputes S and
+   * dP. Device memory, any contents on entry, scratch on exit. */
+  void* ds_ws;
+  int64_t ds_ws_bytes;
 } BwdParams;
 
 /* Paged-KV decode parameters. Reference: fa_iface.h:42-63 / fa_decode.hip:13-35.
@@ -190,6 +198,11 @@ int fa_forward_launch(FwdParams p, int dtype, void* stream);
 
 /* replaces fa_iface.h:66  void fable_attn_backward_launch(BwdParams pr, int MODE, void* stream) */
 int fable_attn_backward_launch(BwdParams p, int dtype, void* stream);
+
+/* Bytes of BwdParams.ds_ws the backward can use for these shapes (0: this head dim / dtype has
+ * no dS-workspace path). No reference counterpart: the reference backward recomputes dS in its
+ * dQ kernel (backward.hip:298-387). Size B*Hq*ceil(SQ/32)*ceil(SK/32)*2 KiB for fp16/bf16. */
+int64_t fable_attn_bwd_ds_bytes(BwdParams p, int dtype);
 
 /* replaces fa_iface.h:67-68  void fa_decode_launch(DecParams p, int dtype, void* stream,
  *                                                  const void* new_k, const void* new_v)

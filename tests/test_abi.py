@@ -15,7 +15,7 @@ HEADER = os.path.join(ROOT, "include", "fable_attn_abi.h")
 def _declared_functions():
     src = open(HEADER).read()
     src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
-    return sorted(set(re.findall(r"^\s*(?:int|size_t|const char\*)\s+(\w+)\s*\(", src, flags=re.M)))
+    return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(\w+)\s*\(", src, flags=re.M)))
 
 
 def _offsets_from_gcc(tmp_path):
@@ -56,7 +56,7 @@ def test_library_exports_every_declared_function():
     assert set(declared) == set(_lib.EXPORTS), declared
     for f in declared:
         assert hasattr(lib, f), f
-    assert lib.fable_attn_abi_version() == _lib.ABI_VERSION == 2
+    assert lib.fable_attn_abi_version() == _lib.ABI_VERSION == 3
     for k, st in _lib.STRUCTS.items():
         assert lib.fable_attn_struct_size(k) == ctypes.sizeof(st)
 
@@ -89,3 +89,21 @@ def test_decode_split_plan(hint, expect):
         assert n == expect
     else:
         assert 1 <= n <= 512
+
+
+def test_bwd_ds_workspace_size():
+    """fable_attn_bwd_ds_bytes: 2 KiB per (32-query, 32-key) tile of every (batch, q head) for
+    the fp16/bf16 head dims with a dS-workspace path (64, 128); 0 elsewhere (host-only call)."""
+    from fable_attn import _lib
+    lib = _lib.load()
+    p = _lib.BwdParams()
+    p.B, p.Hq, p.Hk, p.gqa, p.SQ, p.SK, p.D = 2, 8, 2, 4, 100, 65, 128
+    want = 2 * 8 * 4 * 3 * 2048
+    assert lib.fable_attn_bwd_ds_bytes(p, 0) == want and lib.fable_attn_bwd_ds_bytes(p, 1) == want
+    p.D = 64
+    assert lib.fable_attn_bwd_ds_bytes(p, 1) == want
+    assert lib.fable_attn_bwd_ds_bytes(p, 2) == 0      # fp32 recomputes
+    p.D = 256
+    assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0
+    p.D, p.SQ = 128, 0
+    assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0

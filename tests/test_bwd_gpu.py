@@ -9,6 +9,10 @@ P and dS matrices and are stored in fp16/bf16, so their floor is above the forwa
 bitwise-identical results across repeated runs (the atomic-free contract). At the full
 BASELINE.json configs[2] size the kernel is checked against a float32 torch autograd
 reference on the GPU for sampled heads, and for bitwise reproducibility over 3 runs.
+
+Every case runs both backward paths at head_dim 64/128: "ds" (the dK/dV kernel stores dS in a
+workspace and dQ = dS.K is formed from it, the default) and "recompute" (no workspace: the dQ
+kernel recomputes S and dP); head_dim 256 has the recomputing path only.
 """
 import math
 
@@ -43,7 +47,10 @@ CASES = [
 ]
 
 
-def run(case, dt, seed=0, repeats=1):
+PATHS = {"ds": None, "recompute": 0}  # ds_max_bytes of _C.bwd
+
+
+def run(case, dt, seed=0, repeats=1, path="ds"):
     import torch
 
     from fable_attn import _C
@@ -59,18 +66,19 @@ def run(case, dt, seed=0, repeats=1):
     qd, kd, vd, dod = view(q), view(k), view(v), view(do)
     ald = torch.from_numpy(al).cuda() if al is not None else None
     out, lse = _C.fwd(qd, kd, vd, scale, causal, wl, wr, sc, ald, 0.0, 0)
-    res = [_C.bwd(dod, qd, kd, vd, out, lse, scale, causal, wl, wr, sc, ald, 0.0, 0)
-           for _ in range(repeats)]
+    res = [_C.bwd(dod, qd, kd, vd, out, lse, scale, causal, wl, wr, sc, ald, 0.0, 0,
+                  ds_max_bytes=PATHS[path]) for _ in range(repeats)]
     torch.cuda.synchronize()
     ref = orc.bwd(q, k, v, do, scale, causal, wl, wr, sc, al)
     return res, ref
 
 
+@pytest.mark.parametrize("path", list(PATHS))
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_backward_parity(case, dt):
-    print(f"[bwd] {case[0]} {dt}", flush=True)
-    res, ref = run(case, dt, repeats=3)
+def test_backward_parity(case, dt, path):
+    print(f"[bwd] {case[0]} {dt} {path}", flush=True)
+    res, ref = run(case, dt, repeats=3, path=path)
     for i, name in enumerate(("dq", "dk", "dv")):
         got = to_np(res[0][i])
         assert np.isfinite(got).all(), f"{name} not finite"
@@ -85,7 +93,8 @@ def torch_equal(a, b):
     return bool(torch.equal(a, b))
 
 
-def test_backward_full_config_c3():
+@pytest.mark.parametrize("path", list(PATHS))
+def test_backward_full_config_c3(path):
     """causal bf16, B=2, S=4096, H=32, D=128; bitwise identical over
     3 runs; sampled heads against a float32 torch autograd reference on the GPU."""
     import torch
@@ -99,7 +108,9 @@ def test_backward_full_config_c3():
     qh, kh, vh, doh = (_kernel_view(x) for x in (q, k, v, do))
     scale = D ** -0.5
     out, lse = _C.fwd(qh, kh, vh, scale, True, -1, 0, 0.0, None, 0.0, 0)
-    runs = [_C.bwd(doh, qh, kh, vh, out, lse, scale, True, -1, 0, 0.0, None, 0.0, 0) for _ in range(3)]
+    print(f"[bwd] C3 full size {path}", flush=True)
+    runs = [_C.bwd(doh, qh, kh, vh, out, lse, scale, True, -1, 0, 0.0, None, 0.0, 0,
+                   ds_max_bytes=PATHS[path]) for _ in range(3)]
     torch.cuda.synchronize()
     for r in runs[1:]:
         for a, b in zip(runs[0], r):

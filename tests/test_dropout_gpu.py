@@ -118,20 +118,22 @@ def test_forward_dropout_vs_oracle(case, dt):
     assert inf_ok and le <= LSE_ABS, f"LSE err {le:.3e}"
 
 
+@pytest.mark.parametrize("ds_max", [None, 0], ids=["ds", "recompute"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_backward_dropout_vs_oracle(case, dt):
+def test_backward_dropout_vs_oracle(case, dt, ds_max):
+    """Both backward paths (dS workspace, or the dQ kernel recomputing dS) against the oracle."""
     import torch
 
     from fable_attn import _C
-    print(f"[dropout-bwd] {case[0]} {dt}", flush=True)
+    print(f"[dropout-bwd] {case[0]} {dt} ds_max={ds_max}", flush=True)
     name, B, Hq, Hk, SQ, SK, D, causal, p, sc = case
     q, k, v, do = _inputs(case, dt, seed=10)
     scale = 1.0 / math.sqrt(D)
     qd, kd, vd, dod = (_view(x, dt) for x in (q, k, v, do))
     out, lse = _C.fwd(qd, kd, vd, scale, causal, -1, -1, sc, None, p, SEED)
-    g1 = _C.bwd(dod, qd, kd, vd, out, lse, scale, causal, -1, -1, sc, None, p, SEED)
-    g2 = _C.bwd(dod, qd, kd, vd, out, lse, scale, causal, -1, -1, sc, None, p, SEED)
+    g1 = _C.bwd(dod, qd, kd, vd, out, lse, scale, causal, -1, -1, sc, None, p, SEED, ds_max_bytes=ds_max)
+    g2 = _C.bwd(dod, qd, kd, vd, out, lse, scale, causal, -1, -1, sc, None, p, SEED, ds_max_bytes=ds_max)
     torch.cuda.synchronize()
     ref = orc.bwd(q, k, v, do, scale, causal, -1, -1, sc, None, dropout_p=p, seed=SEED)
     for i, gname in enumerate(("dq", "dk", "dv")):

@@ -51,7 +51,7 @@ def _make(case, dt, seed=0):
     return lq, lk, q, k, v, do
 
 
-def _varlen_kernel(case, dt, lq, lk, q, k, v, do, su_q=None, su_k=None):
+def _varlen_kernel(case, dt, lq, lk, q, k, v, do, su_q=None, su_k=None, ds_max=None):
     import torch
 
     from fable_attn import _C
@@ -65,22 +65,25 @@ def _varlen_kernel(case, dt, lq, lk, q, k, v, do, su_q=None, su_k=None):
     out, lse = _C.fwd_varlen(qd, kd, vd, cq, ck, max(lq), max(lk), scale, causal, wl, wr, sc,
                              None, 0.0, 0, 0, uq, uk, return_lse=True)
     grads = _C.bwd_varlen(dod, qd, kd, vd, out, lse, cq, ck, max(lq), max(lk), scale, causal,
-                          wl, wr, sc, None, 0.0, 0, uq, uk)
+                          wl, wr, sc, None, 0.0, 0, uq, uk, ds_max_bytes=ds_max)
     torch.cuda.synchronize()
     return grads
 
 
+@pytest.mark.parametrize("ds_max", [None, 0], ids=["ds", "recompute"])
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_varlen_backward_vs_oracle_and_dense(case, dt):
+def test_varlen_backward_vs_oracle_and_dense(case, dt, ds_max):
+    """Both backward paths (dS workspace / recomputing dQ kernel); the dense comparison uses
+    the same path."""
     import torch
 
     from fable_attn import _C
-    print(f"[varlen-bwd] {case[0]} {dt}", flush=True)
+    print(f"[varlen-bwd] {case[0]} {dt} ds_max={ds_max}", flush=True)
     _, _, _, Hq, Hk, D, causal, wl, wr, sc = case
     lq, lk, q, k, v, do = _make(case, dt)
-    dq, dk, dv = _varlen_kernel(case, dt, lq, lk, q, k, v, do)
-    again = _varlen_kernel(case, dt, lq, lk, q, k, v, do)
+    dq, dk, dv = _varlen_kernel(case, dt, lq, lk, q, k, v, do, ds_max=ds_max)
+    again = _varlen_kernel(case, dt, lq, lk, q, k, v, do, ds_max=ds_max)
     for a, b in zip((dq, dk, dv), again):
         assert torch.equal(a, b), "varlen backward differs between runs"
     cq, ck = _cu(lq), _cu(lk)
@@ -105,7 +108,7 @@ def test_varlen_backward_vs_oracle_and_dense(case, dt):
         view = lambda x, dtp=dt: to_dev(x, dtp)[None].transpose(1, 2)
         qs, ks, vs, dos = view(q[a:b]), view(k[c:d]), view(v[c:d]), view(do[a:b])
         o1, l1 = _C.fwd(qs, ks, vs, scale, causal, wl, wr, sc, None, 0.0, 0)
-        g1 = _C.bwd(dos, qs, ks, vs, o1, l1, scale, causal, wl, wr, sc, None, 0.0, 0)
+        g1 = _C.bwd(dos, qs, ks, vs, o1, l1, scale, causal, wl, wr, sc, None, 0.0, 0, ds_max_bytes=ds_max)
         torch.cuda.synchronize()
         for name, got, dense, lo, hi in (("dq", dq, g1[0], a, b), ("dk", dk, g1[1], c, d),
                                          ("dv", dv, g1[2], c, d)):
