@@ -456,6 +456,12 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
   }
 }
 
+// f(integral_constant<int, I>) for I in the sequence, in order (compile-time register-set index)
+template <int... I, typename F>
+__device__ __forceinline__ void for_sets(std::integer_sequence<int, I...>, F&& f) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+
 // ------------------------------------------------------------------- dK, dV with wave pairs
 // Each 32-key block belongs to a pair of waves on the same SIMD slot pattern (wave w and w+NP):
 // the S-wave holds K and computes S = Q K^T, P, and dV += dO^T P; the dP-wave holds V and, one
@@ -561,11 +567,10 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
     for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(j < C::QJ ? rq : rd, voff[j]);
     const int q = qt0 + (rsel % C::BQ);
     lok[S] = it < total && q < SQ;
-    lraw[S] = 0.0f;
-    if (it < total) {  // (uniform) the loop runs past the last tile; SQ may be 0
-      const long long ri = (long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + min(q, SQ - 1);
-      lraw[S] = rsel < C::BQ ? p.lse[ri] : p.dsum[ri];
-    }
+    // unconditional (clamped row; SQ >= 1 whenever the loop runs), so the memory waits of
+    // the tile loads stay exact
+    const long long ri = (long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + min(q, SQ - 1);
+    lraw[S] = rsel < C::BQ ? p.lse[ri] : p.dsum[ri];
   };
   auto lstore = [&](auto set, int stage) {
     constexpr int S = decltype(set)::value;
@@ -624,7 +629,18 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
 
   // 4-stage ring (a power of two keeps the stage index cheap; three would do): the S-wave
   // reads tile it (stage it%4), the dP-wave tile it-1, tile it+1 is stored into the stage tile
-  // it-3 used; tiles it+2 .. it+NSET are in flight in registers
+  // it-3 used; tiles it+2 .. it+NSET are in flight in registers.
+  // Each role runs its own loop of straight-line steps: a step whose tile this pair does not
+  // see still multiplies, with its P (or dS) operand selected to exact zeros, so the
+  // accumulators never sit behind a branch (which made the compiler copy them at every join).
+  // The ring starts zeroed, so a masked step multiplies finite values.
+  {
+    T* z = lds + 8 * tid;
+#pragma unroll
+    for (int i = 0; i < 4 * C::STAGE / (8 * C::NT); i++) *(u32x4*)(z + 8 * i * C::NT) = u32x4{0u, 0u, 0u, 0u};
+    static_assert(4 * C::STAGE % (8 * C::NT) == 0, "ring zeroing split");
+  }
+  __syncthreads();  // zeroed before the first tile is stored
   if (total > 0) {
     gload(std::integral_constant<int, 0>{}, 0);
     lstore(std::integral_constant<int, 0>{}, 0);
@@ -632,81 +648,93 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
     if constexpr (NSET > 2) gload(std::integral_constant<int, 2>{}, 2);
   }
   __syncthreads();
-  // iteration it (it % NSET == S): the S-wave works on tile it, the dP-wave on tile it-1
-  auto step = [&](auto set, int it) {
+  // S-wave step `it` (set S holds tile it, stored an iteration ago): S, P, dV += dO^T . P
+  auto s_step = [&](auto set, int it) {
     constexpr int S = decltype(set)::value;
-    gload(set, it + NSET);  // set S held tile it, stored an iteration ago
-    if (!dpw) {
-      if (it < total && active(it)) {
-        const int st = it & 3, hg = it / ntq, qt0 = qstart + (it % ntq) * C::BQ;
-        const float slope = (FEAT && p.alibi) ? p.alibi[kvh * p.gqa + hg] : 0.0f;
-        const T* qs = lds + st * C::STAGE;
-        const f32x16 sv = rowprod(qs);
-        const bool edge = FEAT || (CAUSAL && kw + 31 > qt0 + delta) || qt0 + C::BQ > SQ || kw + 32 > SK;
-        V8 pP[2];
+    gload(set, it + NSET);
+    const bool act = it < total && active(it);
+    const int st = it & 3, hg = min(it / ntq, p.gqa - 1), qt0 = qstart + (it % ntq) * C::BQ;
+    const float slope = (FEAT && p.alibi) ? p.alibi[kvh * p.gqa + hg] : 0.0f;
+    const T* qs = lds + st * C::STAGE;
+    const f32x16 sv = rowprod(qs);
+    const bool edge = FEAT || (CAUSAL && kw + 31 > qt0 + delta) || qt0 + C::BQ > SQ || kw + 32 > SK;
+    V8 pP[2];
 #pragma unroll
-        for (int rq = 0; rq < 4; rq++) {
-          const f32x4 l4 = *(const f32x4*)&rowv[st][0][8 * rq + 4 * hh];
-          f32x4 pd4;
+    for (int rq = 0; rq < 4; rq++) {
+      const f32x4 l4 = *(const f32x4*)&rowv[st][0][8 * rq + 4 * hh];
+      f32x4 pd4;
 #pragma unroll
-          for (int c = 0; c < 4; c++) {
-            const int r = 4 * rq + c, q = qt0 + 8 * rq + 4 * hh + c;
-            float deriv;
-            const float x = bwd_logit2<FEAT>(p, sv[r], c_log2, slope, q, key, deriv);
-            float pr = exp2_fast(x - l4[c]);
-            if (edge && !visible_b<CAUSAL, FEAT>(p, q, key, delta, SQ, SK)) pr = 0.0f;
-            const float z = DROP ? dropout_z(p.drop_seed, ((uint64_t)(kvh * p.gqa + hg) * SQ + q) * SK + key,
-                                                            p.dropout_p, p.keep_scale)
-                                                : 1.0f;
-            pP[r >> 3][r & 7] = (T)(z * pr);
-            // p * deriv >= 0; a dropped score hands it over negated, so the dP-wave knows z
-            pd4[c] = z == 0.0f ? -(pr * deriv) : pr * deriv;
-          }
-          pdx[it & 1][pair][rq][lane] = pd4;
-        }
-        tprod(qs + C::TT, pP);  // dV^T += dO^T . P
+      for (int c = 0; c < 4; c++) {
+        const int r = 4 * rq + c, q = qt0 + 8 * rq + 4 * hh + c;
+        float deriv;
+        const float x = bwd_logit2<FEAT>(p, sv[r], c_log2, slope, q, key, deriv);
+        float pr = exp2_fast(x - l4[c]);
+        if (edge && !visible_b<CAUSAL, FEAT>(p, q, key, delta, SQ, SK)) pr = 0.0f;
+        pr = act ? pr : 0.0f;
+        const float z = DROP ? dropout_z(p.drop_seed, ((uint64_t)(kvh * p.gqa + hg) * SQ + q) * SK + key,
+                                         p.dropout_p, p.keep_scale)
+                             : 1.0f;
+        pP[r >> 3][r & 7] = (T)(z * pr);
+        // p * deriv >= 0; a dropped score hands it over negated, so the dP-wave knows z
+        pd4[c] = z == 0.0f ? -(pr * deriv) : pr * deriv;
       }
-    } else {
-      const int t = it - 1;
-      if (t >= 0 && active(t)) {
-        const int st = t & 3;
-        const T* qs = lds + st * C::STAGE;
-        const f32x16 dpv = rowprod(qs + C::TT);
-        V8 pS[2];
+      pdx[it & 1][pair][rq][lane] = pd4;
+    }
+    tprod(qs + C::TT, pP);  // dV^T += dO^T . P
+    lstore(std::integral_constant<int, (S + 1) % NSET>{}, (it + 1) & 3);  // tile it+1
+    __syncthreads();
+  };
+  // dP-wave step `it`: tile t = it-1 (a step behind the S-wave): dP, dS, dK += Q^T . dS
+  auto d_step = [&](auto set, int it) {
+    constexpr int S = decltype(set)::value;
+    gload(set, it + NSET);
+    const int t = it - 1;
+    const bool act = t >= 0 && t < total && active(max(t, 0));
+    const int st = t & 3;
+    const T* qs = lds + st * C::STAGE;
+    const f32x16 dpv = rowprod(qs + C::TT);
+    V8 pS[2];
 #pragma unroll
-        for (int rq = 0; rq < 4; rq++) {
-          const f32x4 d4 = *(const f32x4*)&rowv[st][1][8 * rq + 4 * hh];
-          const f32x4 pd4 = pdx[t & 1][pair][rq][lane];
+    for (int rq = 0; rq < 4; rq++) {
+      const f32x4 d4 = *(const f32x4*)&rowv[st][1][8 * rq + 4 * hh];
+      const f32x4 pd4 = pdx[t & 1][pair][rq][lane];
 #pragma unroll
-          for (int c = 0; c < 4; c++) {
-            const int r = 4 * rq + c;
-            if constexpr (DROP) {  // dS = p (z dP - D) deriv (backward.hip:170-176)
-              const float z = pd4[c] < 0.0f ? 0.0f : p.keep_scale;
-              pS[r >> 3][r & 7] = (T)(fabsf(pd4[c]) * (z * dpv[r] - d4[c]));
-            } else {
-              pS[r >> 3][r & 7] = (T)(pd4[c] * (dpv[r] - d4[c]));
-            }
-          }
+      for (int c = 0; c < 4; c++) {
+        const int r = 4 * rq + c;
+        float ds;
+        if constexpr (DROP) {  // dS = p (z dP - D) deriv (backward.hip:170-176)
+          const float z = pd4[c] < 0.0f ? 0.0f : p.keep_scale;
+          ds = fabsf(pd4[c]) * (z * dpv[r] - d4[c]);
+        } else {
+          ds = pd4[c] * (dpv[r] - d4[c]);
         }
-        tprod(qs, pS);  // dK^T += Q^T . dS
-        if constexpr (DSW) {  // dS tile (32 queries x this pair's 32 keys) to the workspace
-          const int hg = t / ntq, qt0 = qstart + (t % ntq) * C::BQ;
-          T* dst = ds_tile<T>(p, b, kvh * p.gqa + hg, kw >> 5, qt0 >> 5) + 16 * l32 + 8 * hh;
-          // streaming stores: the tiles are read once, by the dQ kernel, and must not push the
-          // Q/dO tiles this kernel re-reads out of L2
-          __builtin_nontemporal_store(pS[0], (V8*)dst);
-          __builtin_nontemporal_store(pS[1], (V8*)(dst + 512));
-        }
+        pS[r >> 3][r & 7] = (T)(act ? ds : 0.0f);  // a select: masked-step inputs may be garbage
+      }
+    }
+    tprod(qs, pS);  // dK^T += Q^T . dS
+    if constexpr (DSW) {  // dS tile (32 queries x this pair's 32 keys) to the workspace
+      if (act) {
+        const int hg = t / ntq, qt0 = qstart + (t % ntq) * C::BQ;
+        T* dst = ds_tile<T>(p, b, kvh * p.gqa + hg, kw >> 5, qt0 >> 5) + 16 * l32 + 8 * hh;
+        // streaming stores: the tiles are read once, by the dQ kernel, and must not push the
+        // Q/dO tiles this kernel re-reads out of L2
+        __builtin_nontemporal_store(pS[0], (V8*)dst);
+        __builtin_nontemporal_store(pS[1], (V8*)(dst + 512));
       }
     }
     lstore(std::integral_constant<int, (S + 1) % NSET>{}, (it + 1) & 3);  // tile it+1
     __syncthreads();
   };
-  for (int it = 0; it <= total; it += NSET) {
-    step(std::integral_constant<int, 0>{}, it);
-    if (it + 1 <= total) step(std::integral_constant<int, 1>{}, it + 1);
-    if constexpr (NSET > 2)
-      if (it + 2 <= total) step(std::integral_constant<int, 2>{}, it + 2);
+  // steps 0 .. total (the dP-wave's last tile is total-1), rounded up to whole register-set
+  // rounds; both roles run the same number of barriers
+  if (total > 0) {
+    if (dpw) {
+      for (int it = 0; it <= total; it += NSET)
+        for_sets(std::make_integer_sequence<int, NSET>{}, [&](auto set) { d_step(set, it + decltype(set)::value); });
+    } else {
+      for (int it = 0; it <= total; it += NSET)
+        for_sets(std::make_integer_sequence<int, NSET>{}, [&](auto set) { s_step(set, it + decltype(set)::value); });
+    }
   }
   if (key < SK) {
     T* row = dpw ? (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (sq.ko + key) * p.dks.s
@@ -764,12 +792,6 @@ struct BwdDsQCfg {
   static constexpr int DSTR = 32;      // LDS row of a wave's dS block: 32 query slots (64 B)
   static_assert(KCH % NT == 0, "loader split");
 };
-
-// f(integral_constant<int, I>) for I in the sequence, in order (compile-time register-set index)
-template <int... I, typename F>
-__device__ __forceinline__ void for_sets(std::integer_sequence<int, I...>, F&& f) {
-  (f(std::integral_constant<int, I>{}), ...);
-}
 
 // Element offset of (key row r, query slot n) in a wave's dS block: 64-byte rows of four 16-byte
 // chunks, chunk n/8 stored at position (n/8) ^ (2*r.bit2 + r.bit3). The transposing reads
