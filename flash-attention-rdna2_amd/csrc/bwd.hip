@@ -593,15 +593,13 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   };
   // this wave's product of a tile with its B rows: S (S-wave, with Q) or dP (dP-wave, with
   // dO); x[r] is query qt0 + 8*(r/4) + 4*hh + (r%4), key `key`
-  // (two independent accumulation chains, even and odd contraction steps)
+  // (one accumulation chain: dependent MFMAs of one shape issue back to back, and a second
+  // chain would cost 16 VALU adds per product)
   auto rowprod = [&](const T* tile) {
-    f32x16 x0 = f32x16{}, x1 = f32x16{};
+    f32x16 x = f32x16{};
 #pragma unroll
-    for (int ds = 0; ds < C::NDS; ds += 2) {
-      x0 = Dt<T>::mma32(*(const V8*)(tile + bofs<C::HD>(l32, 2 * ds + hh)), kv[ds], x0);
-      x1 = Dt<T>::mma32(*(const V8*)(tile + bofs<C::HD>(l32, 2 * ds + 2 + hh)), kv[ds + 1], x1);
-    }
-    return x0 + x1;
+    for (int ds = 0; ds < C::NDS; ds++) x = Dt<T>::mma32(*(const V8*)(tile + bofs<C::HD>(l32, 2 * ds + hh)), kv[ds], x);
+    return x;
   };
   // acc^T += tile^T . B (A operand by transposing reads of the tile; B = P or dS)
   auto tprod = [&](const T* tile, const V8 (&bop)[2]) {
@@ -631,14 +629,19 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   // reads tile it (stage it%4), the dP-wave tile it-1, tile it+1 is stored into the stage tile
   // it-3 used; tiles it+2 .. it+NSET are in flight in registers.
   // Each role runs its own loop of straight-line steps: a step whose tile this pair does not
-  // see still multiplies, with its P (or dS) operand selected to exact zeros, so the
-  // accumulators never sit behind a branch (which made the compiler copy them at every join).
-  // The ring starts zeroed, so a masked step multiplies finite values.
+  // see still multiplies, with exact zeros for its P (or dS) operand, so the accumulators never
+  // sit behind a branch (which made the compiler copy them at every join). The zeros need no
+  // select: a tile of the range that the pair does not see is masked by the edge test, a step
+  // past the last tile has LSE = +inf (P = 0), and the dP-wave's dS = P deriv (dP - D) inherits
+  // the zero. The ring, the LSE/D rows and the hand-over buffer start zeroed, so the first
+  // dP-wave step (tile -1) and every masked step multiply finite values.
   {
     T* z = lds + 8 * tid;
 #pragma unroll
     for (int i = 0; i < 4 * C::STAGE / (8 * C::NT); i++) *(u32x4*)(z + 8 * i * C::NT) = u32x4{0u, 0u, 0u, 0u};
     static_assert(4 * C::STAGE % (8 * C::NT) == 0, "ring zeroing split");
+    for (int i = tid; i < (int)(sizeof(rowv) / 4); i += C::NT) (&rowv[0][0][0])[i] = 0.0f;
+    for (int i = tid; i < (int)(sizeof(pdx) / 16); i += C::NT) (&pdx[0][0][0][0])[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   __syncthreads();  // zeroed before the first tile is stored
   if (total > 0) {
@@ -652,7 +655,6 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   auto s_step = [&](auto set, int it) {
     constexpr int S = decltype(set)::value;
     gload(set, it + NSET);
-    const bool act = it < total && active(it);
     const int st = it & 3, hg = min(it / ntq, p.gqa - 1), qt0 = qstart + (it % ntq) * C::BQ;
     const float slope = (FEAT && p.alibi) ? p.alibi[kvh * p.gqa + hg] : 0.0f;
     const T* qs = lds + st * C::STAGE;
@@ -670,7 +672,6 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
         const float x = bwd_logit2<FEAT>(p, sv[r], c_log2, slope, q, key, deriv);
         float pr = exp2_fast(x - l4[c]);
         if (edge && !visible_b<CAUSAL, FEAT>(p, q, key, delta, SQ, SK)) pr = 0.0f;
-        pr = act ? pr : 0.0f;
         const float z = DROP ? dropout_z(p.drop_seed, ((uint64_t)(kvh * p.gqa + hg) * SQ + q) * SK + key,
                                          p.dropout_p, p.keep_scale)
                              : 1.0f;
@@ -708,7 +709,7 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
         } else {
           ds = pd4[c] * (dpv[r] - d4[c]);
         }
-        pS[r >> 3][r & 7] = (T)(act ? ds : 0.0f);  // a select: masked-step inputs may be garbage
+        pS[r >> 3][r & 7] = (T)ds;
       }
     }
     tprod(qs, pS);  // dK^T += Q^T . dS
