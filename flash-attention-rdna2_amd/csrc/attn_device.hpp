@@ -149,8 +149,11 @@ __device__ __forceinline__ int kofs(int r, int c, int HD, int KSW) {
 // Raw buffer resource over [base, base + nbytes): 16-byte loads at offsets >= nbytes return
 // zeros, so tile loads need no per-lane condition. nbytes is clamped to the 32-bit range; the
 // third descriptor word selects 32-bit raw (untyped) access on gfx9-family parts.
+// (The clamp tests the high word with 32-bit compares, which stay on the scalar unit; a 64-bit
+// ordered compare has no scalar form and went to the VALU.)
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, long long nbytes) {
-  const unsigned n = nbytes <= 0 ? 0u : (nbytes >= 0xFFFFFFFFll ? 0xFFFFFFFFu : (unsigned)nbytes);
+  const int hi = (int)(nbytes >> 32);
+  const unsigned n = hi < 0 ? 0u : (hi > 0 ? 0xFFFFFFFFu : (unsigned)nbytes);
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
 }
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff) {

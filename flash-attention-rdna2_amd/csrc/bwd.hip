@@ -554,23 +554,49 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   float lraw[NSET];
   bool lok[NSET];
   const int rsel = tid % (2 * C::BQ);  // row value slot: [0,BQ) LSE, [BQ,2BQ) D
-  auto gload = [&](auto set, int it) {
+  // Tiles are loaded in order (tile g = head hg of the group, q tile qi), through a cursor
+  // whose pointers, byte counts and row index advance by additions: the 64-bit products of a
+  // from-scratch address cost ~90 scalar instructions per tile, which the scalar issue port
+  // cannot hide. Past the last tile the cursor stays on it and the loads are emptied.
+  const long long q_step = (long long)C::BQ * p.qs.s, do_step = (long long)C::BQ * p.dos.s;
+  const long long q_wrap = p.qs.h - ntq * q_step, do_wrap = p.dos.h - ntq * do_step;
+  const long long l_wrap = p.lse_sh - (long long)ntq * C::BQ;
+  const long long q_left0 = (long long)(SQ - qstart) * p.qs.s * 2, do_left0 = (long long)(SQ - qstart) * p.dos.s * 2;
+  const T* g_q = (const T*)p.Q + (long long)b * p.qs.b + (long long)(kvh * p.gqa) * p.qs.h + (sq.qo + qstart) * p.qs.s;
+  const T* g_do = (const T*)p.dO + (long long)b * p.dos.b + (long long)(kvh * p.gqa) * p.dos.h + (sq.qo + qstart) * p.dos.s;
+  long long g_l = (long long)b * p.lse_sb + (long long)(kvh * p.gqa) * p.lse_sh + sq.qo + qstart;
+  long long g_qleft = q_left0, g_doleft = do_left0;
+  int g_qi = 0, g_t = 0;  // q tile index within the head, tile number
+  auto gload = [&](auto set) {
     constexpr int S = decltype(set)::value;
-    const int hg = min(it / max(ntq, 1), p.gqa - 1), qt0 = qstart + (it % max(ntq, 1)) * C::BQ;
-    const int h = kvh * p.gqa + hg;
-    const long long rows = it < total ? (long long)(SQ - qt0) : 0;  // past the end: all zeros
-    const auto rq = buf_rsrc((const T*)p.Q + (long long)b * p.qs.b + (long long)h * p.qs.h + (sq.qo + qt0) * p.qs.s,
-                             rows * p.qs.s * 2);
-    const auto rd = buf_rsrc((const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + (sq.qo + qt0) * p.dos.s,
-                             rows * p.dos.s * 2);
+    const bool in = g_t < total;
+    const auto rq = buf_rsrc(g_q, in ? g_qleft : 0);  // past the end: all zeros
+    const auto rd = buf_rsrc(g_do, in ? g_doleft : 0);
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(j < C::QJ ? rq : rd, voff[j]);
-    const int q = qt0 + (rsel % C::BQ);
-    lok[S] = it < total && q < SQ;
+    const int qr = qstart + g_qi * C::BQ + (rsel % C::BQ);
+    lok[S] = in && qr < SQ;
     // unconditional (clamped row; SQ >= 1 whenever the loop runs), so the memory waits of
     // the tile loads stay exact
-    const long long ri = (long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + min(q, SQ - 1);
+    const long long ri = g_l + min(rsel % C::BQ, SQ - 1 - qstart - g_qi * C::BQ);
     lraw[S] = rsel < C::BQ ? p.lse[ri] : p.dsum[ri];
+    if (g_t + 1 < total) {  // advance (uniform, scalar)
+      if (++g_qi == ntq) {
+        g_qi = 0;
+        g_q += q_step + q_wrap;
+        g_do += do_step + do_wrap;
+        g_l += C::BQ + l_wrap;
+        g_qleft = q_left0;
+        g_doleft = do_left0;
+      } else {
+        g_q += q_step;
+        g_do += do_step;
+        g_l += C::BQ;
+        g_qleft -= 2 * q_step;
+        g_doleft -= 2 * do_step;
+      }
+    }
+    ++g_t;
   };
   auto lstore = [&](auto set, int stage) {
     constexpr int S = decltype(set)::value;
@@ -587,10 +613,7 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
       rowv[stage][rsel / C::BQ][rsel % C::BQ] = lv;
     }
   };
-  auto active = [&](int it) {
-    const int qt0 = qstart + (it % ntq) * C::BQ;
-    return pair_keys && qt0 < wq1 && qt0 + C::BQ > wq0;
-  };
+  auto active = [&](int qt0) { return pair_keys && qt0 < wq1 && qt0 + C::BQ > wq0; };
   // this wave's product of a tile with its B rows: S (S-wave, with Q) or dP (dP-wave, with
   // dO); x[r] is query qt0 + 8*(r/4) + 4*hh + (r%4), key `key`
   // (one accumulation chain: dependent MFMAs of one shape issue back to back, and a second
@@ -645,17 +668,26 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   }
   __syncthreads();  // zeroed before the first tile is stored
   if (total > 0) {
-    gload(std::integral_constant<int, 0>{}, 0);
+    gload(std::integral_constant<int, 0>{});
     lstore(std::integral_constant<int, 0>{}, 0);
-    gload(std::integral_constant<int, 1>{}, 1);
-    if constexpr (NSET > 2) gload(std::integral_constant<int, 2>{}, 2);
+    gload(std::integral_constant<int, 1>{});
+    if constexpr (NSET > 2) gload(std::integral_constant<int, 2>{});
   }
   __syncthreads();
+  // the tile a role works on: head hg of the group, q tile qi (advanced once per tile)
+  int w_qi = 0, w_hg = 0;
+  auto w_next = [&]() {
+    if (++w_qi == ntq) {
+      w_qi = 0;
+      w_hg = min(w_hg + 1, p.gqa - 1);
+    }
+  };
   // S-wave step `it` (set S holds tile it, stored an iteration ago): S, P, dV += dO^T . P
   auto s_step = [&](auto set, int it) {
     constexpr int S = decltype(set)::value;
-    gload(set, it + NSET);
-    const int st = it & 3, hg = min(it / ntq, p.gqa - 1), qt0 = qstart + (it % ntq) * C::BQ;
+    gload(set);
+    const int st = it & 3, hg = w_hg, qt0 = qstart + w_qi * C::BQ;
+    w_next();
     const float slope = (FEAT && p.alibi) ? p.alibi[kvh * p.gqa + hg] : 0.0f;
     const T* qs = lds + st * C::STAGE;
     const f32x16 sv = rowprod(qs);
@@ -688,9 +720,11 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
   // dP-wave step `it`: tile t = it-1 (a step behind the S-wave): dP, dS, dK += Q^T . dS
   auto d_step = [&](auto set, int it) {
     constexpr int S = decltype(set)::value;
-    gload(set, it + NSET);
+    gload(set);
     const int t = it - 1;
-    const bool act = t >= 0 && t < total && active(max(t, 0));
+    const int hg = w_hg, qt0 = qstart + w_qi * C::BQ;
+    const bool act = t >= 0 && t < total && active(qt0);
+    if (t >= 0) w_next();
     const int st = t & 3;
     const T* qs = lds + st * C::STAGE;
     const f32x16 dpv = rowprod(qs + C::TT);
@@ -715,7 +749,6 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
     tprod(qs, pS);  // dK^T += Q^T . dS
     if constexpr (DSW) {  // dS tile (32 queries x this pair's 32 keys) to the workspace
       if (act) {
-        const int hg = t / ntq, qt0 = qstart + (t % ntq) * C::BQ;
         T* dst = ds_tile<T>(p, b, kvh * p.gqa + hg, kw >> 5, qt0 >> 5) + 16 * l32 + 8 * hh;
         // streaming stores: the tiles are read once, by the dQ kernel, and must not push the
         // Q/dO tiles this kernel re-reads out of L2
