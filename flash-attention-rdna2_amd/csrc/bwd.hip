@@ -891,17 +891,22 @@ bwd_dq_ds_kernel(BwdParams p, int nqt) {
   constexpr int NS = C::NS;
   V8 dsr[NS][4];  // [register set][key block jb, query half sh] chunks of one K tile
   bool dact[NS][2];
+  // Tiles are loaded in order; the tile addresses advance by additions (a from-scratch 64-bit
+  // address costs a dozen scalar instructions per tile). Past the last key block the dS
+  // address stays on a valid block.
+  const T* d_ptr = dsw + (kstart >> 5) * kstep;
+  int d_kb32 = kstart >> 5;
   auto dsload = [&](auto set, int t) {
     constexpr int S = decltype(set)::value;
-    const int kb = kstart + t * C::BC;
+    const T* src[2] = {d_ptr, d_kb32 + 1 < nkb ? d_ptr + kstep : d_ptr};
 #pragma unroll
     for (int jb = 0; jb < 2; jb++) {
-      const int kb32 = (kb >> 5) + jb;
-      dact[S][jb] = t < ntiles && written(kb32);
-      const T* src = dsw + min(kb32, nkb - 1) * kstep;
-      dsr[S][2 * jb] = __builtin_nontemporal_load((const V8*)src);
-      dsr[S][2 * jb + 1] = __builtin_nontemporal_load((const V8*)(src + 512));
+      dact[S][jb] = t < ntiles && written(d_kb32 + jb);
+      dsr[S][2 * jb] = __builtin_nontemporal_load((const V8*)src[jb]);
+      dsr[S][2 * jb + 1] = __builtin_nontemporal_load((const V8*)(src[jb] + 512));
     }
+    if (d_kb32 + 2 < nkb) d_ptr += 2 * kstep;
+    d_kb32 += 2;
   };
 
   int voff[C::PER];
@@ -911,12 +916,16 @@ bwd_dq_ds_kernel(BwdParams p, int nqt) {
     voff[j] = r * (int)(p.ks.s * 2) + 16 * c;
   }
   u32x4 ld[NS][C::PER];
+  const T* k_ptr = Kg + (long long)kstart * p.ks.s;
+  long long k_left = (long long)(SK - kstart) * p.ks.s * 2;
+  const long long k_step = (long long)C::BC * p.ks.s;
   auto gload = [&](auto set, int t) {
     constexpr int S = decltype(set)::value;
-    const int kb = kstart + t * C::BC;  // past the last tile the descriptor is empty: zeros
-    const auto rs = buf_rsrc(Kg + (long long)kb * p.ks.s, (long long)(SK - kb) * p.ks.s * 2);
+    const auto rs = buf_rsrc(k_ptr, k_left);  // past the last tile the descriptor is empty: zeros
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(rs, voff[j]);
+    k_ptr += k_step;
+    k_left -= 2 * k_step;
   };
   auto lstore = [&](auto set, int stage) {
     constexpr int S = decltype(set)::value;
