@@ -124,3 +124,65 @@ def test_backward_full_config_c3(path):
         for got, ref in ((runs[0][0][bb, hd], qf.grad), (runs[0][1][bb, hd], kf.grad), (runs[0][2][bb, hd], vf.grad)):
             e = ((got.float() - ref).norm() / ref.norm()).item()
             assert e <= GTOL["bf16"], e
+
+
+def test_backward_ds_workspace_too_small_falls_back():
+    """A dS workspace smaller than fable_attn_bwd_ds_bytes reports must be ignored (the
+    recomputing path runs, the buffer stays untouched); a full-size one filled with NaN bit
+    patterns must give the same gradients (tiles that are never written are never read).
+    Both against the oracle, through the C-ABI with a hand-built BwdParams."""
+    import torch
+
+    from fable_attn import _C, _lib
+    lib = _lib.load()
+    case = ("D128 causal tail", 1, 4, 2, 150, 150, 128, True, -1, -1, 0.0, False)
+    name, B, Hq, Hk, SQ, SK, D, causal, wl, wr, sc, alibi = case
+    dt = "bf16"
+    q = gen((B, Hq, SQ, D), 11, dt)
+    k = gen((B, Hk, SK, D), 12, dt)
+    v = gen((B, Hk, SK, D), 13, dt)
+    do = gen((B, Hq, SQ, D), 14, dt)
+    scale = D ** -0.5
+    view = lambda a: to_dev(a, dt).transpose(1, 2).contiguous().transpose(1, 2)
+    qd, kd, vd, dod = view(q), view(k), view(v), view(do)
+    out, lse = _C.fwd(qd, kd, vd, scale, causal, wl, wr, sc, None, 0.0, 0)
+    dq, dk, dv = (torch.empty_like(x) for x in (qd, kd, vd))
+    dsum = torch.empty((B, Hq, SQ), dtype=torch.float32, device="cuda")
+    p = _lib.BwdParams()
+    p.Q, p.K, p.V, p.O, p.dO = qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(), dod.data_ptr()
+    p.dQ, p.dK, p.dV = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    p.lse, p.dsum = lse.data_ptr(), dsum.data_ptr()
+    bhs = lambda t: _lib.Strides(*t.stride()[:3])
+    p.qs, p.ks, p.vs, p.os, p.dos = bhs(qd), bhs(kd), bhs(vd), bhs(out), bhs(dod)
+    p.dqs, p.dks, p.dvs = bhs(dq), bhs(dk), bhs(dv)
+    p.B, p.Hq, p.Hk, p.SQ, p.SK, p.D, p.gqa = B, Hq, Hk, SQ, SK, D, Hq // Hk
+    p.scale, p.causal, p.win_left, p.win_right, p.keep_scale = scale, 1, -1, -1, 1.0
+    need = lib.fable_attn_bwd_ds_bytes(p, 1)
+    assert need == B * Hq * 5 * 5 * 2048
+    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device="cuda")  # NaN bit patterns
+    p.ds_ws, p.ds_ws_bytes = ws.data_ptr(), need - 1
+    stream = ctypes_stream()
+    assert lib.fable_attn_backward_launch(p, 1, stream) == 0
+    torch.cuda.synchronize()
+    assert torch.all(ws == 0xFF), "a too-small workspace must not be written"
+    ref = orc.bwd(q, k, v, do, scale, causal)
+    for got, r, gname in ((dq, ref[0], "dq"), (dk, ref[1], "dk"), (dv, ref[2], "dv")):
+        e = orc.rel_rms(to_np(got), r)
+        assert e <= GTOL[dt], f"{gname} rel_rms {e:.3e}"
+    # a full-size workspace poisoned with NaN patterns: the dQ kernel reads only the tiles the
+    # dK/dV kernel wrote (the causal upper-right tiles stay NaN and must not leak into dQ)
+    p.ds_ws_bytes = need
+    assert lib.fable_attn_backward_launch(p, 1, stream) == 0
+    torch.cuda.synchronize()
+    assert not torch.all(ws == 0xFF), "the workspace path was not taken"
+    for got, r, gname in ((dq, ref[0], "dq"), (dk, ref[1], "dk"), (dv, ref[2], "dv")):
+        assert torch.isfinite(got).all(), f"{gname} not finite"
+        e = orc.rel_rms(to_np(got), r)
+        assert e <= GTOL[dt], f"{gname} rel_rms {e:.3e} (poisoned workspace)"
+
+
+def ctypes_stream():
+    import ctypes
+
+    import torch
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
