@@ -692,24 +692,39 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
     const T* qs = lds + st * C::STAGE;
     const f32x16 sv = rowprod(qs);
     const bool edge = FEAT || (CAUSAL && kw + 31 > qt0 + delta) || qt0 + C::BQ > SQ || kw + 32 > SK;
-    V8 pP[2];
+    // probabilities; on an edge tile (one uniform branch, no per-score branches) the scores a
+    // query does not see are zeroed
+    float pr[16], dv[16];
 #pragma unroll
     for (int rq = 0; rq < 4; rq++) {
       const f32x4 l4 = *(const f32x4*)&rowv[st][0][8 * rq + 4 * hh];
+#pragma unroll
+      for (int c = 0; c < 4; c++) {
+        const int r = 4 * rq + c, q = qt0 + 8 * rq + 4 * hh + c;
+        const float x = bwd_logit2<FEAT>(p, sv[r], c_log2, slope, q, key, dv[r]);
+        pr[r] = exp2_fast(x - l4[c]);
+      }
+    }
+    if (edge) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int q = qt0 + 8 * (r >> 2) + 4 * hh + (r & 3);
+        pr[r] = visible_b<CAUSAL, FEAT>(p, q, key, delta, SQ, SK) ? pr[r] : 0.0f;
+      }
+    }
+    V8 pP[2];
+#pragma unroll
+    for (int rq = 0; rq < 4; rq++) {
       f32x4 pd4;
 #pragma unroll
       for (int c = 0; c < 4; c++) {
         const int r = 4 * rq + c, q = qt0 + 8 * rq + 4 * hh + c;
-        float deriv;
-        const float x = bwd_logit2<FEAT>(p, sv[r], c_log2, slope, q, key, deriv);
-        float pr = exp2_fast(x - l4[c]);
-        if (edge && !visible_b<CAUSAL, FEAT>(p, q, key, delta, SQ, SK)) pr = 0.0f;
         const float z = DROP ? dropout_z(p.drop_seed, ((uint64_t)(kvh * p.gqa + hg) * SQ + q) * SK + key,
                                          p.dropout_p, p.keep_scale)
                              : 1.0f;
-        pP[r >> 3][r & 7] = (T)(z * pr);
+        pP[r >> 3][r & 7] = (T)(z * pr[r]);
         // p * deriv >= 0; a dropped score hands it over negated, so the dP-wave knows z
-        pd4[c] = z == 0.0f ? -(pr * deriv) : pr * deriv;
+        pd4[c] = z == 0.0f ? -(pr[r] * dv[r]) : pr[r] * dv[r];
       }
       pdx[it & 1][pair][rq][lane] = pd4;
     }

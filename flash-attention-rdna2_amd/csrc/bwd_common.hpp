@@ -6,15 +6,17 @@
 
 namespace fa {
 
+// Written with bitwise ands, not early returns: per score the compiler then emits compares and
+// one select instead of a divergent branch (with its exec-mask bookkeeping) per score.
 template <bool CAUSAL, bool FEAT>
 __device__ __forceinline__ bool visible_b(const BwdParams& p, int q, int key, int delta, int SQ, int SK) {
-  if (key >= SK || q >= SQ) return false;
-  if (CAUSAL && key > q + delta) return false;
+  bool ok = (key < SK) & (q < SQ);
+  if (CAUSAL) ok &= key <= q + delta;
   if (FEAT) {
-    if (p.win_left >= 0 && key < q + delta - p.win_left) return false;
-    if (p.win_right >= 0 && key > q + delta + p.win_right) return false;
+    ok &= (p.win_left < 0) | (key >= q + delta - p.win_left);
+    ok &= (p.win_right < 0) | (key <= q + delta + p.win_right);
   }
-  return true;
+  return ok;
 }
 
 // keys visible to query rows [r0, r1]: [k0, k1)
