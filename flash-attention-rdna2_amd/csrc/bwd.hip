@@ -826,13 +826,14 @@ __global__ __launch_bounds__(256) void bwd_dsum_kernel(BwdParams p, int rblocks)
   if (c == 0 && q < sq.SQ) p.dsum[(long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + q] = acc;
 }
 
-template <int HD_, int NW_, int WPE_, int NS_>
+template <int HD_, int NW_, int WPE_, int NS_, int BC_ = 64>
 struct BwdDsQCfg {
   static constexpr int HD = HD_, NW = NW_, WPE = WPE_;
   static constexpr int NS = NS_;       // register sets: K and dS loaded NS-1 tiles ahead
   static constexpr int NT = NW * 64;
   static constexpr int BQ = NW * 32;   // queries per workgroup (32 per wave)
-  static constexpr int BC = 64;        // keys per K tile (two workspace tiles)
+  static constexpr int BC = BC_;       // keys per K tile
+  static constexpr int NKB = BC / 32;  // workspace key blocks per K tile
   static constexpr int NDB = HD / 32;  // 32-row blocks of dQ^T
   static constexpr int DCH = HD / 8;
   static constexpr int KCH = BC * DCH;
@@ -904,8 +905,8 @@ bwd_dq_ds_kernel(BwdParams p, int nqt) {
   const T* dsw = ds_tile<T>(p, b, h, 0, min(qw >> 5, nqb - 1)) + 16 * l32 + 8 * hh;
   const long long kstep = (long long)nqb * 1024;  // elements between key blocks
   constexpr int NS = C::NS;
-  V8 dsr[NS][4];  // [register set][key block jb, query half sh] chunks of one K tile
-  bool dact[NS][2];
+  V8 dsr[NS][2 * C::NKB];  // [register set][key block jb, query half sh] chunks of one K tile
+  bool dact[NS][C::NKB];
   // Tiles are loaded in order; the tile addresses advance by additions (a from-scratch 64-bit
   // address costs a dozen scalar instructions per tile). Past the last key block the dS
   // address stays on a valid block.
@@ -913,15 +914,17 @@ bwd_dq_ds_kernel(BwdParams p, int nqt) {
   int d_kb32 = kstart >> 5;
   auto dsload = [&](auto set, int t) {
     constexpr int S = decltype(set)::value;
-    const T* src[2] = {d_ptr, d_kb32 + 1 < nkb ? d_ptr + kstep : d_ptr};
+    const T* src = d_ptr;
 #pragma unroll
-    for (int jb = 0; jb < 2; jb++) {
+    for (int jb = 0; jb < C::NKB; jb++) {
       dact[S][jb] = t < ntiles && written(d_kb32 + jb);
-      dsr[S][2 * jb] = __builtin_nontemporal_load((const V8*)src[jb]);
-      dsr[S][2 * jb + 1] = __builtin_nontemporal_load((const V8*)(src[jb] + 512));
+      dsr[S][2 * jb] = __builtin_nontemporal_load((const V8*)src);
+      dsr[S][2 * jb + 1] = __builtin_nontemporal_load((const V8*)(src + 512));
+      if (d_kb32 + jb + 1 < nkb) src += kstep;  // past the last key block: stay on it
     }
-    if (d_kb32 + 2 < nkb) d_ptr += 2 * kstep;
-    d_kb32 += 2;
+    if (d_kb32 + C::NKB < nkb) d_ptr += C::NKB * kstep;
+    else d_ptr = dsw + (nkb - 1) * kstep;
+    d_kb32 += C::NKB;
   };
 
   int voff[C::PER];
@@ -964,14 +967,14 @@ bwd_dq_ds_kernel(BwdParams p, int nqt) {
     dsload(std::integral_constant<int, (S + NS - 1) % NS>{}, t + NS - 1);
     // this wave's dS chunks (key rows 32jb + l32, query slots 16sh + 8hh ..) into its LDS block
 #pragma unroll
-    for (int jb = 0; jb < 2; jb++)
+    for (int jb = 0; jb < C::NKB; jb++)
 #pragma unroll
       for (int sh = 0; sh < 2; sh++) *(V8*)(my + dsl_ofs(32 * jb + l32, 16 * sh + 8 * hh)) = dsr[S][2 * jb + sh];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     const T* ks = lds + (t & 1) * C::KT;
 #pragma unroll
-    for (int jb = 0; jb < 2; jb++) {
+    for (int jb = 0; jb < C::NKB; jb++) {
       if (!dact[S][jb]) continue;
 #pragma unroll
       for (int g2 = 0; g2 < 2; g2++) {
