@@ -462,19 +462,20 @@ fwd_kernel(FwdParams p, int nqt) {
   }
 }
 
-// Three workgroup shapes per head dim: C (the widest) runs the plain masks (causal / sequence
-// end) and the wide-window / alibi feature kernels; CF the softcap and dropout kernels, whose
-// per-score work needs a different register balance; CN the narrow masks (a window or chunk
-// under 2048 keys), where a tall workgroup's key span would be mostly masked and its fixed
-// costs (Q rows, pipeline fill, output) are paid over few tiles, so shorter workgroups, more of
-// them per CU, win. Dropout has kernels of its own, so its Philox rounds cost the other
-// features no registers.
+// Workgroup shapes per head dim: C (the widest) runs the plain masks (causal / sequence end)
+// and the wide-window / alibi feature kernels; CS the plain masks when C's grid would give
+// fewer than 4 workgroups per CU (short sequences: more, shorter workgroups balance better);
+// CF the softcap and dropout kernels, whose per-score work needs a different register
+// balance; CN the narrow masks (a window or chunk under 2048 keys), where a tall workgroup's
+// key span would be mostly masked and its fixed costs (Q rows, pipeline fill, output) are paid
+// over few tiles, so shorter workgroups, more of them per CU, win. Dropout has kernels of its
+// own, so its Philox rounds cost the other features no registers.
 template <class K>
 struct CfgTag {
   using type = K;
 };
 
-template <typename T, class C, class CF, class CN>
+template <typename T, class C, class CF, class CN, class CS = C>
 static int launch_fwd(const FwdParams& p, hipStream_t st) {
   const bool drop = p.dropout_p > 0.0f;
   const bool feat = drop || p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
@@ -505,6 +506,11 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
       return go(CfgTag<CF>{}, causal, Y{}, N{});
     }
     if (feat) return go(CfgTag<C>{}, causal, Y{}, N{});
+    if constexpr (!std::is_same<CS, C>::value) {
+      constexpr long long kSmallGrid = 4 * 256;  // 4 workgroups of shape C per CU
+      if ((long long)((p.SQ + C::BR - 1) / C::BR) * p.NH * p.batch < kSmallGrid)
+        return go(CfgTag<CS>{}, causal, N{}, N{});
+    }
     return go(CfgTag<C>{}, causal, N{}, N{});
   };
   return p.causal ? pick(std::integral_constant<bool, true>{}) : pick(std::integral_constant<bool, false>{});

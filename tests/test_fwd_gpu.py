@@ -155,3 +155,42 @@ def test_varlen_parity(kind, dt):
     lerr, inf_ok = lse_err(l, l_ref)
     assert rel <= TOL[dt], f"rel_rms {rel:.3e}"
     assert inf_ok and lerr <= LSE_ABS, f"LSE err {lerr:.3e} inf_ok={inf_ok}"
+
+
+@pytest.mark.parametrize("cfg", [
+    ("C2 causal fp16 B1 S16384 H32", 1, 16384, 32, True, "f16"),
+    ("full bf16 B2 S8192 H32", 2, 8192, 32, False, "bf16"),
+], ids=lambda c: c[0])
+def test_forward_full_size_sampled_heads(cfg):
+    """BASELINE.json configs[1] at its full size (and a non-causal bf16 grid of the same scale):
+    grids of >= 1024 workgroups, which run the widest workgroup shape. Sampled (batch, head)
+    pairs are checked against an exact float32 torch reference on the GPU (the fp64 oracle is
+    too slow at S=16384), at the fp16/bf16 tolerances; LSE within 1e-3."""
+    import torch
+
+    from fable_attn import _C
+    name, B, S, H, causal, dt = cfg
+    D = 128
+    print(f"[fwd-full] {name}", flush=True)
+    tdt = torch.float16 if dt == "f16" else torch.bfloat16
+    g = torch.Generator(device="cuda").manual_seed(3)
+    q, k, v = (torch.randn(B, S, H, D, device="cuda", dtype=tdt, generator=g) for _ in range(3))
+    qh, kh, vh = (x.transpose(1, 2) for x in (q, k, v))
+    scale = D ** -0.5
+    out, lse = _C.fwd(qh, kh, vh, scale, causal, -1, 0 if causal else -1, 0.0, None, 0.0, 0)
+    torch.cuda.synchronize()
+    for bb, hd in ((0, 0), (B - 1, H - 1), (B // 2, H // 2)):
+        qf = q[bb, :, hd].float()
+        kf = k[bb, :, hd].float().t().contiguous()
+        vf = v[bb, :, hd].float()
+        s = (qf @ kf) * scale
+        if causal:
+            s = s.masked_fill(torch.ones(S, S, device="cuda", dtype=torch.bool).triu(1), float("-inf"))
+        ref_lse = torch.logsumexp(s, -1)
+        ref = torch.softmax(s, -1) @ vf
+        del s
+        got = out[bb, hd].float()
+        e = ((got - ref).norm() / ref.norm()).item()
+        assert e <= TOL[dt], f"({bb},{hd}) O rel_rms {e:.3e} > {TOL[dt]}"
+        le = (lse[bb, hd] - ref_lse).abs().max().item()
+        assert le <= LSE_ABS, f"({bb},{hd}) LSE err {le:.3e}"
