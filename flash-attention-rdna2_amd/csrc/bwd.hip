@@ -1076,7 +1076,9 @@ static int launch_bwd2(const BwdParams& p, hipStream_t st) {
   if (gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_backward_launch: grid too large");
   if constexpr (CKV::PAIR) {
     const long long need = ds_bytes(p);
-    if (p.ds_ws && need > 0 && p.ds_ws_bytes >= need) return launch_bwd_ds<T, CKV, CAUSAL, FEAT, DROP>(p, st, nkt);
+    // (the tiles are moved with 16-byte accesses: an unaligned workspace is not used)
+    if (p.ds_ws && ((uintptr_t)p.ds_ws & 15) == 0 && need > 0 && p.ds_ws_bytes >= need)
+      return launch_bwd_ds<T, CKV, CAUSAL, FEAT, DROP>(p, st, nkt);
   }
   if (gq > 0) {
     hipLaunchKernelGGL((bwd_dq_kernel<T, CQ, CAUSAL, FEAT, DROP>), dim3((unsigned)gq), dim3(CQ::NT), 0, st, p, nqt);

@@ -138,7 +138,8 @@ typedef struct BwdParams {
   /* dS workspace (no reference counterpart; ABI version 3). When ds_ws is set and ds_ws_bytes
    * >= fable_attn_bwd_ds_bytes(p, dtype) > 0, the dK/dV kernel writes every dS tile it computes
    * once, and dQ = dS.K becomes one product per tile; otherwise a dQ kernel recomputes S and
-   * dP. Device memory, any contents on entry, scratch on exit. */
+   * dP. Device memory, 16-byte aligned (an unaligned buffer is not used), any contents on
+   * entry, scratch on exit. */
   void* ds_ws;
   int64_t ds_ws_bytes;
 } BwdParams;

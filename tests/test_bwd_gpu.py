@@ -127,8 +127,9 @@ def test_backward_full_config_c3(path):
 
 
 def test_backward_ds_workspace_too_small_falls_back():
-    """A dS workspace smaller than fable_attn_bwd_ds_bytes reports must be ignored (the
-    recomputing path runs, the buffer stays untouched); a full-size one filled with NaN bit
+    """A dS workspace smaller than fable_attn_bwd_ds_bytes reports, or not 16-byte aligned,
+    must be ignored (the recomputing path runs, the buffer stays untouched); a full-size one
+    filled with NaN bit
     patterns must give the same gradients (tiles that are never written are never read).
     Both against the oracle, through the C-ABI with a hand-built BwdParams."""
     import torch
@@ -159,12 +160,15 @@ def test_backward_ds_workspace_too_small_falls_back():
     p.scale, p.causal, p.win_left, p.win_right, p.keep_scale = scale, 1, -1, -1, 1.0
     need = lib.fable_attn_bwd_ds_bytes(p, 1)
     assert need == B * Hq * 5 * 5 * 2048
-    ws = torch.full((need,), 0xFF, dtype=torch.uint8, device="cuda")  # NaN bit patterns
-    p.ds_ws, p.ds_ws_bytes = ws.data_ptr(), need - 1
+    ws = torch.full((need + 16,), 0xFF, dtype=torch.uint8, device="cuda")  # NaN bit patterns
     stream = ctypes_stream()
-    assert lib.fable_attn_backward_launch(p, 1, stream) == 0
-    torch.cuda.synchronize()
-    assert torch.all(ws == 0xFF), "a too-small workspace must not be written"
+    # too small, then big enough but not 16-byte aligned: both ignored
+    for ptr, nbytes in ((ws.data_ptr(), need - 1), (ws.data_ptr() + 8, need)):
+        p.ds_ws, p.ds_ws_bytes = ptr, nbytes
+        assert lib.fable_attn_backward_launch(p, 1, stream) == 0
+        torch.cuda.synchronize()
+        assert torch.all(ws == 0xFF), "an unusable workspace must not be written"
+    p.ds_ws = ws.data_ptr()
     ref = orc.bwd(q, k, v, do, scale, causal)
     for got, r, gname in ((dq, ref[0], "dq"), (dk, ref[1], "dk"), (dv, ref[2], "dv")):
         e = orc.rel_rms(to_np(got), r)
