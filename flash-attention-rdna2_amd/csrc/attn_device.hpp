@@ -77,6 +77,32 @@ __device__ __forceinline__ V bitcast(U u) {
   return __builtin_bit_cast(V, u);
 }
 
+// Store of one 32-column block of a row held in the v_mfma_f32_32x32 accumulator layout: lane
+// (r, hh) holds columns 8rq + 4hh + 0..3 of row r (rq = 0..3), scaled and rounded to T here.
+// A v_permlane32_swap per dword pair (lane l <-> l + 32, i.e. the other half of the same row)
+// trades the rq = 2j+1 run of lane hh = 0 for the rq = 2j run of lane hh = 1, leaving columns
+// 16j + 0..7 in lane hh = 0 and 16j + 8..15 in lane hh = 1: each row goes out in 16-byte stores,
+// 32 contiguous bytes per row and instruction, instead of 8-byte ones. Every lane executes the
+// swaps; `ok` (the same for both lanes of a row) only guards the stores.
+template <typename T>
+__device__ __forceinline__ void store_cblock(T* dst, const f32x16& acc, float scale, int hh, bool ok) {
+  using V4 = typename Dt<T>::V4;
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    V4 x, y;
+#pragma unroll
+    for (int c = 0; c < 4; c++) {
+      x[c] = (T)(acc[8 * j + c] * scale);
+      y[c] = (T)(acc[8 * j + 4 + c] * scale);
+    }
+    const u32x2 xd = __builtin_bit_cast(u32x2, x), yd = __builtin_bit_cast(u32x2, y);
+    const auto r0 = __builtin_amdgcn_permlane32_swap(xd[0], yd[0], false, false);
+    const auto r1 = __builtin_amdgcn_permlane32_swap(xd[1], yd[1], false, false);
+    const u32x4 o = {r0[0], r1[0], r0[1], r1[1]};
+    if (ok) *(u32x4*)(dst + 16 * j + 8 * hh) = o;
+  }
+}
+
 // 2^x on the transcendental unit (v_exp_f32): exp2(-inf) = 0.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -234,17 +234,10 @@ bwd_dq_kernel(BwdParams p, int nqt) {
     lstore(stage ^ 1);
     __syncthreads();
   }
-  if (qi < SQ) {
+  {
     T* row = dQg + (long long)qi * p.dqs.s;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++)
-#pragma unroll
-      for (int rq = 0; rq < 4; rq++) {
-        V4 v;
-#pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = (T)(dqacc[db][4 * rq + c] * p.scale);
-        *(V4*)(row + dbase + 32 * db + 8 * rq + 4 * hh) = v;
-      }
+    for (int db = 0; db < C::NDB; db++) store_cblock<T>(row + dbase + 32 * db, dqacc[db], p.scale, hh, qi < SQ);
   }
 }
 
@@ -437,22 +430,14 @@ bwd_dkdv_kernel(BwdParams p, int nkt) {
     lstore(stage ^ 1);
     __syncthreads();
   }
-  if (key < SK) {
+  {
     T* krow = (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (sq.ko + key) * p.dks.s;
     T* vrow = (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (sq.ko + key) * p.dvs.s;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++)
-#pragma unroll
-      for (int rq = 0; rq < 4; rq++) {
-        V4 vk, vv;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          vk[c] = (T)(dkacc[db][4 * rq + c] * p.scale);
-          vv[c] = (T)dvacc[db][4 * rq + c];
-        }
-        *(V4*)(krow + dbase + 32 * db + 8 * rq + 4 * hh) = vk;
-        *(V4*)(vrow + dbase + 32 * db + 8 * rq + 4 * hh) = vv;
-      }
+    for (int db = 0; db < C::NDB; db++) {
+      store_cblock<T>(krow + dbase + 32 * db, dkacc[db], p.scale, hh, key < SK);
+      store_cblock<T>(vrow + dbase + 32 * db, dvacc[db], 1.0f, hh, key < SK);
+    }
   }
 }
 
@@ -785,19 +770,12 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
         for_sets(std::make_integer_sequence<int, NSET>{}, [&](auto set) { s_step(set, it + decltype(set)::value); });
     }
   }
-  if (key < SK) {
+  {
     T* row = dpw ? (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (sq.ko + key) * p.dks.s
                  : (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (sq.ko + key) * p.dvs.s;
     const float sc = dpw ? p.scale : 1.0f;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++)
-#pragma unroll
-      for (int rq = 0; rq < 4; rq++) {
-        V4 v;
-#pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = (T)(acc[db][4 * rq + c] * sc);
-        *(V4*)(row + 32 * db + 8 * rq + 4 * hh) = v;
-      }
+    for (int db = 0; db < C::NDB; db++) store_cblock<T>(row + 32 * db, acc[db], sc, hh, key < SK);
   }
 }
 
@@ -1027,17 +1005,10 @@ bwd_dq_ds_kernel(BwdParams p, int nqt) {
   for (int t = 0; t < ntiles; t += NS)
     for_sets(std::make_integer_sequence<int, NS>{}, [&](auto set) { step(set, t + decltype(set)::value); });
   const int qi = qw + ds_slot_query(l32);
-  if (qi < SQ) {
+  {
     T* row = dQg + (long long)qi * p.dqs.s;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++)
-#pragma unroll
-      for (int rq = 0; rq < 4; rq++) {
-        V4 v;
-#pragma unroll
-        for (int c = 0; c < 4; c++) v[c] = (T)(dqacc[db][4 * rq + c] * p.scale);
-        *(V4*)(row + 32 * db + 8 * rq + 4 * hh) = v;
-      }
+    for (int db = 0; db < C::NDB; db++) store_cblock<T>(row + 32 * db, dqacc[db], p.scale, hh, qi < SQ);
   }
 }
 

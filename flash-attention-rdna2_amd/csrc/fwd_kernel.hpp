@@ -445,29 +445,9 @@ fwd_kernel(FwdParams p, int nqt) {
     const int qi = qw + 32 * i + l32;
     const float l_tot = half_sum(l_run[i]);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
-    // Lane (q, hh) holds head dims 32db + 8rq + 4hh + 0..3 of row q. Swapping the rq = 2j and
-    // rq = 2j+1 runs across the lane halves (v_permlane32_swap, lane l <-> l+32: the same row)
-    // leaves dims 32db + 16j + 0..7 in lane hh = 0 and 32db + 16j + 8..15 in lane hh = 1, so
-    // the row goes out in 16-byte stores, 32 contiguous bytes per row and instruction (8-byte
-    // stores cost narrow-window kernels 3-10%). Both lanes of a pair share qi, so the swap
-    // runs outside the row test.
     T* orow = Og + (long long)qi * p.sO.s;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++)
-#pragma unroll
-      for (int j = 0; j < 2; j++) {
-        V4 x, y;
-#pragma unroll
-        for (int c = 0; c < 4; c++) {
-          x[c] = (T)(oacc[i][db][8 * j + c] * inv);
-          y[c] = (T)(oacc[i][db][8 * j + 4 + c] * inv);
-        }
-        const u32x2 xd = __builtin_bit_cast(u32x2, x), yd = __builtin_bit_cast(u32x2, y);
-        const auto r0 = __builtin_amdgcn_permlane32_swap(xd[0], yd[0], false, false);
-        const auto r1 = __builtin_amdgcn_permlane32_swap(xd[1], yd[1], false, false);
-        const u32x4 o = {r0[0], r1[0], r0[1], r1[1]};
-        if (qi < SQ) *(u32x4*)(orow + db * 32 + 16 * j + 8 * hh) = o;
-      }
+    for (int db = 0; db < C::NDB; db++) store_cblock<T>(orow + db * 32, oacc[i][db], inv, hh, qi < SQ);
     if (qi < SQ) {
       if (p.LSE && hh == 0)
         p.LSE[sv.lse0 + qi] = l_tot > 0.0f ? m_run[i] * kLn2 + __logf(l_tot) : -INFINITY;
