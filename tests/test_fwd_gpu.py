@@ -194,3 +194,44 @@ def test_forward_full_size_sampled_heads(cfg):
         assert e <= TOL[dt], f"({bb},{hd}) O rel_rms {e:.3e} > {TOL[dt]}"
         le = (lse[bb, hd] - ref_lse).abs().max().item()
         assert le <= LSE_ABS, f"({bb},{hd}) LSE err {le:.3e}"
+
+
+def test_varlen_full_config_c5_sampled():
+    """BASELINE.json configs[4] at its full size: 8 packed sequences with seeded lengths in
+    [512, 8192], H=16, D=256, bf16, causal + window (512, 0) + softcap 30, one varlen launch.
+    Sampled (sequence, head) pairs against an exact float32 torch reference on the GPU
+    (softcap 30*tanh(s/30) on the scaled scores, then the window and causal masks), at the bf16
+    tolerance; LSE within 1e-3."""
+    import itertools
+
+    import torch
+
+    from fable_attn import _C
+    H, D, W, CAP = 16, 256, 512, 30.0
+    lens = torch.randint(512, 8193, (8,), generator=torch.Generator().manual_seed(0)).tolist()
+    offs = [0] + list(itertools.accumulate(lens))
+    print(f"[fwd-full] C5 varlen lens {lens}", flush=True)
+    cu = torch.tensor(offs, dtype=torch.int32, device="cuda")
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q, k, v = (torch.randn(offs[-1], H, D, device="cuda", dtype=torch.bfloat16, generator=g) for _ in range(3))
+    scale = D ** -0.5
+    out, lse = _C.fwd_varlen(q, k, v, cu, cu, max(lens), max(lens), scale, True, W, 0, CAP, None,
+                             0.0, 0, return_lse=True)
+    torch.cuda.synchronize()
+    for z, hd in ((0, 0), (3, 7), (7, H - 1), (int(np.argmax(lens)), 5)):
+        a, L = offs[z], lens[z]
+        qf = q[a:a + L, hd].float()
+        kf = k[a:a + L, hd].float().t().contiguous()
+        vf = v[a:a + L, hd].float()
+        s = CAP * torch.tanh((qf @ kf) * scale / CAP)
+        i = torch.arange(L, device="cuda")
+        vis = (i[None, :] <= i[:, None]) & (i[None, :] >= i[:, None] - W)
+        s = s.masked_fill(~vis, float("-inf"))
+        ref_lse = torch.logsumexp(s, -1)
+        ref = torch.softmax(s, -1) @ vf
+        del s
+        got = out[a:a + L, hd].float()
+        e = ((got - ref).norm() / ref.norm()).item()
+        assert e <= TOL["bf16"], f"(seq {z}, head {hd}) O rel_rms {e:.3e} > {TOL['bf16']}"
+        le = (lse[hd, a:a + L] - ref_lse).abs().max().item()
+        assert le <= LSE_ABS, f"(seq {z}, head {hd}) LSE err {le:.3e}"
