@@ -126,6 +126,28 @@ fwd_kernel(FwdParams p, int nqt) {
     m_run[i] = -INFINITY;
     l_run[i] = 0.0f;
   }
+  // FEAT masks: every mask (sequence end, causal, window, chunk) leaves row qi a single
+  // visible key interval [rlo, rhi), so the edge-tile test per score is one unsigned compare,
+  // with no uniform branches inside the score loop
+  int rlo[QB], rspan[QB];
+  if constexpr (FEAT) {
+#pragma unroll
+    for (int i = 0; i < QB; i++) {
+      // (64-bit: window and chunk sizes up to INT_MAX must not wrap)
+      const long long qd = qw + 32 * i + l32 + delta;
+      long long lo = 0, hi = SK;
+      if (CAUSAL) hi = min(hi, qd + 1);
+      if (p.win_left >= 0) lo = max(lo, qd - p.win_left);
+      if (p.win_right >= 0) hi = min(hi, qd + p.win_right + 1);
+      if (p.attn_chunk > 0) {
+        const long long cs = (max(qd, 0LL) / p.attn_chunk) * p.attn_chunk;
+        lo = max(lo, cs);
+        hi = min(hi, cs + p.attn_chunk);
+      }
+      rlo[i] = (int)lo;
+      rspan[i] = (int)max(hi - lo, 0LL);
+    }
+  }
   const float c_log2 = p.scale * kLog2e;
   const float aslope = (FEAT && p.alibi_slopes) ? p.alibi_slopes[h] : 0.0f;
 
@@ -245,17 +267,8 @@ fwd_kernel(FwdParams p, int nqt) {
             x = s[jb][r] * c_log2;
           }
           if constexpr ((decltype(cap)::value & 2) != 0) x = fmaf(aslope2, (float)(key - qi), x);
-          if constexpr (decltype(masked)::value) {
-            bool ok = key < SK;
-            if (CAUSAL) ok = ok && key <= qi + delta;
-            if (p.win_left >= 0) ok = ok && key >= qi + delta - p.win_left;
-            if (p.win_right >= 0) ok = ok && key <= qi + delta + p.win_right;
-            if (p.attn_chunk > 0) {
-              const int cs = (max(qi + delta, 0) / p.attn_chunk) * p.attn_chunk;
-              ok = ok && key >= cs && key < cs + p.attn_chunk;
-            }
-            x = ok ? x : -INFINITY;
-          }
+          if constexpr (decltype(masked)::value)
+            x = (unsigned)(key - rlo[i]) < (unsigned)rspan[i] ? x : -INFINITY;
           s[jb][r] = x;
           // bound how many scores the scheduler transforms at once (the softcap transform's
           // register pressure); plain logits are left to the scheduler
