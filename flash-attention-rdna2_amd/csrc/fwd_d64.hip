@@ -1,12 +1,12 @@
-// fwd_d64.hip — the fp16/bf16 forward kernels for head_dim 64 (workgroup shapes C, CF, CN of
+// fwd_d64.hip — the fp16/bf16 forward kernels for head_dim 64 (workgroup shapes C, CF, CN, CS of
 // launch_fwd in fwd_kernel.hpp).
 #include "fwd_kernel.hpp"
 
 namespace fa {
 
 int launch_fwd_d64(const FwdParams& p, int dtype, hipStream_t st) {
-  if (dtype == FA_F16) return launch_fwd<_Float16, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 4, 2>>(p, st);
-  return launch_fwd<__bf16, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 4, 2>>(p, st);
+  if (dtype == FA_F16) return launch_fwd<_Float16, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 4, 2>, FwdCfg<64, 64, 4, 2>>(p, st);
+  return launch_fwd<__bf16, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 4, 2>, FwdCfg<64, 64, 4, 2>>(p, st);
 }
 
 }  // namespace fa
