@@ -780,7 +780,10 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
 }
 
 // ------------------------------------------------------------ dQ from a dS workspace
-// D = rowsum(O*dO) for every (b, h, q) row: HD/8 lanes per row, one 16-byte chunk each.
+// D = rowsum(O*dO) for every (b, h, q) row: HD/8 lanes per row, one 16-byte chunk each, and
+// DSUM_RPT rows per lane whose loads are all in flight before the first sum (one row per lane
+// left each workgroup waiting on a single load pair: C3 33 us for 134 MB).
+constexpr int DSUM_RPT = 4;
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void bwd_dsum_kernel(BwdParams p, int rblocks) {
   constexpr int LPR = HD / 8, RPB = 256 / LPR;
@@ -789,19 +792,28 @@ __global__ __launch_bounds__(256) void bwd_dsum_kernel(BwdParams p, int rblocks)
   const int rb = blockIdx.x % rblocks, zh = blockIdx.x / rblocks;
   const int h = zh % p.Hq, b = zh / p.Hq;
   const BwdSeq sq = bwd_seq(p, b);
-  const int q = rb * RPB + tid / LPR, c = tid % LPR;
-  float acc = 0.0f;
-  if (q < sq.SQ) {
-    const V8 o = *(const V8*)((const T*)p.O + (long long)b * p.os.b + (sq.qo + q) * p.os.s +
-                              (long long)h * p.os.h + 8 * c);
-    const V8 d = *(const V8*)((const T*)p.dO + (long long)b * p.dos.b + (sq.qo + q) * p.dos.s +
-                              (long long)h * p.dos.h + 8 * c);
+  if (sq.SQ <= 0) return;
+  const int c = tid % LPR;
+  const T* ob = (const T*)p.O + (long long)b * p.os.b + (long long)h * p.os.h + 8 * c;
+  const T* db = (const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + 8 * c;
+  V8 o[DSUM_RPT], d[DSUM_RPT];
 #pragma unroll
-    for (int e = 0; e < 8; e++) acc += (float)o[e] * (float)d[e];
+  for (int r = 0; r < DSUM_RPT; r++) {
+    // rows past the end load the last row (in bounds) and are not stored
+    const int q = min((rb * DSUM_RPT + r) * RPB + tid / LPR, sq.SQ - 1);
+    o[r] = *(const V8*)(ob + (sq.qo + q) * p.os.s);
+    d[r] = *(const V8*)(db + (sq.qo + q) * p.dos.s);
   }
 #pragma unroll
-  for (int m = LPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m);
-  if (c == 0 && q < sq.SQ) p.dsum[(long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + q] = acc;
+  for (int r = 0; r < DSUM_RPT; r++) {
+    const int q = (rb * DSUM_RPT + r) * RPB + tid / LPR;
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 8; e++) acc += (float)o[r][e] * (float)d[r][e];
+#pragma unroll
+    for (int m = LPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m);
+    if (c == 0 && q < sq.SQ) p.dsum[(long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + q] = acc;
+  }
 }
 
 template <int HD_, int NW_, int WPE_, int NS_, int BC_ = 64>
@@ -1024,7 +1036,7 @@ static long long ds_bytes(const BwdParams& p) {
 template <typename T, class CKV, bool CAUSAL, bool FEAT, bool DROP>
 static int launch_bwd_ds(const BwdParams& p, hipStream_t st, int nkt) {
   using CD = BwdDsQCfg<CKV::HD, 8, 2, DSQ_NS>;
-  constexpr int RPB = 256 / (CKV::HD / 8);
+  constexpr int RPB = 256 / (CKV::HD / 8) * DSUM_RPT;  // rows per dsum workgroup
   const long long gd = (long long)((p.SQ + RPB - 1) / RPB) * p.Hq * p.B;
   const int nqt = (p.SQ + CD::BQ - 1) / CD::BQ;
   const long long gq = (long long)nqt * p.Hq * p.B;
