@@ -186,6 +186,40 @@ def summarize_pmc(fetch_dir, write_dir, kernel_re=None):
     return "\n".join(out)
 
 
+def summarize_mfma(d, kernel_re=None):
+    """Markdown table of matrix-core utilisation per kernel from a `rocprofv3 --pmc
+    SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE` run. SQ_VALU_MFMA_BUSY_CYCLES sums the busy
+    cycles of every SIMD's matrix core; GRBM_GUI_ACTIVE sums the active cycles of every XCD, so
+    GRBM_GUI_ACTIVE / Num_Xcc / duration is the dispatch's mean clock. Utilisation at that
+    clock = busy / (Simd_Count x active cycles per XCD); at the peak clock = busy /
+    (Simd_Count x duration x Max_Engine_Clk_Fcompute)."""
+    agent = [r for r in _rocprof_rows(d, "agent_info.csv") if int(r.get("Simd_Count") or 0) > 0][0]
+    simds, nxcc = int(agent["Simd_Count"]), int(agent["Num_Xcc"])
+    fmax_ghz = float(agent["Max_Engine_Clk_Fcompute"]) / 1e3
+    disp = {}
+    for r in _rocprof_rows(d, "counter_collection.csv"):
+        if kernel_re and not re.search(kernel_re, r["Kernel_Name"]):
+            continue
+        e = disp.setdefault((r["Kernel_Name"], r["Dispatch_Id"]), {})
+        e[r["Counter_Name"]] = float(r["Counter_Value"])
+        e["ns"] = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+    per = {}
+    for (k, _), e in disp.items():
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in e and e.get("GRBM_GUI_ACTIVE", 0) > 0 and e["ns"] > 0:
+            per.setdefault(k, []).append(e)
+    out = [f"| kernel | dispatches | average us | mean clock GHz | MFMA busy at that clock | "
+           f"MFMA busy at {fmax_ghz:.1f} GHz |", "|---|---|---|---|---|---|"]
+    for k, es in sorted(per.items(), key=lambda kv: -sum(e["ns"] for e in kv[1])):
+        busy = sum(e["SQ_VALU_MFMA_BUSY_CYCLES"] for e in es)
+        cyc = sum(e["GRBM_GUI_ACTIVE"] for e in es) / nxcc
+        ns = sum(e["ns"] for e in es)
+        out.append(f"| `{k[:100]}` | {len(es)} | {ns / len(es) / 1e3:.1f} | {cyc / ns:.2f} | "
+                   f"{busy / (simds * cyc):.1%} | {busy / (simds * ns * fmax_ghz):.1%} |")
+    out.append("")
+    out.append(f"Agent: {simds} SIMDs, {nxcc} XCDs, peak engine clock {fmax_ghz:.1f} GHz.")
+    return "\n".join(out)
+
+
 def summarize_stats(d, kernel_re=None, skip=0):
     """Markdown table of the `rocprofv3 --kernel-trace --stats` kernel statistics, with the
     average over the dispatches after the first `skip` of each kernel (bench.py's warmup calls)
@@ -259,6 +293,9 @@ def main():
                     help="print the calibrated PMC table of two rocprofv3 --pmc runs and exit")
     ap.add_argument("--summarize-stats", metavar="DIR",
                     help="print the rocprofv3 --stats kernel table and exit")
+    ap.add_argument("--summarize-mfma", metavar="DIR",
+                    help="print the matrix-core utilisation table of a rocprofv3 --pmc "
+                         "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE run and exit")
     ap.add_argument("--kernel-filter", default=None, help="regex on kernel symbols (summaries)")
     ap.add_argument("--skip", type=int, default=0, help="leading dispatches to skip (summaries)")
     a = ap.parse_args()
@@ -267,6 +304,9 @@ def main():
         return
     if a.summarize_stats:
         print(summarize_stats(a.summarize_stats, a.kernel_filter, a.skip))
+        return
+    if a.summarize_mfma:
+        print(summarize_mfma(a.summarize_mfma, a.kernel_filter))
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the reference has no multi-GPU "
