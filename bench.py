@@ -13,7 +13,8 @@ by its average duration, measured with HIP events on the stream the kernel is la
 `cpu_baseline` times the exact fp32 torch reference (oracle/torch_ref.py) on the host cores over
 a bounded sample of heads of the same workload and scales to TFLOP/s with the same numerator.
 `extra` holds the other BASELINE.json configs (backward, paged decode, varlen) measured the
-same way; they are not the headline.
+same way (at least 3 warmup and 20 timed steps each), with the mean and the median of the
+per-step HIP-event times; they are not the headline.
 """
 import argparse
 import json
@@ -35,23 +36,32 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_steps(fn, steps, warmup):
-    """Returns (wall ms/step, HIP-event ms/step) over exactly `steps` calls after `warmup`."""
+def time_steps(fn, steps, warmup, per_step=None):
+    """Returns (wall ms/step, HIP-event ms/step) over exactly `steps` calls after `warmup`.
+    With a list as `per_step`, also appends each step's own HIP-event time to it (an event
+    pair per step, recorded on the same stream, for medians)."""
     import torch
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
     st = torch.cuda.current_stream()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ev_all = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
-    e0.record(st)
-    for _ in range(steps):
+    ev_all[0].record(st)
+    for i in range(steps):
         fn()
-    e1.record(st)
+        ev_all[i + 1].record(st)
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3 / steps
-    ev = e0.elapsed_time(e1) / steps
+    ev = ev_all[0].elapsed_time(ev_all[-1]) / steps
+    if per_step is not None:
+        per_step += [ev_all[i].elapsed_time(ev_all[i + 1]) for i in range(steps)]
     return wall, ev
+
+
+def _median(x):
+    x = sorted(x)
+    return 0.5 * (x[(len(x) - 1) // 2] + x[len(x) // 2])
 
 
 def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", seed=0):
@@ -63,10 +73,12 @@ def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", see
     k = torch.randn(B, S, H, D, device="cuda", dtype=dt, generator=g)
     v = torch.randn(B, S, H, D, device="cuda", dtype=dt, generator=g)
     flops = 4.0 * B * H * S * S * D / (2 if causal else 1)
-    wall, ev = time_steps(lambda: flash_attn_func(q, k, v, causal=causal), steps, warmup)
+    per = []
+    wall, ev = time_steps(lambda: flash_attn_func(q, k, v, causal=causal), steps, warmup, per)
     return {"S": S, "H": H, "D": D, "B": B, "causal": causal, "dtype": dtype, "flops": flops,
             "ms": wall, "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
-            "kernel_tflops": flops / (ev * 1e-3) / 1e12}
+            "kernel_tflops": flops / (ev * 1e-3) / 1e12, "kernel_ms_median": _median(per),
+            "tflops_median": flops / (_median(per) * 1e-3) / 1e12}
 
 
 def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0):
@@ -85,10 +97,12 @@ def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0):
         return _C.bwd(doh, qh, kh, vh, out, lse, scale, True, -1, 0, 0.0, None, 0.0, 0)
     ref = step()
     same = all(all(torch.equal(a, b) for a, b in zip(ref, step())) for _ in range(2))
-    wall, ev = time_steps(step, steps, warmup)
+    per = []
+    wall, ev = time_steps(step, steps, warmup, per)
     flops = 2.5 * 4.0 * B * H * S * S * D / 2
     return {"B": B, "S": S, "H": H, "D": D, "dtype": "bf16", "flops": flops, "ms": wall,
             "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
+            "kernel_ms_median": _median(per), "tflops_median": flops / (_median(per) * 1e-3) / 1e12,
             "bitwise_identical_x3": bool(same)}
 
 
@@ -106,10 +120,12 @@ def bench_decode(steps, warmup, batch=16, Hq=32, Hk=8, D=128, ctx=32768, page=25
     bt = torch.randperm(nblk, generator=cg).view(batch, ctx // page).int().cuda()
     cs = torch.full((batch,), ctx, dtype=torch.int32, device="cuda")
     f = lambda: flash_attn_with_kvcache(q, kc, vc, cache_seqlens=cs, block_table=bt)
-    wall, ev = time_steps(f, steps, warmup)
+    per = []
+    wall, ev = time_steps(f, steps, warmup, per)
     nbytes = 2.0 * batch * ctx * Hk * D * 2
     return {"batch": batch, "Hq": Hq, "Hk": Hk, "D": D, "ctx": ctx, "page": page, "bytes": nbytes,
             "ms": wall, "kernel_ms": ev, "GBs": nbytes / (wall * 1e-3) / 1e9,
+            "kernel_ms_median": _median(per), "GBs_median": nbytes / (_median(per) * 1e-3) / 1e9,
             "frac_hbm": nbytes / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS,
             "traffic_partial_kernel": profiled_traffic(DEC_C4_KERNEL)}
 
@@ -127,11 +143,13 @@ def bench_varlen(steps, warmup, H=16, D=256, seed=0):
     q, k, v = (torch.randn(T, H, D, device="cuda", dtype=torch.bfloat16, generator=g) for _ in range(3))
     f = lambda: flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), causal=True,
                                        window_size=(512, 0), softcap=30.0, softmax_scale=D ** -0.5)
-    wall, ev = time_steps(f, steps, warmup)
+    per = []
+    wall, ev = time_steps(f, steps, warmup, per)
     pairs = sum(sum(min(i, 512) + 1 for i in range(L)) for L in lens)
     flops = 4.0 * D * H * pairs
     return {"lens": lens, "H": H, "D": D, "flops": flops, "ms": wall, "kernel_ms": ev,
-            "tflops": flops / (wall * 1e-3) / 1e12}
+            "tflops": flops / (wall * 1e-3) / 1e12, "kernel_ms_median": _median(per),
+            "tflops_median": flops / (_median(per) * 1e-3) / 1e12}
 
 
 # ---- rocprofv3 summaries (CPU only: they read the CSV files rocprofv3 wrote) ----------------
@@ -325,14 +343,14 @@ def main():
         try:
             if name == "fwd":
                 for S in (4096, 8192):
-                    extra[f"fwd_causal_S{S}"] = bench_fwd(S, max(a.steps, 10), a.warmup)
+                    extra[f"fwd_causal_S{S}"] = bench_fwd(S, max(a.steps, 20), max(3, a.warmup))
                 extra["fwd_C1_S1024_D64_noncausal"] = bench_fwd(1024, 20, 3, causal=False, H=8, D=64)
             elif name == "bwd":
-                extra["bwd_C3"] = bench_bwd(max(5, a.steps // 2), 2)
+                extra["bwd_C3"] = bench_bwd(max(20, a.steps), max(3, a.warmup))
             elif name == "decode":
-                extra["decode_C4"] = bench_decode(max(a.steps, 20), a.warmup)
+                extra["decode_C4"] = bench_decode(max(a.steps, 20), max(3, a.warmup))
             elif name == "varlen":
-                extra["varlen_C5"] = bench_varlen(max(5, a.steps // 2), 2)
+                extra["varlen_C5"] = bench_varlen(max(20, a.steps), max(3, a.warmup))
             log(f"[bench] extra {name} done")
         except RuntimeError as e:
             extra[name] = {"error": str(e)[:300]}
