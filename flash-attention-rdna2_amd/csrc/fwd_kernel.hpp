@@ -68,8 +68,18 @@ __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
 fwd_kernel(FwdParams p, int nqt) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
-  __shared__ __attribute__((aligned(16))) T kl[2 * C::KTILE];
-  __shared__ __attribute__((aligned(16))) T vl[2 * C::VTILE];
+  // K/V rings of NST stages, a barrier every BP tiles. Iteration t reads K tile t+1 and V tile t
+  // and stores K tile t+BP+1 and V tile t+BP, so what it reads was stored BP iterations earlier
+  // and what it overwrites was last read BP iterations earlier: a barrier in every BP
+  // consecutive iterations orders both. With BP = 2 the waves may drift up to two tiles apart
+  // between barriers, so the two waves of a SIMD fall out of step and one's softmax runs under
+  // the other's products. Used by the 8-wave D=128 shape (151.5 KB of LDS, one workgroup per
+  // CU either way): C2 +0.4-1.9%, bf16 +1.9%, window 4096 +7.6%. The 8-wave D=64 shape was
+  // 3.7% slower with it; the shorter shapes would lose workgroups per CU to the LDS.
+  constexpr int NST = (C::NW == 8 && C::HD == 128) ? 4 : 2;
+  constexpr int BP = NST / 2;
+  __shared__ __attribute__((aligned(16))) T kl[NST * C::KTILE];
+  __shared__ __attribute__((aligned(16))) T vl[NST * C::VTILE];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
@@ -362,12 +372,15 @@ fwd_kernel(FwdParams p, int nqt) {
   // ---- prologue: K tiles 0 and 1, V tile 0 in LDS; S and P of tile 0
   V8 pb[QB][C::NG];
   if (ntiles > 0) {
-    gload_k(kstart);
-    gload_v(kstart);
-    lstore_k(0);
-    lstore_v(0);
-    gload_k(kstart + C::BC);
-    lstore_k(1);
+#pragma unroll
+    for (int j = 0; j < BP; j++) {
+      gload_k(kstart + j * C::BC);
+      gload_v(kstart + j * C::BC);
+      lstore_k(j);
+      lstore_v(j);
+    }
+    gload_k(kstart + BP * C::BC);
+    lstore_k(BP);
   }
   __syncthreads();
   bool a_cur = false;
@@ -412,18 +425,18 @@ fwd_kernel(FwdParams p, int nqt) {
   for (; t + 1 < nint; t++) {
     rescale();
     const int kb1 = kstart + (t + 1) * C::BC;
-    gload_k(kb1 + C::BC);
-    gload_v(kb1);
+    gload_k(kb1 + BP * C::BC);
+    gload_v(kb1 + (BP - 1) * C::BC);
     f32x16 s[QB][C::NB];
     __builtin_amdgcn_s_setprio(1);
-    qk((t + 1) & 1, s);
+    qk((t + 1) & (NST - 1), s);
     __builtin_amdgcn_s_setprio(0);
-    pv(t & 1, pb);
+    pv(t & (NST - 1), pb);
 #pragma unroll
     for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, Cap0{}, i, s[i], kb1, pb[i], resc[i]);
-    lstore_k(t & 1);
-    lstore_v((t + 1) & 1);
-    __syncthreads();
+    lstore_k((t + BP + 1) & (NST - 1));
+    lstore_v((t + BP) & (NST - 1));
+    if (BP == 1 || t % BP == BP - 1) __syncthreads();
   }
   if (t < ntiles && t > 0) a_cur = active(t);
   if constexpr (FEAT && !DROP && C::WPE == 1) {
@@ -445,30 +458,30 @@ fwd_kernel(FwdParams p, int nqt) {
       for (; t < ntiles; t++) {
         rescale();
         const int kb1 = kstart + (t + 1) * C::BC;
-        gload_k(kb1 + C::BC);
-        gload_v(kb1);
+        gload_k(kb1 + BP * C::BC);
+        gload_v(kb1 + (BP - 1) * C::BC);
         f32x16 s[QB][C::NB];
         __builtin_amdgcn_s_setprio(1);
-        qk((t + 1) & 1, s);
+        qk((t + 1) & (NST - 1), s);
         __builtin_amdgcn_s_setprio(0);
-        pv(t & 1, pb);
+        pv(t & (NST - 1), pb);
 #pragma unroll
         for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, cap, i, s[i], kb1, pb[i], resc[i]);
-        lstore_k(t & 1);
-        lstore_v((t + 1) & 1);
-        __syncthreads();
+        lstore_k((t + BP + 1) & (NST - 1));
+        lstore_v((t + BP) & (NST - 1));
+        if (BP == 1 || t % BP == BP - 1) __syncthreads();
       }
     });
   }
   for (; t < ntiles; t++) {
     rescale();
     const int kb1 = kstart + (t + 1) * C::BC;
-    gload_k(kb1 + C::BC);
-    gload_v(kb1);
+    gload_k(kb1 + BP * C::BC);
+    gload_v(kb1 + (BP - 1) * C::BC);
     const bool a_next = t + 1 < ntiles && active(t + 1);
     f32x16 s[QB][C::NB];
-    if (a_next) qk((t + 1) & 1, s);
-    if (a_cur) pv(t & 1, pb);
+    if (a_next) qk((t + 1) & (NST - 1), s);
+    if (a_cur) pv(t & (NST - 1), pb);
     if (a_next) {
       // FEAT tiles every row of the wave sees in full skip the mask code
       auto sm = [&](auto masked, auto cap) {
@@ -481,9 +494,9 @@ fwd_kernel(FwdParams p, int nqt) {
         with_fmode([&](auto cap) { sm(Masked{}, cap); });
     }
     a_cur = a_next;
-    lstore_k(t & 1);
-    lstore_v((t + 1) & 1);
-    __syncthreads();
+    lstore_k((t + BP + 1) & (NST - 1));
+    lstore_v((t + BP) & (NST - 1));
+    if (BP == 1 || t % BP == BP - 1) __syncthreads();
   }
 
   // ---- epilogue: O = acc / l, LSE
