@@ -32,6 +32,9 @@ CASES = [
     ("window (32,32) SQ<SK", 1, 128, 320, 128, 16, 4, False, 32, 32, 0.0, False, 0),
     ("softcap 30", 1, 200, 200, 128, 16, 4, True, -1, -1, 30.0, False, 0),
     ("alibi", 1, 200, 200, 128, 16, 4, True, -1, -1, 0.0, True, 0),
+    # the 8-wave shape's four-stage K/V ring over one and three tiles
+    ("alibi one tile", 1, 64, 64, 128, 16, 4, True, -1, -1, 0.0, True, 0),
+    ("alibi SQ<SK three tiles", 1, 100, 150, 128, 16, 2, False, -1, -1, 0.0, True, 0),
     ("d64 causal ragged", 1, 200, 200, 64, 16, 4, True, -1, -1, 0.0, False, 0),
     ("d256 causal", 1, 160, 160, 256, 8, 4, True, -1, -1, 0.0, False, 0),
     ("d256 full SQ<SK", 1, 96, 200, 256, 8, 2, False, -1, -1, 0.0, False, 0),
