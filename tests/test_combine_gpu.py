@@ -7,6 +7,8 @@
   over all keys (the reference's own check, test_fable_attn.py:232-240), at the fp16 bound.
 - return_attn_probs (flash_attn_interface.py:370-374): the probability matrix against the fp64
   oracle's softmax; every row that sees a key sums to one.
+- The qv term and a value head dim below the score head dim (flash_attn_interface.py:160-191),
+  forward and autograd backward, against the oracle on the concatenated problem.
 """
 import numpy as np
 import pytest
@@ -129,3 +131,48 @@ def test_return_attn_probs(causal, window):
     assert inf_ok and lerr <= LSE_ABS
     rel = orc.rel_rms(to_np(out).transpose(0, 2, 1, 3), ref_o)
     assert rel <= TOL[dt]
+
+
+@pytest.mark.parametrize("kind", ["qv", "headdim_v"])
+def test_qv_forward_backward(kind):
+    """FA-3's qv term (S = q.k^T + qv.v^T, reference flash_attn_interface.py:160-191) and a value
+    head dim below the score head dim, through flash_attn_func and autograd, against the fp64
+    oracle on the concatenated problem [q | qv] . [k | v]^T with values [v | 0]; gradients split
+    back (dv gets both its value and its key part)."""
+    import torch
+
+    from fable_attn import flash_attn_func
+    from tests.helpers import torch_dtype
+    B, S, H, D, dt = 1, 160, 4, 64, "f16"
+    Dk = D if kind == "qv" else 2 * D         # score head dim of q and k
+    print(f"[qv] {kind}", flush=True)
+    q = gen((B, S, H, Dk), 31, dt)
+    k = gen((B, S, H, Dk), 32, dt)
+    v = gen((B, S, H, D), 33, dt)
+    qv = gen((B, S, H, D), 34, dt) if kind == "qv" else None
+    do = gen((B, S, H, D), 35, dt)
+    scale = 0.1
+    ts = [to_dev(x, dt).requires_grad_() for x in (q, k, v)]
+    tqv = to_dev(qv, dt).requires_grad_() if qv is not None else None
+    out = flash_attn_func(*ts, softmax_scale=scale, causal=True, qv=tqv)
+    out.backward(to_dev(do, dt))
+    # the concatenated fp64 problem
+    z = np.zeros((B, S, H, D), dtype=np.float32)
+    qc = np.concatenate([q, qv if qv is not None else z], -1)
+    kc = np.concatenate([k, v], -1)
+    vc = np.concatenate([v, np.zeros((B, S, H, qc.shape[-1] - D), np.float32)], -1)
+    doc = np.concatenate([do, np.zeros_like(vc[..., D:])], -1)
+    th = lambda x: np.ascontiguousarray(x.transpose(0, 2, 1, 3))
+    ref_o, _ = orc.fwd(th(qc), th(kc), th(vc), scale, causal=True, win_right=0)
+    dqc, dkc, dvc = orc.bwd(th(qc), th(kc), th(vc), th(doc), scale, causal=True, win_right=0)
+    ref_o = ref_o[..., :D]
+    rel = orc.rel_rms(to_np(out).transpose(0, 2, 1, 3), ref_o)
+    assert rel <= TOL[dt], f"out rel_rms {rel:.3e}"
+    ref_g = {"dq": dqc[..., :Dk], "dk": dkc[..., :Dk], "dv": dkc[..., Dk:] + dvc[..., :D]}
+    got_g = {"dq": ts[0].grad, "dk": ts[1].grad, "dv": ts[2].grad}
+    if qv is not None:
+        ref_g["dqv"] = dqc[..., Dk:]
+        got_g["dqv"] = tqv.grad
+    for name, g in got_g.items():
+        e = orc.rel_rms(to_np(g).transpose(0, 2, 1, 3), ref_g[name])
+        assert e <= 2e-3, f"{name} rel_rms {e:.3e}"
