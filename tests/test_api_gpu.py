@@ -1,0 +1,86 @@
+"""The packed and paged entry points of the flash_attn API on the GPU: each must give exactly
+what the plain entry point gives on the same data (they are views / gathers in front of the same
+kernels), and the plain entry point is checked against the fp64 oracle here too.
+Reference: flash_attn_interface.py:391-469 (packed variants, paged varlen)."""
+import itertools
+
+import numpy as np
+import pytest
+
+from oracle import oracle as orc
+from tests.helpers import TOL, gen, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_packed_variants_equal_plain(causal):
+    import torch
+
+    from fable_attn import (flash_attn_func, flash_attn_kvpacked_func, flash_attn_qkvpacked_func,
+                            flash_attn_varlen_func, flash_attn_varlen_kvpacked_func,
+                            flash_attn_varlen_qkvpacked_func)
+    B, S, H, D, dt = 2, 130, 4, 64, "f16"
+    print(f"[packed] causal={causal}", flush=True)
+    qkv = to_dev(gen((B, S, 3, H, D), 41, dt), dt)
+    q, k, v = qkv.unbind(2)
+    plain = flash_attn_func(q, k, v, causal=causal)
+    assert torch.equal(flash_attn_qkvpacked_func(qkv, causal=causal), plain)
+    assert torch.equal(flash_attn_kvpacked_func(q, qkv[:, :, 1:], causal=causal), plain)
+    ref, _ = orc.fwd(*(np.ascontiguousarray(to_np(x).transpose(0, 2, 1, 3)) for x in (q, k, v)),
+                     D ** -0.5, causal=causal, win_right=0 if causal else -1)
+    assert orc.rel_rms(to_np(plain).transpose(0, 2, 1, 3), ref) <= TOL[dt]
+    # varlen: the batch packed as two sequences of length S
+    cu = torch.tensor([0, S, 2 * S], dtype=torch.int32, device="cuda")
+    qkv_p = qkv.reshape(B * S, 3, H, D)
+    vl = flash_attn_varlen_func(qkv_p[:, 0], qkv_p[:, 1], qkv_p[:, 2], cu, cu, S, S, causal=causal)
+    assert torch.equal(flash_attn_varlen_qkvpacked_func(qkv_p, cu, S, causal=causal), vl)
+    assert torch.equal(flash_attn_varlen_kvpacked_func(qkv_p[:, 0], qkv_p[:, 1:], cu, cu, S, S,
+                                                       causal=causal), vl)
+    assert orc.rel_rms(to_np(vl).reshape(B, S, H, D), to_np(plain)) <= TOL[dt]
+
+
+def test_paged_varlen_equals_packed():
+    """varlen prefill with K/V in pages (num_blocks, page, Hk, D) and a block table (a seeded
+    permutation of the pages) against the same sequences packed contiguously."""
+    import torch
+
+    from fable_attn import flash_attn_varlen_func
+    lens_q, lens_k, Hq, Hk, D, page, dt = [37, 64, 100], [90, 64, 230], 8, 2, 128, 16, "bf16"
+    print("[paged-varlen]", flush=True)
+    cq = [0] + list(itertools.accumulate(lens_q))
+    ck = [0] + list(itertools.accumulate(lens_k))
+    q = to_dev(gen((cq[-1], Hq, D), 51, dt), dt)
+    k = to_dev(gen((ck[-1], Hk, D), 52, dt), dt)
+    v = to_dev(gen((ck[-1], Hk, D), 53, dt), dt)
+    cu_q = torch.tensor(cq, dtype=torch.int32, device="cuda")
+    cu_k = torch.tensor(ck, dtype=torch.int32, device="cuda")
+    packed = flash_attn_varlen_func(q, k, v, cu_q, cu_k, max(lens_q), max(lens_k), causal=True)
+    # pages: sequence i's keys fill its pages in order; the pages sit at permuted slots
+    npg = [(L + page - 1) // page for L in lens_k]
+    total = sum(npg)
+    perm = torch.randperm(total, generator=torch.Generator().manual_seed(5))
+    kp = torch.zeros(total, page, Hk, D, dtype=k.dtype, device="cuda")
+    vp = torch.zeros_like(kp)
+    bt = torch.zeros(len(lens_k), max(npg), dtype=torch.int32)
+    slot = 0
+    for i, L in enumerate(lens_k):
+        for j in range(npg[i]):
+            phys = int(perm[slot])
+            slot += 1
+            bt[i, j] = phys
+            r0, r1 = ck[i] + j * page, min(ck[i] + (j + 1) * page, ck[i + 1])
+            kp[phys, :r1 - r0] = k[r0:r1]
+            vp[phys, :r1 - r0] = v[r0:r1]
+    paged = flash_attn_varlen_func(q, kp, vp, cu_q, cu_k, max(lens_q), max(lens_k), causal=True,
+                                   block_table=bt.cuda())
+    assert torch.equal(paged, packed)
+    # and the packed result against the oracle, per sequence
+    for i in range(len(lens_q)):
+        qi = to_np(q[cq[i]:cq[i + 1]]).transpose(1, 0, 2)[None]
+        ki = to_np(k[ck[i]:ck[i + 1]]).transpose(1, 0, 2)[None]
+        vi = to_np(v[ck[i]:ck[i + 1]]).transpose(1, 0, 2)[None]
+        ref, _ = orc.fwd(np.ascontiguousarray(qi), np.ascontiguousarray(ki), np.ascontiguousarray(vi),
+                         D ** -0.5, causal=True, win_right=0)
+        got = to_np(packed[cq[i]:cq[i + 1]]).transpose(1, 0, 2)[None]
+        assert orc.rel_rms(got, ref) <= TOL[dt], f"sequence {i}"
