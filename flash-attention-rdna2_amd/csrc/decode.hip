@@ -147,17 +147,19 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
   };
   // K/V rows of the chunk at kc0: K as the A operand (key kc0 + 16*kb + lh, head-dim
   // 32*ds + 8*lg); V load i covers row (64i + lane) / RCH, 16-byte chunk (64i + lane) % RCH
+  // The cache rows are read once per step: non-temporal loads keep them from displacing the
+  // block table and q in the caches (C4: 368.6 -> 360.3 us for the partial kernel).
   auto load = [&](int kc0, u32x4 (&kr)[2][NDS], u32x4 (&vr)[NVI]) {
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
       const long long base = row_off(kblk[kb], kkey(kc0, kb));
 #pragma unroll
-      for (int ds = 0; ds < NDS; ds++) kr[kb][ds] = *(const u32x4*)(Kc + base + 32 * ds + 8 * lg);
+      for (int ds = 0; ds < NDS; ds++) kr[kb][ds] = __builtin_nontemporal_load((const u32x4*)(Kc + base + 32 * ds + 8 * lg));
     }
 #pragma unroll
     for (int i = 0; i < NVI; i++) {
       const int ch = (64 * i + lane) % RCH;
-      vr[i] = *(const u32x4*)(Vc + row_off(vblk[i], vkey(kc0, i)) + 8 * ch);
+      vr[i] = __builtin_nontemporal_load((const u32x4*)(Vc + row_off(vblk[i], vkey(kc0, i)) + 8 * ch));
     }
   };
   // Software pipeline: the rows of the next chunk are in flight while this one is computed;
