@@ -7,7 +7,10 @@
  * a CPU test checks the offsets against this file compiled with gcc). Parameter structs are
  * passed BY VALUE, exactly as the reference passes them, and are plain C: fixed-width fields,
  * device pointers as `const void*` / `void*`, strides in ELEMENTS, the innermost (head_dim)
- * stride is always 1. No torch or HIP types appear in any signature; a stream is `void*`
+ * stride is always 1. Every row of every tensor (its base pointer plus any combination of its
+ * strides) must be 16-byte aligned: the kernels move rows in 16-byte loads and stores (for
+ * 16-bit types, pointers and strides multiples of 8 elements; the Python binding checks this).
+ * No torch or HIP types appear in any signature; a stream is `void*`
  * (a `hipStream_t`, NULL = the legacy default stream).
  *
  * Reference interface replaced (paths relative to the reference repository root):
