@@ -428,11 +428,11 @@ fwd_kernel(FwdParams p, int nqt) {
     gload_k(kb1 + BP * C::BC);
     gload_v(kb1 + (BP - 1) * C::BC);
     f32x16 s[QB][C::NB];
-    // raised wave priority over the S product: +1-3% at D=128; at D=64, where the product is
-    // half as long, 1.5-6% slower, so not there
-    if constexpr (C::HD != 64) __builtin_amdgcn_s_setprio(1);
+    // raised wave priority over the S product: +1-3% at D=128; 1.5-6% slower at D=64 and 4-6%
+    // slower at D=256 (one wave per SIMD there: nothing to take priority over), so not there
+    if constexpr (C::HD == 128) __builtin_amdgcn_s_setprio(1);
     qk((t + 1) & (NST - 1), s);
-    if constexpr (C::HD != 64) __builtin_amdgcn_s_setprio(0);
+    if constexpr (C::HD == 128) __builtin_amdgcn_s_setprio(0);
     pv(t & (NST - 1), pb);
 #pragma unroll
     for (int i = 0; i < QB; i++) corr[i] = softmax(Plain{}, Cap0{}, i, s[i], kb1, pb[i], resc[i]);
@@ -463,9 +463,9 @@ fwd_kernel(FwdParams p, int nqt) {
         gload_k(kb1 + BP * C::BC);
         gload_v(kb1 + (BP - 1) * C::BC);
         f32x16 s[QB][C::NB];
-        if constexpr (C::HD != 64) __builtin_amdgcn_s_setprio(1);
+        if constexpr (C::HD == 128) __builtin_amdgcn_s_setprio(1);
         qk((t + 1) & (NST - 1), s);
-        if constexpr (C::HD != 64) __builtin_amdgcn_s_setprio(0);
+        if constexpr (C::HD == 128) __builtin_amdgcn_s_setprio(0);
         pv(t & (NST - 1), pb);
 #pragma unroll
         for (int i = 0; i < QB; i++) corr[i] = softmax(Masked{}, cap, i, s[i], kb1, pb[i], resc[i]);
