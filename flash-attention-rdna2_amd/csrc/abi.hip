@@ -25,17 +25,26 @@ int launch_status(const char* what) {
 }  // namespace fa
 
 static_assert(sizeof(fa_strides) == 24, "fa_strides layout");
-static_assert(offsetof(FwdParams, sQ) == 40, "FwdParams layout");
+static_assert(offsetof(FableFwdParams, sQ) == 40, "FableFwdParams layout");
+// the reference layouts (fa_iface.h:9-63 compiled for x86-64 / gfx950, both LP64)
+static_assert(sizeof(FwdParams) == 256 && offsetof(FwdParams, sc_q) == 220 && offsetof(FwdParams, seqused_k) == 248,
+              "FwdParams must match the reference layout");
+static_assert(sizeof(BwdParams) == 368 && offsetof(BwdParams, shQ) == 352, "BwdParams must match the reference layout");
+static_assert(sizeof(DecParams) == 192 && offsetof(DecParams, page_shift) == 104 && offsetof(DecParams, rotary_pos) == 184,
+              "DecParams must match the reference layout");
 
 extern "C" int fable_attn_abi_version(void) { return FABLE_ATTN_ABI_VERSION; }
 
 extern "C" size_t fable_attn_struct_size(int which) {
   switch (which) {
-    case 0: return sizeof(FwdParams);
-    case 1: return sizeof(BwdParams);
-    case 2: return sizeof(DecParams);
+    case 0: return sizeof(FableFwdParams);
+    case 1: return sizeof(FableBwdParams);
+    case 2: return sizeof(FableDecParams);
     case 3: return sizeof(CombineParams);
     case 4: return sizeof(fa_strides);
+    case 5: return sizeof(FwdParams);
+    case 6: return sizeof(BwdParams);
+    case 7: return sizeof(DecParams);
     default: return 0;
   }
 }

@@ -1,7 +1,7 @@
 // bwd.hip — exact attention backward for gfx950, fp16/bf16, atomic-free and deterministic.
 //
 // Replaces the reference backward (kernels/backward.hip: fa_bwd_preprocess :86-96, fill_pd
-// :109-202, fa_bwd_dkdv :205-295, fa_bwd_dq :298-387, launcher :508-521); same BwdParams
+// :109-202, fa_bwd_dkdv :205-295, fa_bwd_dq :298-387, launcher :508-521); same FableBwdParams
 // contract and math (P recomputed from the forward LSE; dS = P*(dP - D)*softcap'), two kernels
 // in stream order, no atomics, fixed reduction order => bitwise reproducible:
 //
@@ -15,7 +15,7 @@
 //     S = Q.K^T and dP = dO.V^T; P and dS stay in registers as B operands of
 //     dV^T += dO^T.P and dK^T += Q^T.dS (dO^T/Q^T by transposing LDS reads).
 // On that recomputing path S and dP are computed in both kernels (the price of no atomics, as in
-// the reference). With a dS workspace (BwdParams.ds_ws, fp16/bf16 at head_dim 64/128) the order
+// the reference). With a dS workspace (FableBwdParams.ds_ws, fp16/bf16 at head_dim 64/128) the order
 // is instead: a rowsum kernel for D, the dK/dV kernel, which also stores each dS tile once, and
 // a dQ kernel that forms dQ = dS.K from the stored tiles; every product is computed once, still
 // without atomics and in a fixed order.
@@ -65,7 +65,7 @@ struct BwdQCfg {
 template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-bwd_dq_kernel(BwdParams p, int nqt) {
+bwd_dq_kernel(FableBwdParams p, int nqt) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
   __shared__ __attribute__((aligned(16))) T lds[2 * C::STAGE];
@@ -262,7 +262,7 @@ struct BwdKVCfg {
 template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-bwd_dkdv_kernel(BwdParams p, int nkt) {
+bwd_dkdv_kernel(FableBwdParams p, int nkt) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
   __shared__ __attribute__((aligned(16))) T lds[2 * C::STAGE];
@@ -479,7 +479,7 @@ struct BwdKVPCfg {
 template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false, bool DSW = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
+bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
   __shared__ __attribute__((aligned(16))) T lds[4 * C::STAGE];
@@ -785,7 +785,7 @@ bwd_dkdv_pair_kernel(BwdParams p, int nkt) {
 // left each workgroup waiting on a single load pair: C3 33 us for 134 MB).
 constexpr int DSUM_RPT = 4;
 template <typename T, int HD>
-__global__ __launch_bounds__(256) void bwd_dsum_kernel(BwdParams p, int rblocks) {
+__global__ __launch_bounds__(256) void bwd_dsum_kernel(FableBwdParams p, int rblocks) {
   constexpr int LPR = HD / 8, RPB = 256 / LPR;
   using V8 = typename Dt<T>::V8;
   const int tid = threadIdx.x;
@@ -853,7 +853,7 @@ __device__ __forceinline__ int dsl_ofs(int r, int n) {
 template <typename T, class C, bool CAUSAL, bool FEAT>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-bwd_dq_ds_kernel(BwdParams p, int nqt) {
+bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
   __shared__ __attribute__((aligned(16))) T lds[2 * C::KT];
@@ -1028,35 +1028,35 @@ bwd_dq_ds_kernel(BwdParams p, int nqt) {
 #define DSQ_NS 3
 #endif
 // bytes of dS workspace for the fp16/bf16 path (2-byte elements)
-static long long ds_bytes(const BwdParams& p) {
+static long long ds_bytes(const FableBwdParams& p) {
   return p.SQ > 0 && p.SK > 0 ? (long long)p.B * p.Hq * ds_tiles_per_head(p.SQ, p.SK) * 2048 : 0;
 }
 
 // backward through the dS workspace: D rows, then dK/dV (writing dS), then dQ = dS.K
 template <typename T, class CKV, bool CAUSAL, bool FEAT, bool DROP>
-static int launch_bwd_ds(const BwdParams& p, hipStream_t st, int nkt) {
+static int launch_bwd_ds(const FableBwdParams& p, hipStream_t st, int nkt) {
   using CD = BwdDsQCfg<CKV::HD, 8, 2, DSQ_NS>;
   constexpr int RPB = 256 / (CKV::HD / 8) * DSUM_RPT;  // rows per dsum workgroup
   const long long gd = (long long)((p.SQ + RPB - 1) / RPB) * p.Hq * p.B;
   const int nqt = (p.SQ + CD::BQ - 1) / CD::BQ;
   const long long gq = (long long)nqt * p.Hq * p.B;
   const long long gkv = (long long)nkt * p.Hk * p.B;
-  if (gd > 0x7FFFFFFF || gq > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_backward_launch: grid too large");
+  if (gd > 0x7FFFFFFF || gq > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_bwd: grid too large");
   hipLaunchKernelGGL((bwd_dsum_kernel<T, CKV::HD>), dim3((unsigned)gd), dim3(256), 0, st, p, (p.SQ + RPB - 1) / RPB);
-  if (int rc = launch_status("fable_attn_backward_launch (dsum)")) return rc;
+  if (int rc = launch_status("fable_attn_bwd (dsum)")) return rc;
   hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
-  if (int rc = launch_status("fable_attn_backward_launch (dkdv)")) return rc;
+  if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;
   hipLaunchKernelGGL((bwd_dq_ds_kernel<T, CD, CAUSAL, FEAT>), dim3((unsigned)gq), dim3(CD::NT), 0, st, p, nqt);
-  return launch_status("fable_attn_backward_launch (dq)");
+  return launch_status("fable_attn_bwd (dq)");
 }
 
 template <typename T, class CQ, class CKV, bool CAUSAL, bool FEAT, bool DROP = false>
-static int launch_bwd2(const BwdParams& p, hipStream_t st) {
+static int launch_bwd2(const FableBwdParams& p, hipStream_t st) {
   const int nqt = (p.SQ + CQ::BQ - 1) / CQ::BQ;
   const int nkt = (p.SK + CKV::BK - 1) / CKV::BK;
   const long long gq = (long long)nqt * p.Hq * p.B * CQ::DSPLIT;
   const long long gkv = (long long)nkt * p.Hk * p.B * CKV::DSPLIT;
-  if (gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_backward_launch: grid too large");
+  if (gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_bwd: grid too large");
   if constexpr (CKV::PAIR) {
     const long long need = ds_bytes(p);
     // (the tiles are moved with 16-byte accesses: an unaligned workspace is not used)
@@ -1065,20 +1065,20 @@ static int launch_bwd2(const BwdParams& p, hipStream_t st) {
   }
   if (gq > 0) {
     hipLaunchKernelGGL((bwd_dq_kernel<T, CQ, CAUSAL, FEAT, DROP>), dim3((unsigned)gq), dim3(CQ::NT), 0, st, p, nqt);
-    if (int rc = launch_status("fable_attn_backward_launch (dq)")) return rc;
+    if (int rc = launch_status("fable_attn_bwd (dq)")) return rc;
   }
   if (gkv > 0) {
     if constexpr (CKV::PAIR)
       hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
     else
       hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
-    if (int rc = launch_status("fable_attn_backward_launch (dkdv)")) return rc;
+    if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;
   }
   return FA_OK;
 }
 
 template <typename T, class CQ, class CKV>
-static int launch_bwd(const BwdParams& p, hipStream_t st) {
+static int launch_bwd(const FableBwdParams& p, hipStream_t st) {
   const bool feat = p.softcap > 0.0f || p.alibi != nullptr || p.win_left >= 0 ||
                     (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
   // dropout has kernels of its own (the Philox rounds cost the other features no registers)
@@ -1090,33 +1090,36 @@ static int launch_bwd(const BwdParams& p, hipStream_t st) {
 }
 
 template <typename T>
-static int bwd_dispatch(const BwdParams& p, hipStream_t st) {
+static int bwd_dispatch(const FableBwdParams& p, hipStream_t st) {
   switch (p.D) {
     case 64: return launch_bwd<T, BwdQCfg<64, 64, 4, 2>, BwdKVPCfg<64, 2, 3>>(p, st);
     case 128: return launch_bwd<T, BwdQCfg<128, 32, 4, 2>, BwdKVPCfg<128, 4, 2>>(p, st);
     case 256: return launch_bwd<T, BwdQCfg<256, 32, 4, 1, 2>, BwdKVCfg<256, 4, 1, 4>>(p, st);
-    default: return fail(FA_ERR_HEADDIM, "fable_attn_backward_launch: head_dim=%d has no kernel (64, 128, 256)", p.D);
+    default: return fail(FA_ERR_HEADDIM, "fable_attn_bwd: head_dim=%d has no kernel (64, 128, 256)", p.D);
   }
 }
 
 }  // namespace fa
 
-extern "C" int64_t fable_attn_bwd_ds_bytes(BwdParams p, int dtype) {
+extern "C" int64_t fable_attn_bwd_ds_bytes(FableBwdParams p, int dtype) {
   if ((dtype != FA_F16 && dtype != FA_BF16) || (p.D != 64 && p.D != 128) || p.B <= 0 || p.Hq <= 0) return 0;
   return fa::ds_bytes(p);
 }
 
-extern "C" int fable_attn_backward_launch(BwdParams p, int dtype, void* stream) {
+extern "C" int fable_attn_bwd(FableBwdParams p, int dtype, void* stream) {
   using namespace fa;
   if (!p.Q || !p.K || !p.V || !p.O || !p.dO || !p.dQ || !p.dK || !p.dV || !p.lse || !p.dsum)
-    return fail(FA_ERR_ARG, "fable_attn_backward_launch: null pointer");
+    return fail(FA_ERR_ARG, "fable_attn_bwd: null pointer");
   if (p.Hq <= 0 || p.Hk <= 0 || p.Hq % p.Hk || p.gqa != p.Hq / p.Hk)
-    return fail(FA_ERR_ARG, "fable_attn_backward_launch: Hq=%d Hk=%d gqa=%d", p.Hq, p.Hk, p.gqa);
+    return fail(FA_ERR_ARG, "fable_attn_bwd: Hq=%d Hk=%d gqa=%d", p.Hq, p.Hk, p.gqa);
   if (p.dropout && !(p.dropout_p >= 0.0f && p.dropout_p < 1.0f))
-    return fail(FA_ERR_ARG, "fable_attn_backward_launch: dropout_p=%g", p.dropout_p);
+    return fail(FA_ERR_ARG, "fable_attn_bwd: dropout_p=%g", p.dropout_p);
   if ((p.cu_q == nullptr) != (p.cu_k == nullptr))
-    return fail(FA_ERR_ARG, "fable_attn_backward_launch: cu_q and cu_k go together");
+    return fail(FA_ERR_ARG, "fable_attn_bwd: cu_q and cu_k go together");
   if (p.B <= 0 || p.SQ < 0 || p.SK < 0) return FA_OK;  // empty ranges write zero gradients
+  // a window at least as long as the sequences bounds nothing (keeps mask bounds in 32 bits)
+  if (p.win_left >= p.SK) p.win_left = -1;
+  if (p.win_right >= p.SQ) p.win_right = -1;
   if (!p.cu_q && p.lse_sb == 0 && p.lse_sh == 0) {  // dense [B,Hq,SQ] LSE / dsum
     p.lse_sh = p.SQ;
     p.lse_sb = (int64_t)p.Hq * p.SQ;
@@ -1126,6 +1129,6 @@ extern "C" int fable_attn_backward_launch(BwdParams p, int dtype, void* stream) 
     case FA_F16: return bwd_dispatch<_Float16>(p, st);
     case FA_BF16: return bwd_dispatch<__bf16>(p, st);
     case FA_F32: return launch_bwd_f32(p, st);
-    default: return fail(FA_ERR_DTYPE, "fable_attn_backward_launch: dtype %d not implemented (fp16/bf16/fp32)", dtype);
+    default: return fail(FA_ERR_DTYPE, "fable_attn_bwd: dtype %d not implemented (fp16/bf16/fp32)", dtype);
   }
 }

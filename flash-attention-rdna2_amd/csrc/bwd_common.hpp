@@ -1,6 +1,6 @@
 // bwd_common.hpp — the backward's mask ranges, logit transform and sequence views, shared by
 // the fp16/bf16 kernels (bwd.hip) and the fp32 kernels (bwd_f32.hip). Mask contract and math of
-// the reference backward (kernels/backward.hip:109-202, BwdParams in include/fable_attn_abi.h).
+// the reference backward (kernels/backward.hip:109-202, FableBwdParams in include/fable_attn_abi.h).
 #pragma once
 #include "attn_device.hpp"
 
@@ -9,7 +9,7 @@ namespace fa {
 // Written with bitwise ands, not early returns: per score the compiler then emits compares and
 // one select instead of a divergent branch (with its exec-mask bookkeeping) per score.
 template <bool CAUSAL, bool FEAT>
-__device__ __forceinline__ bool visible_b(const BwdParams& p, int q, int key, int delta, int SQ, int SK) {
+__device__ __forceinline__ bool visible_b(const FableBwdParams& p, int q, int key, int delta, int SQ, int SK) {
   bool ok = (key < SK) & (q < SQ);
   if (CAUSAL) ok &= key <= q + delta;
   if (FEAT) {
@@ -21,7 +21,7 @@ __device__ __forceinline__ bool visible_b(const BwdParams& p, int q, int key, in
 
 // keys visible to query rows [r0, r1]: [k0, k1)
 template <bool CAUSAL, bool FEAT>
-__device__ __forceinline__ void key_range_b(const BwdParams& p, int r0, int r1, int delta, int SK, int& k0, int& k1) {
+__device__ __forceinline__ void key_range_b(const FableBwdParams& p, int r0, int r1, int delta, int SK, int& k0, int& k1) {
   k0 = 0;
   k1 = SK;
   if (CAUSAL) k1 = min(k1, r1 + delta + 1);
@@ -33,7 +33,7 @@ __device__ __forceinline__ void key_range_b(const BwdParams& p, int r0, int r1, 
 
 // queries that see some key in [k0, k1]: [q0, q1)
 template <bool CAUSAL, bool FEAT>
-__device__ __forceinline__ void query_range_b(const BwdParams& p, int k0, int k1, int delta, int SQ, int& q0, int& q1) {
+__device__ __forceinline__ void query_range_b(const FableBwdParams& p, int k0, int k1, int delta, int SQ, int& q0, int& q1) {
   q0 = 0;
   q1 = SQ;
   if (CAUSAL) q0 = max(q0, k0 - delta);
@@ -45,7 +45,7 @@ __device__ __forceinline__ void query_range_b(const BwdParams& p, int k0, int k1
 
 // logit transform of one score: returns log2-domain logit, and d(logit)/d(scale*q.k)
 template <bool FEAT>
-__device__ __forceinline__ float bwd_logit2(const BwdParams& p, float s, float c_log2, float slope, int q,
+__device__ __forceinline__ float bwd_logit2(const FableBwdParams& p, float s, float c_log2, float slope, int q,
                                             int key, float& deriv) {
   if (!FEAT) {
     deriv = 1.0f;
@@ -70,7 +70,7 @@ struct BwdSeq {
   int SQ, SK;
   long long qo, ko;
 };
-__device__ __forceinline__ BwdSeq bwd_seq(const BwdParams& p, int b) {
+__device__ __forceinline__ BwdSeq bwd_seq(const FableBwdParams& p, int b) {
   BwdSeq s;
   if (p.cu_q) {
     s.qo = p.cu_q[b];
@@ -99,7 +99,7 @@ __host__ __device__ inline long long ds_tiles_per_head(int SQ, int SK) {
   return (long long)((SK + 31) >> 5) * ((SQ + 31) >> 5);
 }
 template <typename T>
-__device__ __forceinline__ T* ds_tile(const BwdParams& p, int b, int h, int kb32, int qb32) {
+__device__ __forceinline__ T* ds_tile(const FableBwdParams& p, int b, int h, int kb32, int qb32) {
   const long long nqb = (p.SQ + 31) >> 5, nkb = (p.SK + 31) >> 5;
   return (T*)p.ds_ws + ((((long long)b * p.Hq + h) * nkb + kb32) * nqb + qb32) * 1024;
 }
@@ -107,7 +107,7 @@ __device__ __forceinline__ int ds_slot_query(int n) {
   return 16 * (n >> 4) + 8 * ((n >> 2) & 1) + 4 * ((n >> 3) & 1) + (n & 3);
 }
 
-// the fp32 backward (bwd_f32.hip), dispatched from fable_attn_backward_launch
-int launch_bwd_f32(const BwdParams& p, hipStream_t st);
+// the fp32 backward (bwd_f32.hip), dispatched from fable_attn_bwd
+int launch_bwd_f32(const FableBwdParams& p, hipStream_t st);
 
 }  // namespace fa

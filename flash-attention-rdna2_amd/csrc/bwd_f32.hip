@@ -1,7 +1,7 @@
 // bwd_f32.hip — exact attention backward for gfx950 in fp32, atomic-free and deterministic.
 //
 // The reference runs fp32 through its backward's plain-output mode (kernels/backward.hip:126,
-// 257, 344: MODE == BW_F32, fmaf products, D <= 224). Same BwdParams contract and math as the
+// 257, 344: MODE == BW_F32, fmaf products, D <= 224). Same FableBwdParams contract and math as the
 // fp16/bf16 kernels of bwd.hip (P recomputed from the forward LSE; dS = P*(z*dP - D)*softcap'),
 // the same two-kernel split in stream order, on v_mfma_f32_16x16x4_f32:
 //
@@ -32,7 +32,7 @@ __device__ __forceinline__ float quad_sum_b(float x) {
 
 // log2-domain logit of one score and d(logit)/d(scale*q.k)
 template <bool FEAT>
-__device__ __forceinline__ float logit2_f32(const BwdParams& p, float s, float c_log2, float slope, float inv_cap,
+__device__ __forceinline__ float logit2_f32(const FableBwdParams& p, float s, float c_log2, float slope, float inv_cap,
                                             int q, int key, float& deriv) {
   deriv = 1.0f;
   if (!FEAT) return s * c_log2;
@@ -65,7 +65,7 @@ struct F32BwdQCfg {
 template <class C, bool CAUSAL, bool FEAT, bool DROP>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-bwd_dq_f32_kernel(BwdParams p, int nqt) {
+bwd_dq_f32_kernel(FableBwdParams p, int nqt) {
   __shared__ __attribute__((aligned(16))) float kl[2 * C::TILE];
   __shared__ __attribute__((aligned(16))) float vl[2 * C::TILE];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -236,7 +236,7 @@ struct F32BwdKVCfg {
 template <class C, bool CAUSAL, bool FEAT, bool DROP>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-bwd_dkdv_f32_kernel(BwdParams p, int nkt) {
+bwd_dkdv_f32_kernel(FableBwdParams p, int nkt) {
   __shared__ __attribute__((aligned(16))) float lds[2 * C::STAGE];
   __shared__ __attribute__((aligned(16))) float rowv[2][2][C::BQ];  // [stage][lse2 | D][q]
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -406,25 +406,25 @@ bwd_dkdv_f32_kernel(BwdParams p, int nkt) {
 }
 
 template <class CQ, class CKV, bool CAUSAL, bool FEAT, bool DROP>
-static int launch_bwd_f32_2(const BwdParams& p, hipStream_t st) {
+static int launch_bwd_f32_2(const FableBwdParams& p, hipStream_t st) {
   const int nqt = (p.SQ + CQ::BQ - 1) / CQ::BQ;
   const int nkt = (p.SK + CKV::BK - 1) / CKV::BK;
   const long long gq = (long long)nqt * p.Hq * p.B;
   const long long gkv = (long long)nkt * p.Hk * p.B * CKV::DSPLIT;
-  if (gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_backward_launch: grid too large");
+  if (gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_bwd: grid too large");
   if (gq > 0) {
     hipLaunchKernelGGL((bwd_dq_f32_kernel<CQ, CAUSAL, FEAT, DROP>), dim3((unsigned)gq), dim3(CQ::NT), 0, st, p, nqt);
-    if (int rc = launch_status("fable_attn_backward_launch (dq, fp32)")) return rc;
+    if (int rc = launch_status("fable_attn_bwd (dq, fp32)")) return rc;
   }
   if (gkv > 0) {
     hipLaunchKernelGGL((bwd_dkdv_f32_kernel<CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
-    if (int rc = launch_status("fable_attn_backward_launch (dkdv, fp32)")) return rc;
+    if (int rc = launch_status("fable_attn_bwd (dkdv, fp32)")) return rc;
   }
   return FA_OK;
 }
 
 template <class CQ, class CKV>
-static int launch_bwd_f32_1(const BwdParams& p, hipStream_t st) {
+static int launch_bwd_f32_1(const FableBwdParams& p, hipStream_t st) {
   const bool feat = p.dropout || p.softcap > 0.0f || p.alibi != nullptr || p.win_left >= 0 ||
                     (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
   if (p.dropout)
@@ -434,12 +434,12 @@ static int launch_bwd_f32_1(const BwdParams& p, hipStream_t st) {
   return feat ? launch_bwd_f32_2<CQ, CKV, false, true, false>(p, st) : launch_bwd_f32_2<CQ, CKV, false, false, false>(p, st);
 }
 
-int launch_bwd_f32(const BwdParams& p, hipStream_t st) {
+int launch_bwd_f32(const FableBwdParams& p, hipStream_t st) {
   switch (p.D) {
     case 64: return launch_bwd_f32_1<F32BwdQCfg<64, 64, 8, 2>, F32BwdKVCfg<64, 64, 8, 2>>(p, st);
     case 128: return launch_bwd_f32_1<F32BwdQCfg<128, 64, 8, 2>, F32BwdKVCfg<128, 32, 8, 2>>(p, st);
     case 256: return launch_bwd_f32_1<F32BwdQCfg<256, 32, 4, 1>, F32BwdKVCfg<256, 32, 4, 1, 2>>(p, st);
-    default: return fail(FA_ERR_HEADDIM, "fable_attn_backward_launch: head_dim=%d has no fp32 kernel (64, 128, 256)", p.D);
+    default: return fail(FA_ERR_HEADDIM, "fable_attn_bwd: head_dim=%d has no fp32 kernel (64, 128, 256)", p.D);
   }
 }
 

@@ -2,7 +2,7 @@
 // LSE-weighted combine.
 //
 // Replaces the reference decode (kernels/fa_decode.hip: fd_partial :57-252, fd_combine
-// :255-272, fd_append :275-302, launcher :319-362) with the same DecParams contract
+// :255-272, fd_append :275-302, launcher :319-362) with the same FableDecParams contract
 // (include/fable_attn_abi.h) and a different design:
 //  * one workgroup (4 waves) per (kv head, 16-head group, sequence*new token, split); the q
 //    heads sharing the kv head are packed into the N=16 dimension of v_mfma_f32_16x16x32, so
@@ -36,7 +36,7 @@ struct DecRange {
   int qpos, hi, lo, start, end;
 };
 
-__device__ __forceinline__ DecRange dec_range(const DecParams& p, int b, int tk, int sp, int append) {
+__device__ __forceinline__ DecRange dec_range(const FableDecParams& p, int b, int tk, int sp, int append) {
   DecRange r;
   const int ctx = p.ctx_len[b];
   r.qpos = ctx + tk;
@@ -52,7 +52,7 @@ __device__ __forceinline__ DecRange dec_range(const DecParams& p, int b, int tk,
 }
 
 template <typename T, int HD, bool FEAT>
-__global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_shift, int ngrp, int append) {
+__global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int page_shift, int ngrp, int append) {
   using V8 = typename Dt<T>::V8;
   constexpr int NDS = HD / 32;  // S^T contraction steps
   constexpr int NDB = HD / 16;  // 16-row blocks of O^T
@@ -318,7 +318,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(DecParams p, int page_
 // whose A operand is one float per lane (V[key 16kb + 4lg + j][16db + lh]), read from the cache
 // as well (four 64-byte row segments per load). Rotation of q stays exact in fp32.
 template <int HD, bool FEAT>
-__global__ __launch_bounds__(256) void dec_partial_f32_kernel(DecParams p, int page_shift, int ngrp, int append) {
+__global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, int page_shift, int ngrp, int append) {
   constexpr int NQ = HD / 4;    // S^T contraction steps (q floats per lane)
   constexpr int NDB = HD / 16;  // 16-row blocks of O^T
   constexpr int QSTR = HD + 4;
@@ -477,7 +477,7 @@ __global__ __launch_bounds__(256) void dec_partial_f32_kernel(DecParams p, int p
 
 // merge nsplit partials of one (token, head): grid (batch*nq, NH), block HD
 template <typename T, int HD>
-__global__ __launch_bounds__(256) void dec_combine_kernel(DecParams p) {
+__global__ __launch_bounds__(256) void dec_combine_kernel(FableDecParams p) {
   const int row = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
   const float* base = p.scratch + ((long long)row * p.NH + h) * p.nsplit * (HD + 2);
   float gm = -INFINITY;
@@ -498,7 +498,7 @@ __global__ __launch_bounds__(256) void dec_combine_kernel(DecParams p) {
 
 // write new_k (rotary applied) / new_v at positions ctx_len[b]+tk: grid (batch*nq, NKV), block HD
 template <typename T, int HD>
-__global__ __launch_bounds__(256) void dec_append_kernel(DecParams p, const T* nk, const T* nv, int page_shift) {
+__global__ __launch_bounds__(256) void dec_append_kernel(FableDecParams p, const T* nk, const T* nv, int page_shift) {
   __shared__ float ks[HD];
   const int b = blockIdx.x / p.nq, tk = blockIdx.x % p.nq, kvh = blockIdx.y, d = threadIdx.x;
   const int NKV = p.NH / p.gqa;
@@ -534,14 +534,14 @@ __global__ __launch_bounds__(256) void dec_append_kernel(DecParams p, const T* n
 }
 
 template <typename T, int HD>
-static int launch_dec(const DecParams& p, hipStream_t st, const void* nk, const void* nv) {
+static int launch_dec(const FableDecParams& p, hipStream_t st, const void* nk, const void* nv) {
   const int page_shift = __builtin_ctz((unsigned)p.page);
   const int NKV = p.NH / p.gqa;
   const int ngrp = (p.gqa + 15) / 16;
   if (nk) {
     hipLaunchKernelGGL((dec_append_kernel<T, HD>), dim3(p.batch * p.nq, NKV), dim3(HD), 0, st, p,
                        (const T*)nk, (const T*)nv, page_shift);
-    if (int rc = launch_status("fa_decode_launch (append)")) return rc;
+    if (int rc = launch_status("fable_attn_dec (append)")) return rc;
   }
   const bool feat = p.softcap > 0.0f || p.alibi != nullptr;
   dim3 grid(NKV * ngrp, p.batch * p.nq, p.nsplit);
@@ -556,18 +556,18 @@ static int launch_dec(const DecParams& p, hipStream_t st, const void* nk, const 
     else
       hipLaunchKernelGGL((dec_partial_kernel<T, HD, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
   }
-  if (int rc = launch_status("fa_decode_launch (partial)")) return rc;
+  if (int rc = launch_status("fable_attn_dec (partial)")) return rc;
   hipLaunchKernelGGL((dec_combine_kernel<T, HD>), dim3(p.batch * p.nq, p.NH), dim3(HD), 0, st, p);
-  return launch_status("fa_decode_launch (combine)");
+  return launch_status("fable_attn_dec (combine)");
 }
 
 template <typename T>
-static int dec_dispatch(const DecParams& p, hipStream_t st, const void* nk, const void* nv) {
+static int dec_dispatch(const FableDecParams& p, hipStream_t st, const void* nk, const void* nv) {
   switch (p.HD) {
     case 64: return launch_dec<T, 64>(p, st, nk, nv);
     case 128: return launch_dec<T, 128>(p, st, nk, nv);
     case 256: return launch_dec<T, 256>(p, st, nk, nv);
-    default: return fail(FA_ERR_HEADDIM, "fa_decode_launch: head_dim=%d has no kernel (64, 128, 256)", p.HD);
+    default: return fail(FA_ERR_HEADDIM, "fable_attn_dec: head_dim=%d has no kernel (64, 128, 256)", p.HD);
   }
 }
 
@@ -604,23 +604,23 @@ extern "C" int fa_decode_num_splits(int batch, int nq, int NH, int gqa, int64_t 
   return best;
 }
 
-extern "C" int fa_decode_launch(DecParams p, int dtype, void* stream, const void* new_k, const void* new_v) {
+extern "C" int fable_attn_dec(FableDecParams p, int dtype, void* stream, const void* new_k, const void* new_v) {
   using namespace fa;
   if (!p.q || !p.Kc || !p.Vc || !p.block_table || !p.o || !p.scratch || !p.ctx_len)
-    return fail(FA_ERR_ARG, "fa_decode_launch: null pointer");
-  if (p.page <= 0 || (p.page & (p.page - 1))) return fail(FA_ERR_ARG, "fa_decode_launch: page=%d is not a power of two", p.page);
-  if (p.NH <= 0 || p.gqa <= 0 || p.NH % p.gqa) return fail(FA_ERR_ARG, "fa_decode_launch: NH=%d gqa=%d", p.NH, p.gqa);
-  if (p.nsplit < 1 || p.nsplit > 512) return fail(FA_ERR_ARG, "fa_decode_launch: nsplit=%d", p.nsplit);
+    return fail(FA_ERR_ARG, "fable_attn_dec: null pointer");
+  if (p.page <= 0 || (p.page & (p.page - 1))) return fail(FA_ERR_ARG, "fable_attn_dec: page=%d is not a power of two", p.page);
+  if (p.NH <= 0 || p.gqa <= 0 || p.NH % p.gqa) return fail(FA_ERR_ARG, "fable_attn_dec: NH=%d gqa=%d", p.NH, p.gqa);
+  if (p.nsplit < 1 || p.nsplit > 512) return fail(FA_ERR_ARG, "fable_attn_dec: nsplit=%d", p.nsplit);
   if (p.nq < 1) p.nq = 1;
-  if ((new_k == nullptr) != (new_v == nullptr)) return fail(FA_ERR_ARG, "fa_decode_launch: new_k and new_v go together");
-  if (p.rotary && (!p.cos || !p.sin)) return fail(FA_ERR_ARG, "fa_decode_launch: rotary needs cos and sin");
-  if (p.rotary && (p.rotary_dim < 0 || p.rotary_dim > p.HD || p.rotary_dim % 2)) return fail(FA_ERR_ARG, "fa_decode_launch: rotary_dim=%d", p.rotary_dim);
+  if ((new_k == nullptr) != (new_v == nullptr)) return fail(FA_ERR_ARG, "fable_attn_dec: new_k and new_v go together");
+  if (p.rotary && (!p.cos || !p.sin)) return fail(FA_ERR_ARG, "fable_attn_dec: rotary needs cos and sin");
+  if (p.rotary && (p.rotary_dim < 0 || p.rotary_dim > p.HD || p.rotary_dim % 2)) return fail(FA_ERR_ARG, "fable_attn_dec: rotary_dim=%d", p.rotary_dim);
   if (p.batch <= 0) return FA_OK;
   hipStream_t st = (hipStream_t)stream;
   switch (dtype) {
     case FA_F16: return dec_dispatch<_Float16>(p, st, new_k, new_v);
     case FA_BF16: return dec_dispatch<__bf16>(p, st, new_k, new_v);
     case FA_F32: return dec_dispatch<float>(p, st, new_k, new_v);
-    default: return fail(FA_ERR_DTYPE, "fa_decode_launch: dtype %d not implemented (fp16/bf16/fp32)", dtype);
+    default: return fail(FA_ERR_DTYPE, "fable_attn_dec: dtype %d not implemented (fp16/bf16/fp32)", dtype);
   }
 }

@@ -1,6 +1,6 @@
 // fwd_common.hpp — the forward's sequence views and mask ranges, shared by the fp16/bf16
 // kernels (fwd_kernel.hpp) and the fp32 kernels (fwd_f32.hip). Mask contract of the reference
-// (kernels/fa_forward.hip:224-233, FwdParams in include/fable_attn_abi.h).
+// (kernels/fa_forward.hip:224-233, FableFwdParams in include/fable_attn_abi.h).
 #pragma once
 #include "attn_device.hpp"
 
@@ -17,7 +17,7 @@ struct SeqView {
 
 // lengths and row-0 offsets of sequence z, head h (dense: batch element z; varlen: packed rows
 // cu_q[z].. / cu_k[z].., cut by seqused)
-__device__ __forceinline__ SeqView seq_view(const FwdParams& p, int z, int h) {
+__device__ __forceinline__ SeqView seq_view(const FableFwdParams& p, int z, int h) {
   SeqView sv;
   if (p.cu_q) {
     const int qs = p.cu_q[z], ks = p.cu_k[z];
@@ -44,7 +44,7 @@ __device__ __forceinline__ SeqView seq_view(const FwdParams& p, int z, int h) {
 
 // visible key range [k0, k1) for query rows [r0, r1] (reference mask contract)
 template <bool CAUSAL, bool FEAT>
-__device__ __forceinline__ void key_range(const FwdParams& p, int r0, int r1, int delta, int SK,
+__device__ __forceinline__ void key_range(const FableFwdParams& p, int r0, int r1, int delta, int SK,
                                           int& k0, int& k1) {
   k0 = 0;
   k1 = SK;
@@ -62,7 +62,7 @@ __device__ __forceinline__ void key_range(const FwdParams& p, int r0, int r1, in
 
 // key j visible to query i (delta = SK - SQ, bottom-right alignment)
 template <bool CAUSAL, bool FEAT>
-__device__ __forceinline__ bool fwd_visible(const FwdParams& p, int i, int j, int delta, int SK) {
+__device__ __forceinline__ bool fwd_visible(const FableFwdParams& p, int i, int j, int delta, int SK) {
   bool ok = j < SK;
   if (CAUSAL) ok = ok && j <= i + delta;
   if (FEAT) {
@@ -77,10 +77,10 @@ __device__ __forceinline__ bool fwd_visible(const FwdParams& p, int i, int j, in
 }
 
 // the fp16/bf16 forward per head dim (fwd_d64/128/256.hip) and the fp32 forward (fwd_f32.hip),
-// dispatched from fa_forward_launch
-int launch_fwd_d64(const FwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_d128(const FwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_d256(const FwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_f32(const FwdParams& p, hipStream_t st);
+// dispatched from fable_attn_fwd
+int launch_fwd_d64(const FableFwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_d128(const FableFwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_d256(const FableFwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_f32(const FableFwdParams& p, hipStream_t st);
 
 }  // namespace fa

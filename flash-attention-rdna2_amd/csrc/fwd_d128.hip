@@ -4,7 +4,7 @@
 
 namespace fa {
 
-int launch_fwd_d128(const FwdParams& p, int dtype, hipStream_t st) {
+int launch_fwd_d128(const FableFwdParams& p, int dtype, hipStream_t st) {
   using C = FwdCfg<128, 64, 8, 2>;
   using CF = FwdCfg<128, 32, 4, 2>;
   using CN = FwdCfg<128, 32, 2, 2>;

@@ -4,7 +4,7 @@
 
 namespace fa {
 
-int launch_fwd_d256(const FwdParams& p, int dtype, hipStream_t st) {
+int launch_fwd_d256(const FableFwdParams& p, int dtype, hipStream_t st) {
   if (dtype == FA_F16) return launch_fwd<_Float16, FwdCfg<256, 32, 4, 1>, FwdCfg<256, 32, 4, 1>, FwdCfg<256, 32, 2, 1>>(p, st);
   return launch_fwd<__bf16, FwdCfg<256, 32, 4, 1>, FwdCfg<256, 32, 4, 1>, FwdCfg<256, 32, 2, 1>>(p, st);
 }

@@ -1,7 +1,7 @@
 // fwd_f32.hip — exact attention forward for gfx950 in fp32 (inputs, outputs and arithmetic).
 //
 // The reference runs fp32 through a separate small-tile kernel (kernels/fa_forward.hip:317-400,
-// dispatched at :440-447); same FwdParams contract and masking as the fp16/bf16 path. Here the
+// dispatched at :440-447); same FableFwdParams contract and masking as the fp16/bf16 path. Here the
 // products run on v_mfma_f32_16x16x4_f32 (fp32 operands, fp32 accumulate; the matrix cores'
 // fp32 rate equals the VALU's, so fp32 stays on the MFMA pipe and leaves the VALU to softmax):
 //
@@ -55,7 +55,7 @@ struct F32Cfg {
 template <class C, bool CAUSAL, bool FEAT, bool DROP>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-fwd_f32_kernel(FwdParams p, int nqt) {
+fwd_f32_kernel(FableFwdParams p, int nqt) {
   __shared__ __attribute__((aligned(16))) float kl[2 * C::TILE];
   __shared__ __attribute__((aligned(16))) float vl[2 * C::TILE];
 
@@ -222,14 +222,14 @@ fwd_f32_kernel(FwdParams p, int nqt) {
 }
 
 template <class C>
-static int launch_f32(const FwdParams& p, hipStream_t st) {
+static int launch_f32(const FableFwdParams& p, hipStream_t st) {
   const bool drop = p.dropout_p > 0.0f;
   const bool feat = drop || p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
                     p.win_left >= 0 || (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
   const int nqt = (p.SQ + C::BR - 1) / C::BR;
   const long long nblk = (long long)nqt * p.NH * p.batch;
   if (nblk <= 0) return FA_OK;
-  if (nblk > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fa_forward_launch: grid too large");
+  if (nblk > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_fwd: grid too large");
   const dim3 grid((unsigned)nblk), block(C::NT);
   if (p.causal) {
     if (drop) hipLaunchKernelGGL((fwd_f32_kernel<C, true, true, true>), grid, block, 0, st, p, nqt);
@@ -240,15 +240,15 @@ static int launch_f32(const FwdParams& p, hipStream_t st) {
     else if (feat) hipLaunchKernelGGL((fwd_f32_kernel<C, false, true, false>), grid, block, 0, st, p, nqt);
     else hipLaunchKernelGGL((fwd_f32_kernel<C, false, false, false>), grid, block, 0, st, p, nqt);
   }
-  return launch_status("fa_forward_launch");
+  return launch_status("fable_attn_fwd");
 }
 
-int launch_fwd_f32(const FwdParams& p, hipStream_t st) {
+int launch_fwd_f32(const FableFwdParams& p, hipStream_t st) {
   switch (p.HD) {
     case 64: return launch_f32<F32Cfg<64, 64, 8, 2>>(p, st);
     case 128: return launch_f32<F32Cfg<128, 64, 8, 2>>(p, st);
     case 256: return launch_f32<F32Cfg<256, 32, 8, 2>>(p, st);
-    default: return fail(FA_ERR_HEADDIM, "fa_forward_launch: head_dim=%d has no fp32 kernel (64, 128, 256)", p.HD);
+    default: return fail(FA_ERR_HEADDIM, "fable_attn_fwd: head_dim=%d has no fp32 kernel (64, 128, 256)", p.HD);
   }
 }
 

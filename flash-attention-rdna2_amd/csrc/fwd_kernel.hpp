@@ -3,7 +3,7 @@
 // translation unit each, so they compile in parallel).
 //
 // Replaces the reference forward (kernels/fa_forward.hip:52-313 kernel, :424-451 launcher);
-// same math and masking contract (FwdParams in include/fable_attn_abi.h), new design:
+// same math and masking contract (FableFwdParams in include/fable_attn_abi.h), new design:
 //
 //  * workgroup = NW waves; wave w owns 32 query rows, so a workgroup covers BR = 32*NW rows of
 //    one (batch, head). Q for those rows lives in registers for the whole kernel, laid out as
@@ -65,7 +65,7 @@ struct FwdCfg {
 template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-fwd_kernel(FwdParams p, int nqt) {
+fwd_kernel(FableFwdParams p, int nqt) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
   // K/V rings of NST stages, a barrier every BP tiles. Iteration t reads K tile t+1 and V tile t
@@ -531,7 +531,7 @@ struct CfgTag {
 };
 
 template <typename T, class C, class CF, class CN, class CS = C>
-static int launch_fwd(const FwdParams& p, hipStream_t st) {
+static int launch_fwd(const FableFwdParams& p, hipStream_t st) {
   const bool drop = p.dropout_p > 0.0f;
   const bool feat = drop || p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
                     p.win_left >= 0 || (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
@@ -544,10 +544,10 @@ static int launch_fwd(const FwdParams& p, hipStream_t st) {
     const int nqt = (p.SQ + K::BR - 1) / K::BR;
     const long long nblk = (long long)nqt * p.NH * p.batch;
     if (nblk <= 0) return FA_OK;
-    if (nblk > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fa_forward_launch: grid too large");
+    if (nblk > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_fwd: grid too large");
     hipLaunchKernelGGL((fwd_kernel<T, K, decltype(causal)::value, decltype(ft)::value, decltype(dr)::value>),
                        dim3((unsigned)nblk), dim3(K::NT), 0, st, p, nqt);
-    return launch_status("fa_forward_launch");
+    return launch_status("fable_attn_fwd");
   };
   auto pick = [&](auto causal) -> int {
     using Y = std::integral_constant<bool, true>;

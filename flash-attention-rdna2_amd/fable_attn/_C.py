@@ -22,7 +22,7 @@ workspaces and supplies the current stream; all compute is in libfable_attn_hip.
 no fallback: if the library is missing, importing this module raises ImportError.
 
 Backward dS workspace: for fp16/bf16 at head_dim 64/128 the backward can store dS once and
-form dQ = dS.K from it (BwdParams.ds_ws) instead of recomputing S and dP in its dQ kernel. The
+form dQ = dS.K from it (FableBwdParams.ds_ws) instead of recomputing S and dP in its dQ kernel. The
 workspace is B*Hq*SQ*SK*2 bytes (rounded up to 32x32 tiles); bwd/bwd_varlen allocate it when it
 is at most `ds_max_bytes` (default BWD_DS_MAX_BYTES, 4 GiB, or the environment variable
 FABLE_ATTN_BWD_DS_MAX_BYTES). Both paths give the same gradients to rounding.
@@ -33,7 +33,7 @@ import os
 import torch
 
 from . import _lib
-from ._lib import BwdParams, CombineParams, DecParams, FwdParams, Strides
+from ._lib import FableBwdParams, CombineParams, FableDecParams, FableFwdParams, Strides
 
 _L = _lib.load()
 
@@ -41,13 +41,18 @@ BWD_DS_MAX_BYTES = int(os.environ.get("FABLE_ATTN_BWD_DS_MAX_BYTES", 4 << 30))
 
 
 def _ds_workspace(p, dtype, device, ds_max_bytes):
-    """Attach a dS workspace to BwdParams p when the library has a path for it and it fits the
+    """Attach a dS workspace to FableBwdParams p when the library has a path for it and it fits the
     cap; returns the tensor (kept alive by the caller until the launch is enqueued)."""
     cap = BWD_DS_MAX_BYTES if ds_max_bytes is None else int(ds_max_bytes)
     need = int(_L.fable_attn_bwd_ds_bytes(p, dtype))
     if need <= 0 or need > cap:
         return None
-    ws = torch.empty(need, dtype=torch.uint8, device=device)
+    try:
+        ws = torch.empty(need, dtype=torch.uint8, device=device)
+    except torch.cuda.OutOfMemoryError:
+        return None  # the recomputing path needs no workspace
+    if ws.data_ptr() % 16:  # (the caching allocator aligns; an unaligned buffer is not used)
+        return None
     p.ds_ws, p.ds_ws_bytes = ws.data_ptr(), need
     return ws
 
@@ -87,6 +92,50 @@ def _rows_aligned(t):
             all((s * el) % 16 == 0 for s in t.stride()[:-1]))
 
 
+def _check_index(name, t, dev, n=None, at_least=False):
+    """int32 index tensor on `dev`, contiguous (the kernels read it through a raw pointer),
+    with exactly (or at least) n entries."""
+    _req(torch.is_tensor(t), f"{name}: tensor expected")
+    _req(t.dtype == torch.int32, f"{name}: int32 expected, got {t.dtype}")
+    _req(t.device == dev, f"{name}: must be on {dev}, got {t.device}")
+    _req(t.is_contiguous(), f"{name}: must be contiguous")
+    if n is not None:
+        _req(t.numel() >= n if at_least else t.numel() == n,
+             f"{name}: {'at least ' if at_least else ''}{n} entries expected, got {t.numel()}")
+
+
+def _check_f32(name, t, dev, n=None):
+    """float32 side input (alibi slopes, rotary tables) on `dev`, contiguous."""
+    _req(torch.is_tensor(t), f"{name}: tensor expected")
+    _req(t.dtype == torch.float32, f"{name}: float32 expected, got {t.dtype}")
+    _req(t.device == dev, f"{name}: must be on {dev}, got {t.device}")
+    _req(t.is_contiguous(), f"{name}: must be contiguous")
+    if n is not None:
+        _req(t.numel() == n, f"{name}: {n} entries expected, got {t.numel()}")
+
+
+def _check_varlen_index(q, cu_q, cu_k, seqused_q, seqused_k):
+    batch = cu_q.numel() - 1
+    _req(batch >= 0, "cu_seqlens_q must have batch+1 entries")
+    _check_index("cu_seqlens_q", cu_q, q.device)
+    _check_index("cu_seqlens_k", cu_k, q.device, cu_q.numel())
+    if seqused_q is not None:
+        _check_index("seqused_q", seqused_q, q.device, batch)
+    if seqused_k is not None:
+        _check_index("seqused_k", seqused_k, q.device, batch)
+    return batch
+
+
+def _alibi(alibi, H, dev):
+    """alibi slopes as float32 [H] on dev (converted, as the public API passes them)."""
+    if alibi is None:
+        return None
+    _req(torch.is_tensor(alibi) and alibi.device == dev, f"alibi_slopes must be on {dev}")
+    al = alibi.to(torch.float32).contiguous()
+    _req(al.numel() == H, f"alibi_slopes: {H} entries (one per q head) expected, got {al.numel()}")
+    return al
+
+
 def _check_bhsd(name, t, dtype, dev):
     _req(t.is_cuda, f"{name}: GPU tensor required")
     _req(t.dim() == 4, f"{name}: expected [B,H,S,D]")
@@ -112,8 +161,8 @@ def fwd(q, k, v, scale, causal, win_left, win_right, softcap, alibi, dropout_p, 
         _req(out.dtype == q.dtype, "out must have the dtype of q")
         _req(_rows_aligned(out), "out: head_dim must be contiguous with 16-byte aligned rows")
     lse = torch.empty((B, Hq, SQ), dtype=torch.float32, device=q.device)
-    al = alibi.float().contiguous() if alibi is not None else None
-    p = FwdParams()
+    al = _alibi(alibi, Hq, q.device)
+    p = FableFwdParams()
     p.Q, p.K, p.V, p.O, p.LSE = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
     p.sQ, p.sK, p.sV, p.sO = _bhs(q), _bhs(k), _bhs(v), _bhs(out)
     p.SQ, p.SK, p.HD, p.NH, p.gqa = SQ, SK, D, Hq, Hq // Hk
@@ -128,7 +177,7 @@ def fwd(q, k, v, scale, causal, win_left, win_right, softcap, alibi, dropout_p, 
     p.seqused_q = p.seqused_k = None
     p.lse_sb, p.lse_sh = Hq * SQ, SQ
     with torch.cuda.device(q.device):
-        _lib.check(_L.fa_forward_launch(p, _dt(q), _stream(q)), "fa_forward_launch")
+        _lib.check(_L.fable_attn_fwd(p, _dt(q), _stream(q)), "fable_attn_fwd")
     return out, lse
 
 
@@ -145,12 +194,13 @@ def fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win
     for n, t in (("q", q), ("k", k), ("v", v)):
         _req(t.dtype == q.dtype, f"{n}: dtype mismatch")
         _req(_rows_aligned(t), f"{n}: head_dim must be contiguous with 16-byte aligned rows")
-    _req(cu_q.dtype == torch.int32 and cu_k.dtype == torch.int32, "cu_seqlens must be int32")
-    batch = cu_q.numel() - 1
+    _req(k.device == q.device and v.device == q.device, "q, k, v must be on one device")
+    _req(k.shape[2] == D and v.shape[:2] == k.shape[:2], "k/v shape mismatch")
+    batch = _check_varlen_index(q, cu_q, cu_k, seqused_q, seqused_k)
     out = torch.zeros_like(q) if seqused_q is not None else torch.empty_like(q)
     lse = torch.empty((Hq, q.shape[0]), dtype=torch.float32, device=q.device) if return_lse else None
-    al = alibi.float().contiguous() if alibi is not None else None
-    p = FwdParams()
+    al = _alibi(alibi, Hq, q.device)
+    p = FableFwdParams()
     p.Q, p.K, p.V, p.O = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr()
     p.LSE = lse.data_ptr() if lse is not None else None
     p.sQ = Strides(0, q.stride(1), q.stride(0))
@@ -170,7 +220,7 @@ def fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win
     p.seqused_k = seqused_k.data_ptr() if seqused_k is not None else None
     p.lse_sb, p.lse_sh = 0, q.shape[0]
     with torch.cuda.device(q.device):
-        _lib.check(_L.fa_forward_launch(p, _dt(q), _stream(q)), "fa_forward_launch (varlen)")
+        _lib.check(_L.fable_attn_fwd(p, _dt(q), _stream(q)), "fable_attn_fwd (varlen)")
     return (out, lse) if return_lse else out
 
 
@@ -183,14 +233,14 @@ def bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, al
     Hk, SK = k.shape[1], k.shape[2]
     for n, t in (("dout", dout), ("q", q), ("k", k), ("v", v), ("out", out)):
         _check_bhsd(n, t, q.dtype, q.device)
-    _req(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (B, Hq, SQ),
-         "lse must be contiguous fp32 [B,Hq,SQ]")
+    _req(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (B, Hq, SQ)
+         and lse.device == q.device, "lse must be contiguous fp32 [B,Hq,SQ] on q's device")
     dq = torch.empty((B, SQ, Hq, D), dtype=q.dtype, device=q.device).transpose(1, 2)
     dk = torch.empty((B, SK, Hk, D), dtype=k.dtype, device=q.device).transpose(1, 2)
     dv = torch.empty((B, SK, Hk, D), dtype=v.dtype, device=q.device).transpose(1, 2)
     dsum = torch.empty((B, Hq, SQ), dtype=torch.float32, device=q.device)
-    al = alibi.float().contiguous() if alibi is not None else None
-    p = BwdParams()
+    al = _alibi(alibi, Hq, q.device)
+    p = FableBwdParams()
     p.Q, p.K, p.V, p.O, p.dO = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr()
     p.dQ, p.dK, p.dV = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
     p.lse, p.dsum = lse.data_ptr(), dsum.data_ptr()
@@ -206,7 +256,7 @@ def bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, al
     p.lse_sb, p.lse_sh = Hq * SQ, SQ
     ws = _ds_workspace(p, _dt(q), q.device, ds_max_bytes)  # noqa: F841  (alive through the launch)
     with torch.cuda.device(q.device):
-        _lib.check(_L.fable_attn_backward_launch(p, _dt(q), _stream(q)), "fable_attn_backward_launch")
+        _lib.check(_L.fable_attn_bwd(p, _dt(q), _stream(q)), "fable_attn_bwd")
     return dq, dk, dv
 
 
@@ -226,15 +276,14 @@ def bwd_varlen(dout, q, k, v, out, lse, cu_q, cu_k, max_sq, max_sk, scale, causa
     Hq, D, Hk = q.shape[1], q.shape[2], k.shape[1]
     _req(Hq % Hk == 0, "Hq must be a multiple of Hk (GQA)")
     _req(dout.shape == q.shape and out.shape == q.shape and v.shape == k.shape, "shape mismatch")
-    _req(cu_q.dtype == torch.int32 and cu_k.dtype == torch.int32, "cu_seqlens must be int32")
-    _req(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (Hq, q.shape[0]),
-         "lse must be contiguous fp32 [Hq, total_q]")
-    batch = cu_q.numel() - 1
+    _req(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (Hq, q.shape[0])
+         and lse.device == q.device, "lse must be contiguous fp32 [Hq, total_q] on q's device")
+    batch = _check_varlen_index(q, cu_q, cu_k, seqused_q, seqused_k)
     dq, dk, dv = torch.zeros_like(q), torch.zeros_like(k), torch.zeros_like(v)
     dsum = torch.empty((Hq, q.shape[0]), dtype=torch.float32, device=q.device)
-    al = alibi.float().contiguous() if alibi is not None else None
+    al = _alibi(alibi, Hq, q.device)
     row = lambda t: Strides(0, t.stride(1), t.stride(0))
-    p = BwdParams()
+    p = FableBwdParams()
     p.Q, p.K, p.V, p.O, p.dO = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dout.data_ptr()
     p.dQ, p.dK, p.dV = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
     p.lse, p.dsum = lse.data_ptr(), dsum.data_ptr()
@@ -253,7 +302,7 @@ def bwd_varlen(dout, q, k, v, out, lse, cu_q, cu_k, max_sq, max_sk, scale, causa
     p.lse_sb, p.lse_sh = 0, q.shape[0]
     ws = _ds_workspace(p, _dt(q), q.device, ds_max_bytes)  # noqa: F841  (alive through the launch)
     with torch.cuda.device(q.device):
-        _lib.check(_L.fable_attn_backward_launch(p, _dt(q), _stream(q)), "fable_attn_backward_launch (varlen)")
+        _lib.check(_L.fable_attn_bwd(p, _dt(q), _stream(q)), "fable_attn_bwd (varlen)")
     return dq, dk, dv
 
 
@@ -274,17 +323,44 @@ def dec(q, k_cache, v_cache, block_table, cache_seqlens, new_k, new_v, rotary_co
     page, Hk = k_cache.shape[1], k_cache.shape[2]
     _req(Hq % Hk == 0, "Hq must be a multiple of nheads_k (GQA)")
     _req(page > 0 and (page & (page - 1)) == 0, "page must be a power of two")
+    dev = q.device
     for n, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
-        _req(t.is_contiguous() and t.dtype == q.dtype, f"{n}: contiguous, dtype of q")
-    _req(block_table.dtype == torch.int32 and block_table.is_contiguous(), "block_table int32")
-    _req(cache_seqlens.dtype == torch.int32, "cache_seqlens int32")
+        _req(t.is_contiguous() and t.dtype == q.dtype and t.device == dev,
+             f"{n}: contiguous, dtype and device of q")
+    _req(v_cache.shape == k_cache.shape and k_cache.shape[3] == D,
+         "k_cache/v_cache must both be [num_blocks, page, nheads_k, D] with q's D")
+    _req(block_table.dim() == 2 and block_table.shape[0] == B, "block_table must be [B, max_blocks]")
+    _check_index("block_table", block_table, dev)
+    _check_index("cache_seqlens", cache_seqlens, dev, B)
+    if cache_leftpad is not None:
+        _check_index("cache_leftpad", cache_leftpad, dev, B)
+    if rotary_pos is not None:
+        _check_index("rotary_seqlens", rotary_pos, dev, B)
+    if alibi is not None:
+        _check_f32("alibi_slopes", alibi, dev, Hq)
+    _req((rotary_cos is None) == (rotary_sin is None), "rotary_cos and rotary_sin go together")
+    if rotary_cos is not None:
+        _check_f32("rotary_cos", rotary_cos, dev)
+        _check_f32("rotary_sin", rotary_sin, dev)
+        _req(rotary_cos.dim() == 2 and rotary_sin.shape == rotary_cos.shape,
+             "rotary_cos/rotary_sin must be [seqlen_ro, rotary_dim/2]")
+        rd = int(rotary_dim) or D
+        _req(rotary_cos.shape[1] * 2 == rd and rd <= D and rd % 2 == 0,
+             f"rotary tables of width {rotary_cos.shape[1]} do not match rotary_dim {rd}")
+    if new_k is not None:
+        _req(new_v is not None, "new_k and new_v go together")
+        for n, t in (("k", new_k), ("v", new_v)):
+            _req(tuple(t.shape) == (B, NQ, Hk, D) and t.dtype == q.dtype and t.device == dev and
+                 t.is_contiguous(), f"{n}: contiguous [B, seqlen_q, nheads_k, D] of q's dtype")
+    else:
+        _req(new_v is None, "new_k and new_v go together")
     ctx_bound = block_table.shape[1] * page
     nsplit = int(_L.fa_decode_num_splits(B, NQ, Hq, Hq // Hk, ctx_bound, int(num_splits or 0)))
     out = torch.empty((B, NQ, Hq, D), dtype=q.dtype, device=q.device)
     scratch = torch.empty((B * NQ * Hq * nsplit * (D + 2),), dtype=torch.float32, device=q.device)
     lse = (torch.empty((B, NQ, Hq), dtype=torch.float32, device=q.device) if return_lse
            else torch.empty((0,), dtype=torch.float32, device=q.device))
-    p = DecParams()
+    p = FableDecParams()
     p.q, p.Kc, p.Vc = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr()
     p.block_table, p.o, p.scratch = block_table.data_ptr(), out.data_ptr(), scratch.data_ptr()
     p.ctx_len = cache_seqlens.data_ptr()
@@ -300,12 +376,9 @@ def dec(q, k_cache, v_cache, block_table, cache_seqlens, new_k, new_v, rotary_co
     p.alibi = alibi.data_ptr() if alibi is not None else None
     p.nq, p.rotary_dim = NQ, int(rotary_dim)
     p.rotary_pos = rotary_pos.data_ptr() if rotary_pos is not None else None
-    if new_k is not None:
-        _req(new_k.is_contiguous() and new_v is not None and new_v.is_contiguous(),
-             "new_k/new_v contiguous [B,nq,Hk,D]")
     with torch.cuda.device(q.device):
-        _lib.check(_L.fa_decode_launch(p, _dt(q), _stream(q), _ptr(new_k), _ptr(new_v)),
-                   "fa_decode_launch")
+        _lib.check(_L.fable_attn_dec(p, _dt(q), _stream(q), _ptr(new_k), _ptr(new_v)),
+                   "fable_attn_dec")
     return out, lse
 
 
@@ -316,6 +389,9 @@ def combine(out_partial, lse_partial, out_dtype):
     _req(out_partial.dim() == 5 and lse_partial.dim() == 4, "shapes [nsplit,B,S,H,D] / [nsplit,B,H,S]")
     _req(out_partial.stride(-1) == 1, "out_partial: head_dim must be contiguous")
     ns, B, S, H, D = out_partial.shape
+    _req(tuple(lse_partial.shape) == (ns, B, H, S),
+         f"lse_partial must be [nsplit, B, H, S] = {(ns, B, H, S)}, got {tuple(lse_partial.shape)}")
+    _req(lse_partial.device == out_partial.device, "out_partial and lse_partial on one device")
     lp = lse_partial.float()
     out = torch.empty((B, S, H, D), dtype=out_dtype, device=out_partial.device)
     c = CombineParams()

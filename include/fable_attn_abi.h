@@ -3,36 +3,35 @@
  * `libfable_attn_hip.so`.
  *
  * One header, included verbatim by the HIP translation units that implement the entry points
- * and by every host caller (the Python ctypes binding mirrors these structs field for field and
- * a CPU test checks the offsets against this file compiled with gcc). Parameter structs are
- * passed BY VALUE, exactly as the reference passes them, and are plain C: fixed-width fields,
- * device pointers as `const void*` / `void*`, strides in ELEMENTS, the innermost (head_dim)
- * stride is always 1. Every row of every tensor (its base pointer plus any combination of its
- * strides) must be 16-byte aligned: the kernels move rows in 16-byte loads and stores (for
- * 16-bit types, pointers and strides multiples of 8 elements; the Python binding checks this).
- * No torch or HIP types appear in any signature; a stream is `void*`
- * (a `hipStream_t`, NULL = the legacy default stream).
+ * and by every host caller. Parameter structs are passed BY VALUE, as the reference passes
+ * them, and are plain C: device pointers as `const void*` / `void*`, strides in ELEMENTS, the
+ * innermost (head_dim) stride is always 1. Every row of every tensor (its base pointer plus any
+ * combination of its strides) must be 16-byte aligned: the kernels move rows in 16-byte loads
+ * and stores (for 16-bit types, pointers and strides multiples of 8 elements). No torch or HIP
+ * types appear in any signature; a stream is `void*` (a `hipStream_t`, NULL = the legacy
+ * default stream). Nothing allocates: every output, workspace and scratch buffer belongs to the
+ * caller. Work is enqueued asynchronously on the stream; no entry point synchronises.
  *
- * Reference interface replaced (paths relative to the reference repository root):
- *   package/csrc/fa_iface.h:9-24   struct Strides + struct FwdParams
- *   package/csrc/fa_iface.h:27-38  struct Str + struct BwdParams
- *   package/csrc/fa_iface.h:42-63  struct DecParams
- *   package/csrc/fa_iface.h:65-68  the three extern "C" launchers
- *   package/csrc/stream.cu:8-10    fable_current_stream (not needed: callers pass their stream)
+ * Two sets of entry points (paths relative to the reference repository root):
  *
- * Deliberate differences from the reference's mirror structs (each one removes a defect or a
- * gfx1030-only mechanism; field meanings are otherwise unchanged):
- *   - launchers return an int status (FA_OK == 0) instead of printf+abort(); the message of the
- *     last failure on the calling thread is available from fable_attn_last_error();
- *   - one definition of every struct for host and device (the reference's kernel-side BwdParams
- *     carried a trailing `probe` field its host mirror lacked, backward.hip:72 vs fa_iface.h:38);
- *   - the bf16 power-of-two shift fields (sc_q/sc_k/sc_v, shQ/shK/shV/shdO) are gone: gfx950 MFMA
- *     consumes bf16 natively, so no host-side `.item()` synchronisation is needed;
- *   - the forward writes LSE for every batch element in one launch (lse_sb/lse_sh strides), so
- *     the host no longer loops over the batch (reference dispatch.cpp:61-78), and the varlen
- *     forward can return LSE too (the reference passed LSE=nullptr, dispatch.cpp:139);
- *   - the backward takes packed variable-length batches natively (cu_q/cu_k, ABI version 2)
- *     and an optional dS workspace that removes the dQ kernel's recomputation (ABI version 3).
+ * 1. The reference's own launchers, bit for bit: the structs Strides/FwdParams, Str/BwdParams
+ *    and DecParams have exactly the layout of package/csrc/fa_iface.h:9-63 and the three
+ *    launchers its :65-68 declares, so the reference's compiled glue
+ *    (package/csrc/dispatch.cpp) links against this library unchanged. The fields the
+ *    reference needed only for gfx1030 (bf16 power-of-two shifts sc_q/sc_k/sc_v and
+ *    shQ/shK/shV/shdO; page_shift/page_mask/append, which its launcher overwrote) are accepted
+ *    and ignored: gfx950 MFMA takes bf16 natively and the decode launcher derives the rest.
+ *    The reference's launchers return void; these return an int status (FA_OK == 0) in the
+ *    return register, which a caller declaring them void ignores. On failure they also print
+ *    the message to stderr, since such a caller never reads the status (the reference printed
+ *    and aborted).
+ *
+ * 2. This library's extended entry points (fable_attn_fwd/bwd/dec with FableFwdParams,
+ *    FableBwdParams, FableDecParams), used by the Python binding: the forward writes LSE for
+ *    every batch element and for packed variable-length batches (lse_sb/lse_sh), the backward
+ *    takes packed variable-length batches natively (cu_q/cu_k) and an optional dS workspace
+ *    that removes the dQ kernel's recomputation, plus the combine kernel, the decode split
+ *    planner and introspection.
  */
 #ifndef FABLE_ATTN_ABI_H
 #define FABLE_ATTN_ABI_H
@@ -44,7 +43,7 @@
 extern "C" {
 #endif
 
-#define FABLE_ATTN_ABI_VERSION 3
+#define FABLE_ATTN_ABI_VERSION 4
 
 /* dtype codes, same values as the reference (fa_forward.hip:403, backward.hip:25) */
 enum { FA_F16 = 0, FA_BF16 = 1, FA_F32 = 2 };
@@ -59,13 +58,96 @@ enum {
   FA_ERR_LAUNCH = 5        /* the HIP runtime rejected the launch */
 };
 
-/* Element strides of a [batch, head, seq, head_dim] view; head_dim stride is 1.
- * Reference: fa_iface.h:9 (Strides), fa_iface.h:27 (Str). */
+/* ========================================================================================
+ * 1. The reference's launchers with the reference's struct layouts (fa_iface.h:9-68).
+ * ======================================================================================== */
+
+/* Element strides {batch, head, seq} of a [B, H, S, D] view (fa_iface.h:9, :27). */
+typedef struct Strides { long long b, h, s; } Strides;
+typedef struct Str { long long b, h, s; } Str;
+
+/* fa_iface.h:10-24. Semantics as FableFwdParams below, with these limits of the reference
+ * layout: LSE (optional) is [NH][SQ] of ONE batch element — there is no batch stride, so a call
+ * with LSE != NULL must be dense with batch == 1 (the reference's glue calls once per batch
+ * element, dispatch.cpp:61-78); sc_q/sc_k/sc_v are ignored. */
+typedef struct FwdParams {
+  const void* Q; const void* K; const void* V; void* O; float* LSE;
+  Strides sQ, sK, sV, sO;
+  int SQ, SK, HD, NH, gqa;
+  float scale, softcap;
+  int win_left, win_right;
+  const float* alibi_slopes;
+  int causal;
+  float dropout_p; unsigned long long philox_seed;
+  const int* cu_q; const int* cu_k;
+  int batch;
+  float sc_q, sc_k, sc_v;
+  int attn_chunk;
+  const int* seqused_q; const int* seqused_k;
+} FwdParams;
+
+/* fa_iface.h:28-38. Dense [B,H,S,D] views only; lse and dsum are [B][Hq][SQ] fp32 (dsum is a
+ * caller-allocated workspace, overwritten); shQ/shK/shV/shdO are ignored. The dQ kernel
+ * recomputes S and dP (this struct has no field for a dS workspace; fable_attn_bwd takes one). */
+typedef struct BwdParams {
+  const void *Q, *K, *V, *O, *dO; void *dQ, *dK, *dV;
+  const float *lse; float *dsum;
+  Str qs, ks, vs, os, dos, dqs, dks, dvs;
+  int B, Hq, Hk, SQ, SK, D, gqa;
+  float scale, softcap;
+  const float *alibi;
+  int causal, win_left, win_right;
+  int dropout; unsigned long long drop_seed; float dropout_p, keep_scale;
+  int shQ, shK, shV, shdO;
+} BwdParams;
+
+/* fa_iface.h:42-63. Semantics as FableDecParams below; page_shift/page_mask/append are derived
+ * by the launcher (as the reference's launcher overwrote them) and sc_q/sc_k/sc_v are ignored.
+ * scratch holds batch*nq*NH*nsplit*(HD+2) floats. */
+typedef struct DecParams {
+  const void* q;
+  const void* Kc; const void* Vc;
+  const int* block_table;
+  void* o;
+  float* scratch;
+  const int* ctx_len;
+  const float* cos; const float* sin;
+  int batch, NH, gqa, HD, page, max_blocks, nsplit, window;
+  int page_shift, page_mask;
+  int rotary;
+  float scale;
+  float sc_q, sc_k, sc_v;
+  const int* leftpad;
+  float* lse_out;
+  float softcap;
+  const float* alibi;
+  int nq;
+  int append;
+  int rotary_dim;
+  const int* rotary_pos;
+} DecParams;
+
+/* fa_iface.h:65  extern "C" void fa_forward_launch(FwdParams p, int dtype, void* stream) */
+int fa_forward_launch(FwdParams p, int dtype, void* stream);
+
+/* fa_iface.h:66  extern "C" void fable_attn_backward_launch(BwdParams pr, int MODE, void* stream) */
+int fable_attn_backward_launch(BwdParams pr, int MODE, void* stream);
+
+/* fa_iface.h:67-68  extern "C" void fa_decode_launch(DecParams p, int dtype, void* stream,
+ *                                                    const void* new_k, const void* new_v) */
+int fa_decode_launch(DecParams p, int dtype, void* stream, const void* new_k, const void* new_v);
+
+/* ========================================================================================
+ * 2. This library's extended entry points (used by the Python binding).
+ * ======================================================================================== */
+
+/* Element strides of a [batch, head, seq, head_dim] view; head_dim stride is 1. */
 typedef struct fa_strides {
   int64_t b, h, s;
 } fa_strides;
 
-/* Forward parameters. Reference: fa_iface.h:10-24 / fa_forward.hip:23-49.
+/* Forward parameters: the reference's FwdParams (fa_iface.h:10-24, fa_forward.hip:23-49)
+ * without the bf16 shift fields, plus LSE strides.
  * Dense: Q [B,NH,SQ,HD], K/V [B,NH/gqa,SK,HD] as strided views, batch = B.
  * Varlen: cu_q/cu_k non-null (int32, batch+1 entries), SQ/SK = max_seqlen_q/k (grid size),
  *         sequence z occupies rows cu_q[z]..cu_q[z+1] (seq stride sQ.s), sQ.b/sK.b are ignored;
@@ -77,7 +159,7 @@ typedef struct fa_strides {
  *         then + alibi_slopes[h]*(j-i). A row with no visible key gets O = 0 and LSE = -inf.
  * LSE (natural log, fp32, optional): dense LSE[b*lse_sb + h*lse_sh + i];
  *         varlen LSE[h*lse_sh + cu_q[z] + i] (lse_sb ignored). */
-typedef struct FwdParams {
+typedef struct FableFwdParams {
   const void* Q;
   const void* K;
   const void* V;
@@ -101,13 +183,14 @@ typedef struct FwdParams {
   const int32_t* seqused_q;
   const int32_t* seqused_k;
   int64_t lse_sb, lse_sh;
-} FwdParams;
+} FableFwdParams;
 
-/* Backward parameters. Reference: fa_iface.h:28-38 / backward.hip:59-73.
+/* Backward parameters: the reference's BwdParams (fa_iface.h:28-38, backward.hip:59-73) without
+ * the bf16 shift fields, plus packed variable-length batches and the dS workspace.
  * Q,O,dO,dQ [B,Hq,SQ,D]; K,V,dK,dV [B,Hk,SK,D] (strided, D contiguous);
  * lse [B,Hq,SQ] fp32 contiguous (from the forward); dsum: fp32 workspace [B,Hq,SQ]
- * (caller-allocated, overwritten). Masking/softcap/alibi exactly as FwdParams. */
-typedef struct BwdParams {
+ * (caller-allocated, overwritten). Masking/softcap/alibi exactly as FableFwdParams. */
+typedef struct FableBwdParams {
   const void* Q;
   const void* K;
   const void* V;
@@ -145,9 +228,10 @@ typedef struct BwdParams {
    * entry, scratch on exit. */
   void* ds_ws;
   int64_t ds_ws_bytes;
-} BwdParams;
+} FableBwdParams;
 
-/* Paged-KV decode parameters. Reference: fa_iface.h:42-63 / fa_decode.hip:13-35.
+/* Paged-KV decode parameters: the reference's DecParams (fa_iface.h:42-63, fa_decode.hip:13-35)
+ * without the fields its launcher derived or that only gfx1030 needed.
  * q [batch, nq, NH, HD] contiguous; Kc/Vc [num_blocks, page, NH/gqa, HD] contiguous;
  * block_table [batch, max_blocks] int32; ctx_len [batch] int32 = cache length BEFORE the
  * append (flash_attn cache_seqlens); o [batch, nq, NH, HD]; scratch fp32
@@ -157,7 +241,7 @@ typedef struct BwdParams {
  * page must be a power of two. rotary: 0 none, 1 neox (half split), 2 interleaved (pairs);
  * cos/sin tables [seqlen_ro, rotary_dim/2] fp32, row chosen by (rotary_pos ? rotary_pos[b] :
  * ctx_len[b]) + tk; rotary_dim 0 means HD. */
-typedef struct DecParams {
+typedef struct FableDecParams {
   const void* q;
   const void* Kc;
   const void* Vc;
@@ -177,7 +261,7 @@ typedef struct DecParams {
   int32_t nq;
   int32_t rotary_dim;
   const int32_t* rotary_pos;
-} DecParams;
+} FableDecParams;
 
 /* LSE-weighted merge of split partial results (flash_attn_combine).
  * Reference: package/fable_attn/flash_attn_interface.py:567-580 (pure torch there).
@@ -197,22 +281,21 @@ typedef struct CombineParams {
 /* Entry points. Each returns FA_OK or an FA_ERR_* code; work is enqueued asynchronously on
  * `stream`; nothing is allocated or freed; every pointer is device memory. */
 
-/* replaces fa_iface.h:65  void fa_forward_launch(FwdParams p, int dtype, void* stream) */
-int fa_forward_launch(FwdParams p, int dtype, void* stream);
+/* the forward (reference launcher kernels/fa_forward.hip:424-451); dense or packed varlen */
+int fable_attn_fwd(FableFwdParams p, int dtype, void* stream);
 
-/* replaces fa_iface.h:66  void fable_attn_backward_launch(BwdParams pr, int MODE, void* stream) */
-int fable_attn_backward_launch(BwdParams p, int dtype, void* stream);
+/* the backward (reference launcher kernels/backward.hip:508-521); dense or packed varlen */
+int fable_attn_bwd(FableBwdParams p, int dtype, void* stream);
 
-/* Bytes of BwdParams.ds_ws the backward can use for these shapes (0: this head dim / dtype has
+/* Bytes of FableBwdParams.ds_ws the backward can use for these shapes (0: this head dim / dtype has
  * no dS-workspace path). No reference counterpart: the reference backward recomputes dS in its
  * dQ kernel (backward.hip:298-387). Size B*Hq*ceil(SQ/32)*ceil(SK/32)*2 KiB for fp16/bf16. */
-int64_t fable_attn_bwd_ds_bytes(BwdParams p, int dtype);
+int64_t fable_attn_bwd_ds_bytes(FableBwdParams p, int dtype);
 
-/* replaces fa_iface.h:67-68  void fa_decode_launch(DecParams p, int dtype, void* stream,
- *                                                  const void* new_k, const void* new_v)
+/* paged-KV decode (reference launcher kernels/fa_decode.hip:343-362).
  * new_k/new_v [batch, nq, NH/gqa, HD] (NULL = no append) are written into the paged cache
  * (with rotary on k) before attention, in stream order: no device-wide synchronisation. */
-int fa_decode_launch(DecParams p, int dtype, void* stream, const void* new_k, const void* new_v);
+int fable_attn_dec(FableDecParams p, int dtype, void* stream, const void* new_k, const void* new_v);
 
 /* split count chosen for a decode call (reference heuristic: dispatch.cpp:182-200, retuned for
  * 256 CUs); num_splits_hint > 0 is honoured (clamped to [1, 512]). */
@@ -223,7 +306,9 @@ int fa_combine_launch(CombineParams p, void* stream);
 
 /* introspection for bindings and tests */
 int fable_attn_abi_version(void);
-size_t fable_attn_struct_size(int which); /* 0 FwdParams, 1 BwdParams, 2 DecParams, 3 CombineParams, 4 fa_strides */
+/* sizeof of a struct: 0 FableFwdParams, 1 FableBwdParams, 2 FableDecParams, 3 CombineParams,
+ * 4 fa_strides, 5 FwdParams, 6 BwdParams, 7 DecParams (0 for any other value) */
+size_t fable_attn_struct_size(int which);
 const char* fable_attn_last_error(void);
 
 #ifdef __cplusplus

@@ -13,6 +13,9 @@
  *   oracle_bwd      kernels/backward.hip:566-597 (fp64 backward of the gate): recompute P from
  *                   the exact forward, Di = sum(O*dO), dS = P*(z*dP - Di)*softcap'(.), dQ,dK,dV
  *                   with dropout multiplier z (1 when dropout_p == 0).
+ *   oracle_bwd_model the same gradients with only the roundings a 16-bit-operand backward must
+ *                   make (O before Di, z*P before dV, dS before dK/dQ); not a reference
+ *                   routine: it measures the floor of fp16/bf16 kernels against oracle_bwd.
  *   dropout         kernels/fa_common.hpp:71-88: Philox4x32-10 (Salmon, Moraes, Dror, Shaw,
  *                   "Parallel random numbers: as easy as 1, 2, 3", SC 2011) on counter
  *                   (idx, 0, 0) and key = seed; u = (word0 >> 8) * 2^-24; kept (z = 1/(1-p))
@@ -165,8 +168,25 @@ void oracle_fwd(const float* Q, const float* K, const float* V, float* O, float*
 
 /* Backward (exact fp64 gradients of the forward above). dQ/dK/dV are double outputs,
  * overwritten. dO [B][H][SQ][D]. */
-void oracle_bwd(const float* Q, const float* K, const float* V, const float* dO, double* dQ,
-                double* dK, double* dV, const OracleCfg* c) {
+static float round_f16(float x);
+static float round_bf16(float x);
+
+/* Round a double to the storage dtype of `mode` (0 keep, 1 fp16, 2 bf16), back to double. */
+static double round_mode(double x, int mode) {
+  if (mode == 1) return (double)round_f16((float)x);
+  if (mode == 2) return (double)round_bf16((float)x);
+  return x;
+}
+
+/* mode 0: exact fp64 gradients. mode 1/2 (fp16/bf16): the same gradients with the roundings a
+ * kernel that feeds 16-bit matrix products must make, and nothing else: O is rounded to the
+ * dtype before Di = sum(O*dO) (the kernels read D from the stored O), the dropped probability
+ * z*P is rounded before dV += (z*P)^T dO, and dS is rounded (before the softmax scale) before
+ * dK += scale*dS^T Q and dQ += scale*dS K. Accumulation stays in double. The distance of this
+ * model from mode 0 is the floor that any 16-bit-operand backward shows against the exact
+ * gradients. */
+static void bwd_impl(const float* Q, const float* K, const float* V, const float* dO, double* dQ,
+                     double* dK, double* dV, const OracleCfg* c, int mode) {
   const int gqa = c->H / c->Hk;
   const size_t nq = (size_t)c->B * c->H * c->SQ * c->D, nk = (size_t)c->B * c->Hk * c->SK * c->D;
   memset(dQ, 0, nq * sizeof(double));
@@ -212,8 +232,8 @@ void oracle_bwd(const float* Q, const float* K, const float* V, const float* dO,
             double acc = 0.0;
             for (int j = 0; j < c->SK; j++)
               acc += P[j] * drop_mul(c, h, i, j) * (double)Vb[(size_t)j * c->D + d];
-            o[d] = acc;
-            Di += acc * (double)g[d];
+            o[d] = round_mode(acc, mode);
+            Di += o[d] * (double)g[d];
           }
           double* dq = dQ + qo;
           for (int j = 0; j < c->SK; j++) {
@@ -221,9 +241,10 @@ void oracle_bwd(const float* Q, const float* K, const float* V, const float* dO,
             const double z = drop_mul(c, h, i, j);
             double dp = 0.0;
             for (int d = 0; d < c->D; d++) dp += (double)g[d] * (double)Vb[(size_t)j * c->D + d];
-            const double dS = P[j] * (z * dp - Di) * Dv[j]; /* backward.hip:170-176 */
+            const double dS = round_mode(P[j] * (z * dp - Di) * Dv[j], mode); /* backward.hip:170-176 */
+            const double zp = round_mode(z * P[j], mode);
             for (int d = 0; d < c->D; d++) {
-              dVb[(size_t)j * c->D + d] += z * P[j] * (double)g[d];
+              dVb[(size_t)j * c->D + d] += zp * (double)g[d];
               dKb[(size_t)j * c->D + d] += c->scale * dS * (double)q[d];
               dq[d] += c->scale * dS * (double)Kb[(size_t)j * c->D + d];
             }
@@ -233,6 +254,18 @@ void oracle_bwd(const float* Q, const float* K, const float* V, const float* dO,
       free(Dv);
       free(o);
     }
+}
+
+/* exact fp64 gradients */
+void oracle_bwd(const float* Q, const float* K, const float* V, const float* dO, double* dQ,
+                double* dK, double* dV, const OracleCfg* c) {
+  bwd_impl(Q, K, V, dO, dQ, dK, dV, c, 0);
+}
+
+/* rounding model of a 16-bit-operand backward (mode 1 fp16, 2 bf16), see bwd_impl */
+void oracle_bwd_model(const float* Q, const float* K, const float* V, const float* dO,
+                      double* dQ, double* dK, double* dV, const OracleCfg* c, int mode) {
+  bwd_impl(Q, K, V, dO, dQ, dK, dV, c, mode);
 }
 
 typedef struct OracleDecCfg {

@@ -196,8 +196,12 @@ def fwd(q, k, v, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0, al
 
 
 def bwd(q, k, v, do, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0, alibi=None,
-        chunk=0, dropout_p=0.0, seed=0):
-    """fp64 backward oracle: returns (dq, dk, dv) float64 with the layouts of q, k, v."""
+        chunk=0, dropout_p=0.0, seed=0, model=None):
+    """fp64 backward oracle: returns (dq, dk, dv) float64 with the layouts of q, k, v.
+    model=None gives the exact gradients. model='f16'/'bf16' gives the rounding model of a
+    backward whose matrix products take 16-bit operands (oracle.c bwd_impl): O rounded before
+    D = rowsum(O*dO), z*P rounded before the dV product, dS rounded before the dK/dQ products;
+    its distance from the exact gradients is the floor of any such kernel."""
     q, k, v, do = _f32(q), _f32(k), _f32(v), _f32(do)
     B, H, SQ, D = q.shape
     Hk, SK = k.shape[1], k.shape[2]
@@ -209,7 +213,12 @@ def bwd(q, k, v, do, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0
                     int(win_right), int(bool(causal)), int(chunk),
                     al.ctypes.data if al is not None else None, _f32s(dropout_p),
                     int(seed) & ((1 << 64) - 1))
-    lib().oracle_bwd(_p(q), _p(k), _p(v), _p(do), _p(dq), _p(dk), _p(dv), ctypes.byref(cfg))
+    mode = {None: 0, "f32": 0, "f16": 1, "bf16": 2}[model]
+    if mode:
+        lib().oracle_bwd_model(_p(q), _p(k), _p(v), _p(do), _p(dq), _p(dk), _p(dv),
+                               ctypes.byref(cfg), ctypes.c_int(mode))
+    else:
+        lib().oracle_bwd(_p(q), _p(k), _p(v), _p(do), _p(dq), _p(dk), _p(dv), ctypes.byref(cfg))
     return dq, dk, dv
 
 

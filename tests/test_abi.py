@@ -18,35 +18,69 @@ def _declared_functions():
     return sorted(set(re.findall(r"^\s*(?:int|int64_t|size_t|const char\*)\s+(\w+)\s*\(", src, flags=re.M)))
 
 
-def _offsets_from_gcc(tmp_path):
+REF_IFACE = "/root/reference/package/csrc/fa_iface.h"
+
+
+def _struct_table():
     from fable_attn import _lib
-    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{HEADER}"', "int main(void){"]
-    for name, st in (("fa_strides", _lib.Strides), ("FwdParams", _lib.FwdParams),
-                     ("BwdParams", _lib.BwdParams), ("DecParams", _lib.DecParams),
-                     ("CombineParams", _lib.CombineParams)):
+    return (("fa_strides", _lib.Strides), ("FableFwdParams", _lib.FableFwdParams),
+            ("FableBwdParams", _lib.FableBwdParams), ("FableDecParams", _lib.FableDecParams),
+            ("CombineParams", _lib.CombineParams), ("Strides", _lib.RefStrides),
+            ("FwdParams", _lib.RefFwdParams), ("BwdParams", _lib.RefBwdParams),
+            ("DecParams", _lib.RefDecParams))
+
+
+def _offsets(tmp_path, header, structs, compiler):
+    """sizeof and offsetof of every field of `structs` (name, ctypes mirror) as the compiler
+    lays them out from `header`."""
+    lines = ['#include <stdio.h>', '#include <stddef.h>', f'#include "{header}"', "int main(void){"]
+    for name, st in structs:
         lines.append(f'printf("{name} sizeof %zu\\n", sizeof({name}));')
         for f, _ in st._fields_:
             lines.append(f'printf("{name} {f} %zu\\n", offsetof({name}, {f}));')
     lines.append("return 0;}")
-    c = tmp_path / "abi.c"
-    c.write_text("\n".join(lines))
-    exe = tmp_path / "abi"
-    subprocess.run(["gcc", "-std=c11", "-Wall", "-Werror", "-o", str(exe), str(c)], check=True)
+    src = tmp_path / ("abi.c" if compiler == "gcc" else "abi.cpp")
+    src.write_text("\n".join(lines))
+    exe = tmp_path / ("abi_" + compiler)
+    std = "-std=c11" if compiler == "gcc" else "-std=c++17"
+    subprocess.run([compiler, std, "-Wall", "-Werror", "-o", str(exe), str(src)], check=True)
     out = subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
     return {tuple(l.split()[:2]): int(l.split()[2]) for l in out.splitlines()}
 
 
-def test_struct_layout_matches_header(tmp_path):
-    from fable_attn import _lib
-    got = _offsets_from_gcc(tmp_path)
-    for name, st in (("fa_strides", _lib.Strides), ("FwdParams", _lib.FwdParams),
-                     ("BwdParams", _lib.BwdParams), ("DecParams", _lib.DecParams),
-                     ("CombineParams", _lib.CombineParams)):
+def _check_layout(got, structs):
+    for name, st in structs:
         assert got[(name, "sizeof")] == ctypes.sizeof(st), name
         for f, _ in st._fields_:
             assert got[(name, f)] == getattr(st, f).offset, (name, f)
+
+
+def test_struct_layout_matches_header(tmp_path):
+    """Both struct families of the header, compiled as C and as C++, against the binding."""
+    from fable_attn import _lib
+    structs = _struct_table()
+    _check_layout(_offsets(tmp_path, HEADER, structs, "gcc"), structs)
+    _check_layout(_offsets(tmp_path, HEADER, structs, "g++"), structs)
     # every header field is mirrored (nothing missing on the Python side)
-    assert len(_lib.FwdParams._fields_) == 30
+    assert len(_lib.FableFwdParams._fields_) == 30
+    assert len(_lib.RefFwdParams._fields_) == 31 and len(_lib.RefDecParams._fields_) == 32
+
+
+def test_reference_layout_matches_reference_header(tmp_path):
+    """The reference-layout structs are bit-for-bit the reference's own fa_iface.h:9-63 (every
+    field's offset and the size), so its compiled glue can pass them by value to this library.
+    Needs the reference tree (skipped where it is absent, e.g. on a GPU box)."""
+    if not os.path.exists(REF_IFACE):
+        pytest.skip("reference tree absent")
+    from fable_attn import _lib
+    ref = (("Strides", _lib.RefStrides), ("Str", _lib.RefStrides), ("FwdParams", _lib.RefFwdParams),
+           ("BwdParams", _lib.RefBwdParams), ("DecParams", _lib.RefDecParams))
+    _check_layout(_offsets(tmp_path, REF_IFACE, ref, "g++"), ref)
+    # and the library's own compiled sizes agree
+    lib = _lib.load()
+    assert lib.fable_attn_struct_size(5) == ctypes.sizeof(_lib.RefFwdParams)
+    assert lib.fable_attn_struct_size(6) == ctypes.sizeof(_lib.RefBwdParams)
+    assert lib.fable_attn_struct_size(7) == ctypes.sizeof(_lib.RefDecParams)
 
 
 def test_library_exports_every_declared_function():
@@ -56,7 +90,7 @@ def test_library_exports_every_declared_function():
     assert set(declared) == set(_lib.EXPORTS), declared
     for f in declared:
         assert hasattr(lib, f), f
-    assert lib.fable_attn_abi_version() == _lib.ABI_VERSION == 3
+    assert lib.fable_attn_abi_version() == _lib.ABI_VERSION == 4
     for k, st in _lib.STRUCTS.items():
         assert lib.fable_attn_struct_size(k) == ctypes.sizeof(st)
 
@@ -64,20 +98,39 @@ def test_library_exports_every_declared_function():
 def test_launchers_validate_before_device_work():
     from fable_attn import _lib
     lib = _lib.load()
-    p = _lib.FwdParams()          # null tensors
-    assert lib.fa_forward_launch(p, 0, None) == 3
+    p = _lib.FableFwdParams()          # null tensors
+    assert lib.fable_attn_fwd(p, 0, None) == 3
     assert b"null" in lib.fable_attn_last_error()
     p.Q = p.K = p.V = p.O = 16    # never dereferenced: rejected on head_dim first
     p.NH, p.gqa, p.batch, p.SQ, p.SK, p.HD = 4, 1, 1, 8, 8, 72
-    assert lib.fa_forward_launch(p, 0, None) == 2
+    assert lib.fable_attn_fwd(p, 0, None) == 2
     assert b"head_dim=72" in lib.fable_attn_last_error()
     p.HD = 64
-    assert lib.fa_forward_launch(p, 7, None) == 1          # unknown dtype
+    assert lib.fable_attn_fwd(p, 7, None) == 1          # unknown dtype
     p.dropout_p = 1.0                                      # keeps nothing: rejected
-    assert lib.fa_forward_launch(p, 0, None) == 3
+    assert lib.fable_attn_fwd(p, 0, None) == 3
     assert b"dropout_p" in lib.fable_attn_last_error()
     c = _lib.CombineParams()
     assert lib.fa_combine_launch(c, None) == 3
+
+
+def test_reference_launchers_validate_before_device_work():
+    """The reference-layout launchers reject bad arguments with a status (and print it) before
+    any device work, through the same checks as the extended entry points."""
+    from fable_attn import _lib
+    lib = _lib.load()
+    r = _lib.RefFwdParams()
+    assert lib.fa_forward_launch(r, 0, None) == 3          # null tensors
+    r.Q = r.K = r.V = r.O = 16
+    r.NH, r.gqa, r.batch, r.SQ, r.SK, r.HD = 4, 1, 1, 8, 8, 72
+    assert lib.fa_forward_launch(r, 0, None) == 2          # no head_dim 72 kernel
+    r.HD, r.batch, r.LSE = 64, 2, 16                       # LSE without a batch stride
+    assert lib.fa_forward_launch(r, 0, None) == 3
+    assert b"batch == 1" in lib.fable_attn_last_error()
+    b = _lib.RefBwdParams()
+    assert lib.fable_attn_backward_launch(b, 1, None) == 3
+    d = _lib.RefDecParams()
+    assert lib.fa_decode_launch(d, 0, None, None, None) == 3
 
 
 @pytest.mark.parametrize("hint,expect", [(4, 4), (1000, 512), (-1, None)])
@@ -96,7 +149,7 @@ def test_bwd_ds_workspace_size():
     the fp16/bf16 head dims with a dS-workspace path (64, 128); 0 elsewhere (host-only call)."""
     from fable_attn import _lib
     lib = _lib.load()
-    p = _lib.BwdParams()
+    p = _lib.FableBwdParams()
     p.B, p.Hq, p.Hk, p.gqa, p.SQ, p.SK, p.D = 2, 8, 2, 4, 100, 65, 128
     want = 2 * 8 * 4 * 3 * 2048
     assert lib.fable_attn_bwd_ds_bytes(p, 0) == want and lib.fable_attn_bwd_ds_bytes(p, 1) == want

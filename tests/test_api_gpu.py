@@ -84,3 +84,43 @@ def test_paged_varlen_equals_packed():
                          D ** -0.5, causal=True, win_right=0)
         got = to_np(packed[cq[i]:cq[i + 1]]).transpose(1, 0, 2)[None]
         assert orc.rel_rms(got, ref) <= TOL[dt], f"sequence {i}"
+
+
+def test_host_checks_reject_before_launch():
+    """Argument checks of the _C glue raise on the host, before any kernel is enqueued: a
+    mismatched lse_partial in combine, cu_seqlens on the CPU or with too few entries, seqused
+    of the wrong length, and decode side inputs of the wrong dtype or length."""
+    import pytest
+    import torch
+
+    from fable_attn import _C
+    dev = "cuda"
+    op = torch.zeros(2, 1, 8, 4, 64, device=dev, dtype=torch.float16)
+    with pytest.raises(RuntimeError, match="lse_partial"):
+        _C.combine(op, torch.zeros(2, 1, 8, 4, device=dev), torch.float16)    # (S, H) swapped
+    with pytest.raises(RuntimeError, match="lse_partial"):
+        _C.combine(op, torch.zeros(1, 1, 4, 8, device=dev), torch.float16)    # fewer splits
+    q = torch.zeros(10, 4, 64, device=dev, dtype=torch.float16)
+    cu = torch.tensor([0, 4, 10], dtype=torch.int32)
+    args = (q, q, q)
+    with pytest.raises(RuntimeError, match="cu_seqlens_q"):
+        _C.fwd_varlen(*args, cu, cu.to(dev), 6, 6, 0.1, True, -1, 0, 0.0, None, 0.0, 0)
+    with pytest.raises(RuntimeError, match="cu_seqlens_k"):
+        _C.fwd_varlen(*args, cu.to(dev), cu[:2].to(dev), 6, 6, 0.1, True, -1, 0, 0.0, None, 0.0, 0)
+    with pytest.raises(RuntimeError, match="seqused_q"):
+        _C.fwd_varlen(*args, cu.to(dev), cu.to(dev), 6, 6, 0.1, True, -1, 0, 0.0, None, 0.0, 0,
+                      seqused_q=torch.tensor([1, 2, 3], dtype=torch.int32, device=dev))
+    qd = torch.zeros(2, 1, 8, 64, device=dev, dtype=torch.float16)
+    kc = torch.zeros(4, 16, 2, 64, device=dev, dtype=torch.float16)
+    bt = torch.zeros(2, 2, dtype=torch.int32, device=dev)
+    cs = torch.full((2,), 5, dtype=torch.int32, device=dev)
+    with pytest.raises(RuntimeError, match="alibi"):
+        _C.dec(qd, kc, kc, bt, cs, None, None, None, None, False, 0.1, -1,
+               alibi=torch.zeros(8, dtype=torch.float16, device=dev))
+    with pytest.raises(RuntimeError, match="cache_leftpad"):
+        _C.dec(qd, kc, kc, bt, cs, None, None, None, None, False, 0.1, -1,
+               cache_leftpad=torch.zeros(2, dtype=torch.int64, device=dev))
+    with pytest.raises(RuntimeError, match="cache_seqlens"):
+        _C.dec(qd, kc, kc, bt, cs[:1], None, None, None, None, False, 0.1, -1)
+    with pytest.raises(RuntimeError, match="block_table"):
+        _C.dec(qd, kc, kc, bt[:1], cs, None, None, None, None, False, 0.1, -1)

@@ -1,14 +1,19 @@
-"""Backward parity on the GPU: fable_attn_backward_launch (through fable_attn._C.bwd, the C-ABI)
-vs exact fp64 gradients from the oracle, on identical seeded inputs; O and LSE come from this
-library's forward as they do in training.
+"""Backward parity on the GPU: fable_attn_bwd (through fable_attn._C.bwd, the C-ABI) vs exact
+fp64 gradients from the oracle, on identical seeded inputs; O and LSE come from this library's
+forward as they do in training.
 
 Cases follow the reference backward gate (kernels/backward.hip:710-735: base, causal, GQA,
-ragged tails, SQ != SK both ways, windows, head dims, softcap, alibi). Bounds: rel_rms of each
-gradient <= 2e-3 (fp16) / 8e-3 (bf16) — the gradients are the product of fp16/bf16-rounded
-P and dS matrices and are stored in fp16/bf16, so their floor is above the forward's — and
-bitwise-identical results across repeated runs (the atomic-free contract). At the full
-BASELINE.json configs[2] size the kernel is checked against a float32 torch autograd
-reference on the GPU for sampled heads, and for bitwise reproducibility over 3 runs.
+ragged tails, SQ != SK both ways, windows, head dims, softcap, alibi). Bounds, per gradient:
+  * rel_rms against the exact fp64 gradients <= 5e-4 (fp16) / 4e-3 (bf16), the BASELINE.json
+    bounds (the reference's own gate allowed 2.5e-3 / 6e-3, kernels/backward.hip:734);
+  * rel_rms against the oracle's rounding model (oracle.bwd(..., model=dtype): O, z*P and dS
+    rounded to the dtype as any 16-bit-operand kernel must round them) <= MODEL_TOL (4e-4 /
+    3e-3, tests/helpers.py), which leaves room for the rounding of the stored gradients and
+    little else;
+  * bitwise-identical results across repeated runs (the atomic-free contract).
+The model's own distance from the exact gradients (its floor) is ~2.3e-4 (fp16) and ~2e-3
+(bf16) on these cases. Every case logs its measured errors (tests/helpers.py log_errors).
+At the full BASELINE.json configs[2] size sampled heads are checked against the fp64 oracle.
 
 Every case runs both backward paths at head_dim 64/128: "ds" (the dK/dV kernel stores dS in a
 workspace and dQ = dS.K is formed from it, the default) and "recompute" (no workspace: the dQ
@@ -20,11 +25,9 @@ import numpy as np
 import pytest
 
 from oracle import oracle as orc
-from tests.helpers import gen, to_dev, to_np
+from tests.helpers import check_grads, gen, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
-
-GTOL = {"f16": 2e-3, "bf16": 8e-3}
 
 # name, B, Hq, Hk, SQ, SK, D, causal, wl, wr, softcap, alibi
 CASES = [
@@ -70,7 +73,8 @@ def run(case, dt, seed=0, repeats=1, path="ds"):
                   ds_max_bytes=PATHS[path]) for _ in range(repeats)]
     torch.cuda.synchronize()
     ref = orc.bwd(q, k, v, do, scale, causal, wl, wr, sc, al)
-    return res, ref
+    model = orc.bwd(q, k, v, do, scale, causal, wl, wr, sc, al, model=dt)
+    return res, ref, model
 
 
 @pytest.mark.parametrize("path", list(PATHS))
@@ -78,14 +82,11 @@ def run(case, dt, seed=0, repeats=1, path="ds"):
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
 def test_backward_parity(case, dt, path):
     print(f"[bwd] {case[0]} {dt} {path}", flush=True)
-    res, ref = run(case, dt, repeats=3, path=path)
+    res, ref, model = run(case, dt, repeats=3, path=path)
     for i, name in enumerate(("dq", "dk", "dv")):
-        got = to_np(res[0][i])
-        assert np.isfinite(got).all(), f"{name} not finite"
-        e = orc.rel_rms(got, ref[i])
-        assert e <= GTOL[dt], f"{name} rel_rms {e:.3e} > {GTOL[dt]}"
         for r in res[1:]:
             assert torch_equal(r[i], res[0][i]), f"{name} differs between runs"
+    check_grads("bwd_" + path, case[0], dt, res[0], ref, model)
 
 
 def torch_equal(a, b):
@@ -96,7 +97,8 @@ def torch_equal(a, b):
 @pytest.mark.parametrize("path", list(PATHS))
 def test_backward_full_config_c3(path):
     """causal bf16, B=2, S=4096, H=32, D=128; bitwise identical over
-    3 runs; sampled heads against a float32 torch autograd reference on the GPU."""
+    3 runs; the gradients of sampled (batch, head) pairs (first, last and a middle one) against
+    the fp64 oracle and its rounding model, with the bounds of the small cases."""
     import torch
 
     from fable_attn import _C
@@ -115,15 +117,15 @@ def test_backward_full_config_c3(path):
     for r in runs[1:]:
         for a, b in zip(runs[0], r):
             assert torch.equal(a, b)
-    for bb, hd in ((0, 0), (1, 31)):
-        qf, kf, vf = (x[bb, :, hd].float().detach().clone().requires_grad_() for x in (q, k, v))
-        s = (qf @ kf.t()) * scale
-        s = s.masked_fill(torch.ones(S, S, device="cuda", dtype=torch.bool).triu(1), float("-inf"))
-        o = torch.softmax(s, -1) @ vf
-        o.backward(do[bb, :, hd].float())
-        for got, ref in ((runs[0][0][bb, hd], qf.grad), (runs[0][1][bb, hd], kf.grad), (runs[0][2][bb, hd], vf.grad)):
-            e = ((got.float() - ref).norm() / ref.norm()).item()
-            assert e <= GTOL["bf16"], e
+    heads = ((0, 0), (1, 31), (1, 13))
+    # the sampled heads as one B=1, H=3 problem (the oracle runs one thread per head)
+    pick = lambda t: np.stack([to_np(t[bb, :, hd]) for bb, hd in heads])[None]
+    qs, ks, vs, dos = pick(q), pick(k), pick(v), pick(do)
+    ref = orc.bwd(qs, ks, vs, dos, scale, True)
+    model = orc.bwd(qs, ks, vs, dos, scale, True, model="bf16")
+    got = [torch.stack([x[bb, hd] for bb, hd in heads])[None] for x in runs[0]]
+    check_grads("bwd_full_c3_" + path, "C3 B2 S4096 H32 D128 heads (0,0),(1,31),(1,13)", "bf16",
+                got, ref, model)
 
 
 def test_backward_ds_workspace_too_small_falls_back():
@@ -131,7 +133,7 @@ def test_backward_ds_workspace_too_small_falls_back():
     must be ignored (the recomputing path runs, the buffer stays untouched); a full-size one
     filled with NaN bit
     patterns must give the same gradients (tiles that are never written are never read).
-    Both against the oracle, through the C-ABI with a hand-built BwdParams."""
+    Both against the oracle, through the C-ABI with a hand-built FableBwdParams."""
     import torch
 
     from fable_attn import _C, _lib
@@ -149,7 +151,7 @@ def test_backward_ds_workspace_too_small_falls_back():
     out, lse = _C.fwd(qd, kd, vd, scale, causal, wl, wr, sc, None, 0.0, 0)
     dq, dk, dv = (torch.empty_like(x) for x in (qd, kd, vd))
     dsum = torch.empty((B, Hq, SQ), dtype=torch.float32, device="cuda")
-    p = _lib.BwdParams()
+    p = _lib.FableBwdParams()
     p.Q, p.K, p.V, p.O, p.dO = qd.data_ptr(), kd.data_ptr(), vd.data_ptr(), out.data_ptr(), dod.data_ptr()
     p.dQ, p.dK, p.dV = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
     p.lse, p.dsum = lse.data_ptr(), dsum.data_ptr()
@@ -165,24 +167,20 @@ def test_backward_ds_workspace_too_small_falls_back():
     # too small, then big enough but not 16-byte aligned: both ignored
     for ptr, nbytes in ((ws.data_ptr(), need - 1), (ws.data_ptr() + 8, need)):
         p.ds_ws, p.ds_ws_bytes = ptr, nbytes
-        assert lib.fable_attn_backward_launch(p, 1, stream) == 0
+        assert lib.fable_attn_bwd(p, 1, stream) == 0
         torch.cuda.synchronize()
         assert torch.all(ws == 0xFF), "an unusable workspace must not be written"
     p.ds_ws = ws.data_ptr()
     ref = orc.bwd(q, k, v, do, scale, causal)
-    for got, r, gname in ((dq, ref[0], "dq"), (dk, ref[1], "dk"), (dv, ref[2], "dv")):
-        e = orc.rel_rms(to_np(got), r)
-        assert e <= GTOL[dt], f"{gname} rel_rms {e:.3e}"
+    model = orc.bwd(q, k, v, do, scale, causal, model=dt)
+    check_grads("bwd_ws_ignored", name, dt, (dq, dk, dv), ref, model)
     # a full-size workspace poisoned with NaN patterns: the dQ kernel reads only the tiles the
     # dK/dV kernel wrote (the causal upper-right tiles stay NaN and must not leak into dQ)
     p.ds_ws_bytes = need
-    assert lib.fable_attn_backward_launch(p, 1, stream) == 0
+    assert lib.fable_attn_bwd(p, 1, stream) == 0
     torch.cuda.synchronize()
     assert not torch.all(ws == 0xFF), "the workspace path was not taken"
-    for got, r, gname in ((dq, ref[0], "dq"), (dk, ref[1], "dk"), (dv, ref[2], "dv")):
-        assert torch.isfinite(got).all(), f"{gname} not finite"
-        e = orc.rel_rms(to_np(got), r)
-        assert e <= GTOL[dt], f"{gname} rel_rms {e:.3e} (poisoned workspace)"
+    check_grads("bwd_ws_poisoned", name, dt, (dq, dk, dv), ref, model)
 
 
 def ctypes_stream():

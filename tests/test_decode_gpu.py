@@ -1,4 +1,4 @@
-"""Paged-KV decode parity on the GPU: fa_decode_launch (through fable_attn._C.dec, the C-ABI)
+"""Paged-KV decode parity on the GPU: fable_attn_dec (through fable_attn._C.dec, the C-ABI)
 vs the fp64 decode oracle on identical seeded inputs.
 
 Cases follow the reference decode gate (kernels/fa_decode_gate.inc:159-191: GQA, rotary
@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import oracle as orc
-from tests.helpers import LSE_ABS, TOL, gen, to_dev, to_np
+from tests.helpers import LSE_ABS, TOL, gen, log_errors, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -92,15 +92,15 @@ def run_oracle(c, dt):
                       alibi=c["al"], append_dtype=dt)
 
 
-def check(o, l, o_ref, l_ref, dt):
+def check(o, l, o_ref, l_ref, dt, case="decode"):
     rel = orc.rel_rms(o, o_ref)
+    fin = np.isfinite(l_ref)
+    err = float(np.abs(l[fin] - l_ref[fin]).max()) if fin.any() else 0.0
+    log_errors("decode", case, dt, o=rel, lse=err)
     assert np.isfinite(o).all()
     assert rel <= TOL[dt], f"rel_rms {rel:.3e} > {TOL[dt]}"
     assert np.array_equal(np.isneginf(l), np.isneginf(l_ref))
-    fin = np.isfinite(l_ref)
-    if fin.any():
-        err = np.abs(l[fin] - l_ref[fin]).max()
-        assert err <= LSE_ABS, f"LSE err {err:.3e}"
+    assert err <= LSE_ABS, f"LSE err {err:.3e}"
 
 
 @pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
@@ -110,7 +110,7 @@ def test_decode_parity(case, dt):
     c = make_case(case, dt)
     o, l, kc, vc = run_kernel(c, dt)
     o_ref, l_ref = run_oracle(c, dt)
-    check(o, l, o_ref, l_ref, dt)
+    check(o, l, o_ref, l_ref, dt, case[0])
     if c["nk"] is not None:
         # the appended V rows were written into the cache at positions ctx..ctx+nq-1
         vcn = to_np(vc)
@@ -127,7 +127,7 @@ def test_decode_split_counts_agree(nsplit):
     c = make_case(("splits", 128, 32, 4, [3000, 1111], -1, 0, False, 0, 1, 0.0, False, 64), "f16")
     o, l, _, _ = run_kernel(c, "f16", num_splits=nsplit)
     o_ref, l_ref = run_oracle(c, "f16")
-    check(o, l, o_ref, l_ref, "f16")
+    check(o, l, o_ref, l_ref, "f16", f"nsplit {nsplit}")
 
 
 def test_decode_page_permutation_bitwise():
@@ -172,4 +172,5 @@ def test_decode_full_config_sampled():
         tb = np.arange(ctx // page, dtype=np.int32)[None]
         o_ref, l_ref = orc.decode(q[b:b + 1].float().cpu().numpy(), kb, vb, tb,
                                   np.array([ctx], np.int32), D ** -0.5)
-        check(to_np(out[b:b + 1]), to_np(lse[b:b + 1]).transpose(0, 2, 1), o_ref, l_ref, "f16")
+        check(to_np(out[b:b + 1]), to_np(lse[b:b + 1]).transpose(0, 2, 1), o_ref, l_ref, "f16",
+              f"C4 full size sequence {b}")

@@ -1,4 +1,4 @@
-"""fp32 forward and backward on the GPU (fa_forward_launch / fable_attn_backward_launch with
+"""fp32 forward and backward on the GPU (fable_attn_fwd / fable_attn_bwd with
 dtype FA_F32, through fable_attn._C), against the fp64 oracle on the same inputs.
 
 The reference serves fp32 through separate kernels (kernels/fa_forward.hip:317-400, 440-447;
