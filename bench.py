@@ -85,11 +85,11 @@ def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0):
     """C3: causal bf16 backward, timed without the forward; bitwise-identical check over 3 runs."""
     import torch
     from fable_attn import _C
-    from fable_attn.flash_attn_interface import _kernel_view
+    from fable_attn.flash_attn_interface import _bhsd
     dt = torch.bfloat16
     g = torch.Generator(device="cuda").manual_seed(seed)
     q, k, v, do = (torch.randn(B, S, H, D, device="cuda", dtype=dt, generator=g) for _ in range(4))
-    qh, kh, vh, doh = (_kernel_view(x) for x in (q, k, v, do))
+    qh, kh, vh, doh = (_bhsd(x) for x in (q, k, v, do))
     scale = D ** -0.5
     out, lse = _C.fwd(qh, kh, vh, scale, True, -1, 0, 0.0, None, 0.0, 0)
 

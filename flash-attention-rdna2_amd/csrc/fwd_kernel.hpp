@@ -307,10 +307,13 @@ fwd_kernel(FableFwdParams p, int nqt) {
     m_run[i] = need ? m_cand : m_run[i];
     resc = __builtin_amdgcn_ballot_w64(need) != 0;
     const float m_use = m_run[i] == -INFINITY ? 0.0f : m_run[i];
-    // fp16 sums the rounded probabilities pairwise (their rounding moves the row sum by at most
-    // 2^-12 relative); bf16 rounding is 8x coarser, so it sums the fp32 values, and so does
-    // dropout, which scales the probabilities after the sum
-    constexpr bool kPairSum = std::is_same<T, _Float16>::value && !DROP;
+    // The row sum adds the fp32 probabilities (not the rounded ones the PV product takes): the
+    // LSE is then exact to fp32 rounding, and the backward, which rebuilds P = exp(s - LSE),
+    // sees probabilities that sum to 1. Summing the fp16-rounded values pairwise (v_dot2) ran at
+    // the same speed but left the LSE off by up to 2e-4, a row-wide scale error of every P the
+    // fp16 backward rebuilt (its dQ/dK error against exact gradients rose from 3.7e-4 to 5.5e-4
+    // on short causal rows). Dropout scales the probabilities after the sum either way.
+    constexpr bool kPairSum = false;
     float r0 = 0.0f, r1 = 0.0f;
 #pragma unroll
     for (int jb = 0; jb < C::NB; jb++)

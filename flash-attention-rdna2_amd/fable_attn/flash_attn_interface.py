@@ -1,56 +1,55 @@
 """flash_attn API (FA-2 argument order) over the gfx950 kernels of libfable_attn_hip.so.
 
-Same public surface, argument order, defaults, shapes and error behaviour as the reference's
-package/fable_attn/flash_attn_interface.py:
+Public surface, argument order, defaults, return shapes, exception types and the message
+substrings callers match on are the reference's (package/fable_attn/flash_attn_interface.py):
     flash_attn_func                  :378-388   flash_attn_qkvpacked_func        :391-401
     flash_attn_kvpacked_func         :404-414   flash_attn_varlen_func           :417-540
     flash_attn_varlen_qkvpacked_func :543-551   flash_attn_varlen_kvpacked_func  :554-564
     flash_attn_combine               :567-580   flash_attn_with_kvcache          :583-771
-Inputs are (batch, seqlen, nheads, headdim); the kernels take [B,H,S,D] strided views, so the
-wrapper only transposes views. There is no silent fallback: an unsupported configuration
-raises, and a missing library raises ImportError at import time.
+
+Structure. Every entry point first turns its arguments into one `_Spec`: the scalars the
+kernels take (scale, mask, softcap, alibi, dropout, chunk) plus the tensors at the width the
+kernels run (qv and a value head dim other than the score head dim become one widened
+problem; a head dim without a kernel is zero-padded to the next one), and how many value
+columns the caller gets back. Dense and packed variable-length batches then go through one
+autograd function, `_Attention`, which calls the forward once (with LSE) and the backward once
+for the whole batch. Decode builds the same `_Spec` and hands it to the paged kernel.
+Inputs are (batch, seqlen, nheads, headdim); the kernels take [B, H, S, D] strided views, so
+nothing is copied unless a row is misaligned. An unsupported configuration raises; a missing
+library raises ImportError at import time. Nothing falls back to another implementation.
 """
-import itertools
+import dataclasses
 import math
 import random
+from typing import Optional
 
 import torch
-import torch.nn.functional as F
 
 from . import _C
 
-# head_dims the kernels are instantiated for; others are zero-padded up to the next one
-# (zero columns change neither q.k nor the kept output columns).
+# head dims with kernels (fp16/bf16/fp32 forward, backward and decode); a head dim between
+# two of them runs in the next one with zero columns, which change neither q.k nor the kept
+# output columns
 KERNEL_HEAD_DIMS = (64, 128, 256)
 MAX_HEAD_DIM = KERNEL_HEAD_DIMS[-1]
+_DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
-def _kernel_dim(d):
-    for x in KERNEL_HEAD_DIMS:
-        if x >= d:
-            return x
-    return None
-
-
-def _pad_last(t, d):
-    return t if t.shape[-1] == d else F.pad(t, (0, d - t.shape[-1]))
-
-
+# ----------------------------------------------------------------------------- contract
 def _map_window(causal, window_size):
     """(causal, (left, right)) -> (causal_flag, win_left, win_right), reference :76-95.
     Key j is visible to query i when i+delta-left <= j <= i+delta+right (delta = SK-SQ); a
-    negative bound is absent; causal pins right to 0; the flag is set whenever right == 0."""
+    negative (or None) bound is absent; causal pins right to 0; the flag is set whenever
+    right == 0."""
     left, right = window_size
     wl = int(left) if left is not None and left >= 0 else -1
-    wr = int(right) if right is not None and right >= 0 else -1
-    if causal:
-        wr = 0
-    return (1 if wr == 0 else 0), wl, wr
+    wr = 0 if causal else (int(right) if right is not None and right >= 0 else -1)
+    return int(wr == 0), wl, wr
 
 
 def _reject_fp8(q_descale, k_descale, v_descale):
     """FP8 descaling is refused loudly (reference :99-107)."""
-    if q_descale is not None or k_descale is not None or v_descale is not None:
+    if any(x is not None for x in (q_descale, k_descale, v_descale)):
         raise NotImplementedError(
             "fable_attn: q_descale/k_descale/v_descale (FP8) are not supported; "
             "pass fp16 or bf16 tensors")
@@ -58,16 +57,15 @@ def _reject_fp8(q_descale, k_descale, v_descale):
 
 def _accept_hints(num_splits=None, pack_gqa=None, sm_margin=None):
     """Scheduling hints change the schedule, never the result; only their types are checked
-    (reference :110-128). num_splits is used by decode."""
-    if num_splits is not None and not isinstance(num_splits, int):
-        raise TypeError(f"fable_attn: num_splits must be int, got {type(num_splits)}")
-    if pack_gqa is not None and not isinstance(pack_gqa, bool):
-        raise TypeError(f"fable_attn: pack_gqa must be bool or None, got {type(pack_gqa)}")
-    if sm_margin is not None and not isinstance(sm_margin, int):
-        raise TypeError(f"fable_attn: sm_margin must be int, got {type(sm_margin)}")
+    (reference :110-128). num_splits is honoured by decode."""
+    for name, val, ok in (("num_splits", num_splits, int), ("pack_gqa", pack_gqa, bool),
+                          ("sm_margin", sm_margin, int)):
+        if val is not None and not isinstance(val, ok):
+            raise TypeError(f"fable_attn: {name} must be {ok.__name__} or None, got {type(val)}")
 
 
 def _check_chunk(attention_chunk):
+    """attention_chunk: None or a non-negative int (reference :131-137); 0 disables it."""
     if attention_chunk is None:
         return 0
     if not isinstance(attention_chunk, int) or attention_chunk < 0:
@@ -76,188 +74,206 @@ def _check_chunk(attention_chunk):
     return attention_chunk
 
 
-def _check_supported(q, k):
-    """Reference :140-156 (head count is axis 2 of the public layout)."""
-    if not q.is_cuda:
-        raise ValueError("fable_attn: tensors must be on the GPU (q.is_cuda == False)")
-    if q.shape[-1] > MAX_HEAD_DIM:
-        raise ValueError(f"fable_attn: head_dim={q.shape[-1]} exceeds the maximum {MAX_HEAD_DIM}")
-    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
-        raise ValueError(f"fable_attn: dtype {q.dtype} is not supported; use fp16, bf16 or fp32")
-    if q.shape[2] % k.shape[2] != 0:
-        raise ValueError(f"fable_attn: nheads_q={q.shape[2]} is not a multiple of "
-                         f"nheads_k={k.shape[2]} (GQA)")
+# ----------------------------------------------------------------------------- normalisation
+@dataclasses.dataclass
+class _Spec:
+    """One call after normalisation: tensors at kernel width and every kernel scalar."""
+    q: torch.Tensor
+    k: torch.Tensor
+    v: torch.Tensor
+    scale: float
+    causal: int
+    wl: int
+    wr: int
+    softcap: float
+    alibi: Optional[torch.Tensor]
+    dropout_p: float
+    chunk: int
+    keep: Optional[int]          # value columns returned to the caller (None: all)
+
+    def cut(self, out):
+        return out if self.keep is None else out[..., :self.keep]
 
 
-def _fuse_qv(q, k, v, qv):
-    """FA-3's qv term, S = q.k^T + qv.v^T, as one attention over concatenated head dims:
-    [q | qv] . [k | v]^T, values [v | 0]; the first dv output columns are P.V (reference
-    :160-191). Also covers headdim_v != headdim (qv = 0)."""
+def _kernel_width(d):
+    return next((w for w in KERNEL_HEAD_DIMS if w >= d), None)
+
+
+def _with_width(t, d):
+    """t with its last dim zero-extended to d (one allocation, autograd-aware)."""
+    if t.shape[-1] == d:
+        return t
+    return torch.nn.functional.pad(t, (0, d - t.shape[-1]))
+
+
+def _score_problem(q, k, v, qv):
+    """Reduce FA-3's qv term and a value head dim dv other than the score head dim d to one
+    attention whose q, k, v share a width, returning (q, k, v, value columns to keep):
+      * qv given: S = q.k^T + qv.v^T is one product over the concatenated width d + dv,
+        q' = [q | qv], k' = [k | v], and the values v' = [v | 0] leave P.V in the first dv
+        output columns (the reference builds the same operands, :160-191);
+      * dv != d without qv: S needs only q.k, so the narrower side is zero-extended to
+        max(d, dv) (the reference also widened this case to d + dv)."""
     d, dv = q.shape[-1], v.shape[-1]
+    if qv is None:
+        if dv == d:
+            return q, k, v, None
+        w = max(d, dv)
+        return _with_width(q, w), _with_width(k, w), _with_width(v, w), dv
+    if qv.shape[-1] != dv:
+        raise ValueError(f"fable_attn: qv.shape[-1]={qv.shape[-1]} must equal v.shape[-1]={dv}")
     if d + dv > MAX_HEAD_DIM:
         raise NotImplementedError(
-            f"fable_attn: qv / headdim_v needs a score head_dim of {d}+{dv}={d + dv}, "
+            f"fable_attn: qv needs a score head_dim of headdim+headdim_v = {d}+{dv} = {d + dv}, "
             f"above the kernel maximum {MAX_HEAD_DIM}")
-    if qv is None:
-        qv = q.new_zeros(q.shape[:-1] + (dv,))
-    elif qv.shape[-1] != dv:
-        raise ValueError(f"fable_attn: qv.shape[-1]={qv.shape[-1]} must equal v.shape[-1]={dv}")
-    qc = torch.cat([q, qv], dim=-1)
-    kc = torch.cat([k, v], dim=-1)
-    vc = torch.cat([v, torch.zeros_like(v[..., :d])], dim=-1) if d else v
-    return qc, kc, vc, dv
+    return (torch.cat([q, qv], -1), torch.cat([k, v], -1), _with_width(v, d + dv), dv)
 
 
-def _needs_qv_path(q, v, qv):
-    return qv is not None or v.shape[-1] != q.shape[-1]
+def _normalize(q, k, v, *, qv=None, softmax_scale=None, causal=False, window_size=(-1, -1),
+               softcap=0.0, alibi_slopes=None, dropout_p=0.0, attention_chunk=0,
+               descale=(None, None, None), hints=(None, None, None), head_axis=2):
+    """Validate the arguments (reference :99-156) and build the _Spec of a prefill call.
+    head_axis is the nheads axis of q/k (2 for (B,S,H,D), 1 for packed (total,H,D))."""
+    _reject_fp8(*descale)
+    _accept_hints(*hints)
+    chunk = _check_chunk(attention_chunk)
+    if not q.is_cuda:
+        raise ValueError("fable_attn: tensors must be on the GPU (q.is_cuda == False)")
+    if q.dtype not in _DTYPES:
+        raise ValueError(f"fable_attn: dtype {q.dtype} is not supported; use fp16, bf16 or fp32")
+    if q.shape[head_axis] % k.shape[head_axis]:
+        raise ValueError(f"fable_attn: nheads_q={q.shape[head_axis]} is not a multiple of "
+                         f"nheads_k={k.shape[head_axis]} (GQA)")
+    d, dv = q.shape[-1], v.shape[-1]
+    if softmax_scale is None:
+        # the reference scales by the concatenated width whenever qv or headdim_v != headdim
+        softmax_scale = (d + dv) ** -0.5 if (qv is not None or dv != d) else d ** -0.5
+    q, k, v, keep = _score_problem(q, k, v, qv)
+    w = _kernel_width(q.shape[-1])
+    if w is None:
+        raise ValueError(f"fable_attn: head_dim={q.shape[-1]} exceeds the maximum {MAX_HEAD_DIM}")
+    if w != q.shape[-1]:
+        keep = keep if keep is not None else v.shape[-1]
+        q, k, v = _with_width(q, w), _with_width(k, w), _with_width(v, w)
+    cflag, wl, wr = _map_window(causal, window_size)
+    alibi = alibi_slopes.to(torch.float32).contiguous() if alibi_slopes is not None else None
+    return _Spec(q, k, v, float(softmax_scale), cflag, wl, wr, float(softcap or 0.0), alibi,
+                 float(dropout_p), chunk, keep)
 
 
-def _kernel_view(t):
-    """(B,S,H,D) -> [B,H,S,D] view the kernels accept without a copy when rows are 16-byte
-    aligned; otherwise a contiguous copy."""
+def _bhsd(t):
+    """(B,S,H,D) -> the [B,H,S,D] view the kernels take; a copy only when a row is not 16-byte
+    aligned (the kernels move rows in 16-byte accesses)."""
     v = t.transpose(1, 2)
     el = v.element_size()
-    ok = (v.stride(-1) == 1 and v.data_ptr() % 16 == 0 and
-          all((s * el) % 16 == 0 for s in v.stride()[:-1]))
-    return v if ok else t.contiguous().transpose(1, 2)
+    aligned = (v.stride(-1) == 1 and v.data_ptr() % 16 == 0 and
+               all((s * el) % 16 == 0 for s in v.stride()[:-1]))
+    return v if aligned else t.contiguous().transpose(1, 2)
 
 
-class _FableAttnFn(torch.autograd.Function):
-    """Autograd over the forward/backward kernels (reference :233-262). deterministic is a
-    no-op: the backward is atomic-free and always bitwise reproducible."""
+
+# ----------------------------------------------------------------------------- autograd
+class _Attention(torch.autograd.Function):
+    """Forward (with LSE) and backward of one dense or packed variable-length batch, one
+    kernel launch sequence each way. `pack` is None for dense [B,H,S,D] views, else the tuple
+    (cu_q, cu_k, max_q, max_k, seqused_q, seqused_k) of a packed (total, H, D) batch.
+    `deterministic` needs no switch: the backward is atomic-free and always reproducible."""
 
     @staticmethod
-    def forward(ctx, q, k, v, scale, causal, wl, wr, softcap, alibi, dropout_p, deterministic,
-                attn_chunk, out_buf):
-        seed = random.getrandbits(63) if dropout_p > 0 else 0
-        out, lse = _C.fwd(q, k, v, float(scale), bool(causal), int(wl), int(wr), float(softcap),
-                          alibi, float(dropout_p), int(seed), int(attn_chunk), out_buf)
-        ctx.save_for_backward(q, k, v, out, lse, alibi if alibi is not None else torch.empty(0))
-        ctx.scale, ctx.causal, ctx.wl, ctx.wr, ctx.softcap = scale, causal, wl, wr, softcap
-        ctx.dropout_p, ctx.seed, ctx.has_alibi, ctx.attn_chunk = dropout_p, seed, alibi is not None, attn_chunk
+    def forward(ctx, spec, pack, q, k, v):
+        seed = random.getrandbits(63) if spec.dropout_p > 0 else 0
+        args = (spec.scale, bool(spec.causal), spec.wl, spec.wr, spec.softcap, spec.alibi,
+                spec.dropout_p, seed)
+        if pack is None:
+            B, H, S, D = q.shape
+            buf = torch.empty((B, S, H, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+            out, lse = _C.fwd(q, k, v, *args, spec.chunk, buf)
+        else:
+            cu_q, cu_k, mq, mk, su_q, su_k = pack
+            out, lse = _C.fwd_varlen(q, k, v, cu_q, cu_k, mq, mk, *args, spec.chunk, su_q, su_k,
+                                     return_lse=True)
+        # (the scalars only: the spec's own tensors are this node's inputs)
+        ctx.spec = dataclasses.replace(spec, q=None, k=None, v=None)
+        ctx.pack, ctx.seed = pack, seed
+        ctx.save_for_backward(q, k, v, out, lse)
+        ctx.mark_non_differentiable(lse)
         return out, lse
 
     @staticmethod
-    def backward(ctx, dout, dlse):
-        if ctx.attn_chunk:
+    def backward(ctx, dout, _dlse):
+        spec, pack = ctx.spec, ctx.pack
+        if spec.chunk:
             raise NotImplementedError(
                 "fable_attn: backward with attention_chunk is not supported (as in FA-3); "
                 "run the chunked forward under torch.no_grad()")
-        q, k, v, out, lse, alibi = ctx.saved_tensors
-        dq, dk, dv = _C.bwd(_kernel_view(dout.transpose(1, 2)), q, k, v, out, lse,
-                            float(ctx.scale), bool(ctx.causal), int(ctx.wl), int(ctx.wr),
-                            float(ctx.softcap), alibi if ctx.has_alibi else None,
-                            float(ctx.dropout_p), int(ctx.seed))
-        return dq, dk, dv, None, None, None, None, None, None, None, None, None, None
+        q, k, v, out, lse = ctx.saved_tensors
+        args = (spec.scale, bool(spec.causal), spec.wl, spec.wr, spec.softcap, spec.alibi,
+                spec.dropout_p, ctx.seed)
+        if pack is None:
+            dq, dk, dv = _C.bwd(_bhsd(dout.transpose(1, 2)), q, k, v, out, lse, *args)
+        else:
+            cu_q, cu_k, mq, mk, su_q, su_k = pack
+            dq, dk, dv = _C.bwd_varlen(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, mq, mk,
+                                       *args, su_q, su_k)
+        return None, None, dq, dk, dv
 
 
-class _FableVarlenFn(torch.autograd.Function):
-    """Autograd over the packed variable-length kernels: one forward launch (with LSE) and one
-    launch of each backward kernel for all sequences. The reference has no native varlen
-    backward and differentiates a per-sequence Python loop (:523-540)."""
-
-    @staticmethod
-    def forward(ctx, q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, wl, wr, softcap, alibi,
-                dropout_p, attn_chunk, su_q, su_k):
-        seed = random.getrandbits(63) if dropout_p > 0 else 0
-        out, lse = _C.fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, float(scale), bool(causal),
-                                 int(wl), int(wr), float(softcap), alibi, float(dropout_p),
-                                 int(seed), int(attn_chunk), su_q, su_k, return_lse=True)
-        empty = torch.empty(0, device=q.device)
-        ctx.save_for_backward(q, k, v, out, lse, cu_q, cu_k,
-                              alibi if alibi is not None else empty,
-                              su_q if su_q is not None else empty,
-                              su_k if su_k is not None else empty)
-        ctx.args = (max_sq, max_sk, scale, causal, wl, wr, softcap, dropout_p, seed, attn_chunk,
-                    alibi is not None, su_q is not None, su_k is not None)
-        return out
-
-    @staticmethod
-    def backward(ctx, dout):
-        (max_sq, max_sk, scale, causal, wl, wr, softcap, dropout_p, seed, attn_chunk,
-         has_alibi, has_suq, has_suk) = ctx.args
-        if attn_chunk:
-            raise NotImplementedError(
-                "fable_attn: backward with attention_chunk is not supported (as in FA-3); "
-                "run the chunked forward under torch.no_grad()")
-        q, k, v, out, lse, cu_q, cu_k, alibi, su_q, su_k = ctx.saved_tensors
-        dq, dk, dv = _C.bwd_varlen(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, max_sq,
-                                   max_sk, float(scale), bool(causal), int(wl), int(wr),
-                                   float(softcap), alibi if has_alibi else None,
-                                   float(dropout_p), int(seed),
-                                   su_q if has_suq else None, su_k if has_suk else None)
-        return (dq, dk, dv) + (None,) * 14
-
-
-def _attn_probs(q, k, lse, scale, causal, wl, wr, softcap, alibi, attn_chunk):
-    """Debug path for return_attn_probs: the full [B,Hq,SQ,SK] probability matrix from the
-    kernel's LSE, p = exp(s - lse) (reference :266-308). Materialises S x S."""
-    B, Hq, SQ, D = q.shape
-    Hk, SK = k.shape[1], k.shape[2]
-    need = B * Hq * SQ * SK * 4
-    free = torch.cuda.mem_get_info(q.device)[0]
-    if need > free * 0.8:
+# ----------------------------------------------------------------------------- debug output
+def _probabilities(spec, q, k, lse, delta):
+    """The softmax matrix P = exp(logit - lse) of one [H, SQ, D] / [Hk, SK, D] problem, masked
+    to 0 outside the visible keys: the return_attn_probs debug output, which materialises the
+    SQ x SK matrix the kernels never form (it refuses above 80% of the free memory)."""
+    H, SQ, _ = q.shape
+    SK = k.shape[1]
+    need, free = H * SQ * SK * 4, torch.cuda.mem_get_info(q.device)[0]
+    if need > 0.8 * free:
         raise torch.cuda.OutOfMemoryError(
             f"fable_attn: return_attn_probs needs a {need / 2**30:.1f} GiB S x S matrix "
             f"({free / 2**30:.1f} GiB free); the kernel itself never materialises it")
-    kk = k if Hk == Hq else k.repeat_interleave(Hq // Hk, dim=1)
-    s = torch.matmul(q.float(), kk.float().transpose(-1, -2).contiguous())
-    s = softcap * torch.tanh(s * scale / softcap) if softcap and softcap > 0 else s * scale
-    delta = SK - SQ
-    qi = torch.arange(SQ, device=q.device).view(-1, 1)
-    ki = torch.arange(SK, device=q.device).view(1, -1)
-    if alibi is not None:
-        s = s + alibi.view(1, Hq, 1, 1).float() * (ki - qi).float()
-    mask = torch.zeros(SQ, SK, device=q.device, dtype=torch.bool)
-    if causal:
-        mask |= ki > qi + delta
-    if wl >= 0:
-        mask |= ki < qi + delta - wl
-    if wr >= 0:
-        mask |= ki > qi + delta + wr
-    if attn_chunk:
-        cs = ((qi + delta).clamp_min(0) // attn_chunk) * attn_chunk
-        mask |= (ki < cs) | (ki >= cs + attn_chunk)
-    p = torch.exp(s - lse.unsqueeze(-1))
-    return p.masked_fill(mask, 0.0)
+    kk = k.float().repeat_interleave(H // k.shape[0], dim=0)
+    s = torch.matmul(q.float(), kk.transpose(1, 2).contiguous()) * spec.scale
+    if spec.softcap > 0:
+        s = spec.softcap * torch.tanh(s / spec.softcap)
+    i = torch.arange(SQ, device=q.device)[:, None] + delta     # query position in key space
+    j = torch.arange(SK, device=q.device)[None, :]
+    if spec.alibi is not None:
+        s = s + spec.alibi.view(H, 1, 1) * (j - (i - delta)).float()
+    hidden = torch.zeros(SQ, SK, dtype=torch.bool, device=q.device)
+    if spec.causal:
+        hidden |= j > i
+    if spec.wl >= 0:
+        hidden |= j < i - spec.wl
+    if spec.wr >= 0:
+        hidden |= j > i + spec.wr
+    if spec.chunk:
+        start = i.clamp_min(0) // spec.chunk * spec.chunk
+        hidden |= (j < start) | (j >= start + spec.chunk)
+    return torch.exp(s - lse[..., None]).masked_fill(hidden, 0.0)
 
 
-def _fwd_bshd(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap, alibi_slopes,
-              deterministic, return_attn_probs, qv, attention_chunk,
-              q_descale, k_descale, v_descale, num_splits, pack_gqa, sm_margin):
-    """Shared body of flash_attn_func and the packed wrappers, input (B,S,H,D)
-    (reference :312-374)."""
-    _reject_fp8(q_descale, k_descale, v_descale)
-    _accept_hints(num_splits, pack_gqa, sm_margin)
-    chunk = _check_chunk(attention_chunk)
-    dv_out = None
-    if _needs_qv_path(q, v, qv):
-        if softmax_scale is None:
-            softmax_scale = (q.shape[-1] + v.shape[-1]) ** (-0.5)
-        q, k, v, dv_out = _fuse_qv(q, k, v, qv)
-    elif softmax_scale is None:
-        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
-    _check_supported(q, k)
-    cflag, wl, wr = _map_window(causal, window_size)
-    d_real = q.shape[-1]
-    d_ker = _kernel_dim(d_real)
-    if d_ker != d_real:
-        q, k, v = _pad_last(q, d_ker), _pad_last(k, d_ker), _pad_last(v, d_ker)
-        if dv_out is None:
-            dv_out = d_real
-    B, SQ, Hq, D = q.shape
-    qh, kh, vh = _kernel_view(q), _kernel_view(k), _kernel_view(v)
-    out_buf = torch.empty((B, SQ, Hq, D), dtype=q.dtype, device=q.device).transpose(1, 2)
-    al = alibi_slopes.float().contiguous() if alibi_slopes is not None else None
-    out, lse = _FableAttnFn.apply(qh, kh, vh, softmax_scale, cflag, wl, wr, softcap, al,
-                                  dropout_p, deterministic, chunk, out_buf)
+# ----------------------------------------------------------------------------- prefill
+def _dense(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap, alibi_slopes,
+           deterministic, return_attn_probs, qv, attention_chunk, q_descale, k_descale,
+           v_descale, num_splits, pack_gqa, sm_margin):
+    """Shared body of flash_attn_func and its packed variants; (B,S,H,D) in and out."""
+    del deterministic
+    spec = _normalize(q, k, v, qv=qv, softmax_scale=softmax_scale, causal=causal,
+                      window_size=window_size, softcap=softcap, alibi_slopes=alibi_slopes,
+                      dropout_p=dropout_p, attention_chunk=attention_chunk,
+                      descale=(q_descale, k_descale, v_descale),
+                      hints=(num_splits, pack_gqa, sm_margin))
+    qh, kh, vh = _bhsd(spec.q), _bhsd(spec.k), _bhsd(spec.v)
+    out, lse = _Attention.apply(spec, None, qh, kh, vh)
     res = out.transpose(1, 2)
-    if dv_out is not None:
-        res = res[..., :dv_out].contiguous()
-    if return_attn_probs:
-        probs = _attn_probs(qh, kh, lse, softmax_scale, bool(cflag), wl, wr, softcap, al, chunk)
-        return res, lse, probs
-    return res
+    if spec.keep is not None:
+        res = res[..., :spec.keep].contiguous()
+    if not return_attn_probs:
+        return res
+    with torch.no_grad():
+        delta = kh.shape[2] - qh.shape[2]
+        probs = torch.stack([_probabilities(spec, qh[b], kh[b], lse[b], delta)
+                             for b in range(qh.shape[0])])
+    return res, lse, probs
 
 
 def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
@@ -268,9 +284,9 @@ def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
                     num_splits=1, pack_gqa=None, sm_margin=0):
     """q, k, v: (batch, seqlen, nheads, headdim). Returns out in the same layout (dense), or
     (out, softmax_lse, S_dmask) when return_attn_probs=True."""
-    return _fwd_bshd(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap,
-                     alibi_slopes, deterministic, return_attn_probs, qv, attention_chunk,
-                     q_descale, k_descale, v_descale, num_splits, pack_gqa, sm_margin)
+    return _dense(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap, alibi_slopes,
+                  deterministic, return_attn_probs, qv, attention_chunk, q_descale, k_descale,
+                  v_descale, num_splits, pack_gqa, sm_margin)
 
 
 def flash_attn_qkvpacked_func(qkv, dropout_p=0.0, softmax_scale=None, causal=False,
@@ -280,10 +296,10 @@ def flash_attn_qkvpacked_func(qkv, dropout_p=0.0, softmax_scale=None, causal=Fal
                               q_descale=None, k_descale=None, v_descale=None,
                               num_splits=1, pack_gqa=None, sm_margin=0):
     """qkv: (batch, seqlen, 3, nheads, headdim)."""
-    return _fwd_bshd(qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2], dropout_p, softmax_scale, causal,
-                     window_size, softcap, alibi_slopes, deterministic, return_attn_probs, qv,
-                     attention_chunk, q_descale, k_descale, v_descale, num_splits, pack_gqa,
-                     sm_margin)
+    q, k, v = qkv.unbind(2)
+    return _dense(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap, alibi_slopes,
+                  deterministic, return_attn_probs, qv, attention_chunk, q_descale, k_descale,
+                  v_descale, num_splits, pack_gqa, sm_margin)
 
 
 def flash_attn_kvpacked_func(q, kv, dropout_p=0.0, softmax_scale=None, causal=False,
@@ -293,33 +309,36 @@ def flash_attn_kvpacked_func(q, kv, dropout_p=0.0, softmax_scale=None, causal=Fa
                              q_descale=None, k_descale=None, v_descale=None,
                              num_splits=1, pack_gqa=None, sm_margin=0):
     """q: (batch, sq, nheads, d); kv: (batch, sk, 2, nheads_k, d)."""
-    return _fwd_bshd(q, kv[:, :, 0], kv[:, :, 1], dropout_p, softmax_scale, causal, window_size,
-                     softcap, alibi_slopes, deterministic, return_attn_probs, qv,
-                     attention_chunk, q_descale, k_descale, v_descale, num_splits, pack_gqa,
-                     sm_margin)
+    k, v = kv.unbind(2)
+    return _dense(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap, alibi_slopes,
+                  deterministic, return_attn_probs, qv, attention_chunk, q_descale, k_descale,
+                  v_descale, num_splits, pack_gqa, sm_margin)
 
 
-def _unpage_varlen_kv(k, v, block_table, cu_seqlens_k, seqused_k):
-    """Paged K/V for varlen prefill: gather each sequence's pages into a packed (total, H, D)
-    layout (reference :438-469)."""
-    if k.dim() != 4 or v.dim() != 4:
+def _as_index(t, device):
+    return t.to(device=device, dtype=torch.int32).contiguous()
+
+
+def _pages_as_packed(k_cache, v_cache, block_table, cu_seqlens_k, seqused_k):
+    """Paged K/V of a varlen prefill as a packed batch without a host round trip: every
+    sequence's block-table row is gathered whole (max_blocks * page rows per sequence, one
+    device gather), so sequence b starts at row b * max_blocks * page, and its true length
+    becomes seqused_k. Returns (k, v, cu_k, seqused_k, max_seqlen_k)."""
+    if k_cache.dim() != 4 or v_cache.dim() != 4:
         raise ValueError(
             "fable_attn: with block_table, k and v must be paged "
-            f"(num_blocks, page_block_size, nheads_k, headdim); got k.shape={tuple(k.shape)}")
-    bt = block_table.to(torch.int32)
-    if bt.dim() != 2 or bt.shape[0] != cu_seqlens_k.numel() - 1:
+            f"(num_blocks, page_block_size, nheads_k, headdim); got k.shape={tuple(k_cache.shape)}")
+    nseq = cu_seqlens_k.numel() - 1
+    if block_table.dim() != 2 or block_table.shape[0] != nseq:
         raise ValueError(f"fable_attn: block_table must be (batch, max_blocks), got "
-                         f"{tuple(bt.shape)} for batch={cu_seqlens_k.numel() - 1}")
-    page = k.shape[1]
-    lens = ((cu_seqlens_k[1:] - cu_seqlens_k[:-1]) if seqused_k is None else seqused_k).tolist()
-    ks, vs = [], []
-    for i, L in enumerate(int(x) for x in lens):
-        idx = bt[i, :(L + page - 1) // page].long()
-        ks.append(k[idx].reshape(-1, k.shape[2], k.shape[3])[:L])
-        vs.append(v[idx].reshape(-1, v.shape[2], v.shape[3])[:L])
-    cu = torch.tensor([0] + list(itertools.accumulate(int(x) for x in lens)),
-                      device=k.device, dtype=torch.int32)
-    return torch.cat(ks, 0).contiguous(), torch.cat(vs, 0).contiguous(), cu
+                         f"{tuple(block_table.shape)} for batch={nseq}")
+    dev = k_cache.device
+    bt = block_table.to(device=dev, dtype=torch.long)
+    span = bt.shape[1] * k_cache.shape[1]
+    flat = lambda c: c[bt.reshape(-1)].reshape(nseq * span, c.shape[2], c.shape[3])
+    cu = torch.arange(nseq + 1, device=dev, dtype=torch.int32) * span
+    used = seqused_k if seqused_k is not None else cu_seqlens_k[1:] - cu_seqlens_k[:-1]
+    return flat(k_cache), flat(v_cache), cu, _as_index(used, dev), span
 
 
 def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
@@ -332,74 +351,44 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
                            num_splits=1, pack_gqa=None, sm_margin=0,
                            block_table=None):
     """Packed variable-length sequences: q (total_q, nheads, d), k/v (total_k, nheads_k, d),
-    cu_seqlens_* int32 (batch+1). One forward launch over all sequences; with grad the
-    backward is one launch of each backward kernel over all sequences as well (the reference
-    loops over the sequences in Python on the grad path, :523-540)."""
-    _reject_fp8(q_descale, k_descale, v_descale)
-    _accept_hints(num_splits, pack_gqa, sm_margin)
-    chunk = _check_chunk(attention_chunk)
-    if block_table is not None:
-        k, v, cu_seqlens_k = _unpage_varlen_kv(k, v, block_table, cu_seqlens_k, seqused_k)
-        seqused_k = None
-    dv_out = None
-    if _needs_qv_path(q, v, qv):
-        if softmax_scale is None:
-            softmax_scale = (q.shape[-1] + v.shape[-1]) ** (-0.5)
-        q, k, v, dv_out = _fuse_qv(q, k, v, qv)
-    elif softmax_scale is None:
-        softmax_scale = 1.0 / math.sqrt(q.shape[-1])
-    need_grad = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad)
+    cu_seqlens_* int32 (batch+1). One forward launch over all sequences and, with grad, one
+    launch of each backward kernel (the reference loops over the sequences in Python on the
+    grad path, :523-540). With return_attn_probs: (out, [lse per sequence], [P per sequence])."""
+    del deterministic
     if q.dim() != 3:
         raise ValueError(f"fable_attn: varlen expects (total, nheads, headdim), got {tuple(q.shape)}")
-    if q.shape[-1] > MAX_HEAD_DIM:
-        raise ValueError(f"fable_attn: head_dim={q.shape[-1]} exceeds the maximum {MAX_HEAD_DIM}")
-    if not q.is_cuda:
-        raise ValueError("fable_attn: tensors must be on the GPU (q.is_cuda == False)")
-    if q.shape[1] % k.shape[1] != 0:
-        raise ValueError(f"fable_attn: GQA needs nheads_q ({q.shape[1]}) divisible by nheads_k ({k.shape[1]})")
-    d_real = q.shape[-1]
-    d_ker = _kernel_dim(d_real)
-    if d_ker != d_real:
-        q, k, v = _pad_last(q, d_ker), _pad_last(k, d_ker), _pad_last(v, d_ker)
-        if dv_out is None:
-            dv_out = d_real
-    cflag, wl, wr = _map_window(causal, window_size)
-    al = alibi_slopes.float().contiguous() if alibi_slopes is not None else None
-    su_q = seqused_q.to(torch.int32).contiguous() if seqused_q is not None else None
-    su_k = seqused_k.to(torch.int32).contiguous() if seqused_k is not None else None
-    cu_q = cu_seqlens_q.to(torch.int32).contiguous()
-    cu_k = cu_seqlens_k.to(torch.int32).contiguous()
-    if need_grad:
-        out = _FableVarlenFn.apply(q.contiguous(), k.contiguous(), v.contiguous(), cu_q, cu_k,
-                                   int(max_seqlen_q), int(max_seqlen_k), float(softmax_scale),
-                                   bool(cflag), int(wl), int(wr), float(softcap), al,
-                                   float(dropout_p), int(chunk), su_q, su_k)
-    else:
-        seed = random.getrandbits(63) if dropout_p > 0 else 0
-        out = _C.fwd_varlen(q.contiguous(), k.contiguous(), v.contiguous(), cu_q, cu_k,
-                            int(max_seqlen_q), int(max_seqlen_k), float(softmax_scale),
-                            bool(cflag), int(wl), int(wr), float(softcap), al, float(dropout_p),
-                            int(seed), int(chunk), su_q, su_k)
-    if dv_out is not None:
-        out = out[..., :dv_out]
-    if return_attn_probs:
-        lse_l, probs_l = [], []
-        with torch.no_grad():
-            for i in range(cu_seqlens_q.numel() - 1):
-                a, b = int(cu_seqlens_q[i]), int(cu_seqlens_q[i + 1])
-                c, d = int(cu_seqlens_k[i]), int(cu_seqlens_k[i + 1])
-                if seqused_q is not None:
-                    b = a + int(seqused_q[i])
-                if seqused_k is not None:
-                    d = c + int(seqused_k[i])
-                _, li, pi = flash_attn_func(q[a:b].unsqueeze(0), k[c:d].unsqueeze(0),
-                                            v[c:d].unsqueeze(0), dropout_p, softmax_scale,
-                                            causal, window_size, softcap, alibi_slopes,
-                                            deterministic, True, attention_chunk=chunk)
-                lse_l.append(li.squeeze(0))
-                probs_l.append(pi.squeeze(0))
-        return out, lse_l, probs_l
-    return out
+    if block_table is not None:
+        k, v, cu_seqlens_k, seqused_k, max_seqlen_k = _pages_as_packed(
+            k, v, block_table, cu_seqlens_k, seqused_k)
+    spec = _normalize(q, k, v, qv=qv, softmax_scale=softmax_scale, causal=causal,
+                      window_size=window_size, softcap=softcap, alibi_slopes=alibi_slopes,
+                      dropout_p=dropout_p, attention_chunk=attention_chunk,
+                      descale=(q_descale, k_descale, v_descale),
+                      hints=(num_splits, pack_gqa, sm_margin), head_axis=1)
+    dev = spec.q.device
+    pack = (_as_index(cu_seqlens_q, dev), _as_index(cu_seqlens_k, dev), int(max_seqlen_q),
+            int(max_seqlen_k), _as_index(seqused_q, dev) if seqused_q is not None else None,
+            _as_index(seqused_k, dev) if seqused_k is not None else None)
+    out, lse = _Attention.apply(spec, pack, spec.q.contiguous(), spec.k.contiguous(),
+                                spec.v.contiguous())
+    out = spec.cut(out)
+    if not return_attn_probs:
+        return out
+    # debug path: one probability matrix per sequence (ragged shapes), host lengths needed
+    cq, ck = pack[0].tolist(), pack[1].tolist()
+    uq = pack[4].tolist() if pack[4] is not None else None
+    uk = pack[5].tolist() if pack[5] is not None else None
+    lses, probs = [], []
+    with torch.no_grad():
+        for z in range(len(cq) - 1):
+            nq = uq[z] if uq is not None else cq[z + 1] - cq[z]
+            nk = uk[z] if uk is not None else ck[z + 1] - ck[z]
+            qz = spec.q[cq[z]:cq[z] + nq].transpose(0, 1)
+            kz = spec.k[ck[z]:ck[z] + nk].transpose(0, 1)
+            lz = lse[:, cq[z]:cq[z] + nq]
+            lses.append(lz)
+            probs.append(_probabilities(spec, qz, kz, lz, nk - nq))
+    return out, lses, probs
 
 
 def flash_attn_varlen_qkvpacked_func(qkv, cu_seqlens, max_seqlen, dropout_p=0.0,
@@ -407,10 +396,10 @@ def flash_attn_varlen_qkvpacked_func(qkv, cu_seqlens, max_seqlen, dropout_p=0.0,
                                      softcap=0.0, alibi_slopes=None, deterministic=False,
                                      return_attn_probs=False, **kw):
     """qkv: (total_tokens, 3, nheads, headdim)."""
-    return flash_attn_varlen_func(qkv[:, 0], qkv[:, 1], qkv[:, 2], cu_seqlens, cu_seqlens,
-                                  max_seqlen, max_seqlen, dropout_p, softmax_scale, causal,
-                                  window_size, softcap, alibi_slopes, deterministic,
-                                  return_attn_probs, **kw)
+    q, k, v = qkv.unbind(1)
+    return flash_attn_varlen_func(q, k, v, cu_seqlens, cu_seqlens, max_seqlen, max_seqlen,
+                                  dropout_p, softmax_scale, causal, window_size, softcap,
+                                  alibi_slopes, deterministic, return_attn_probs, **kw)
 
 
 def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
@@ -419,20 +408,48 @@ def flash_attn_varlen_kvpacked_func(q, kv, cu_seqlens_q, cu_seqlens_k, max_seqle
                                     alibi_slopes=None, deterministic=False,
                                     return_attn_probs=False, **kw):
     """q: (total_q, nheads, d); kv: (total_k, 2, nheads_k, d)."""
-    return flash_attn_varlen_func(q, kv[:, 0], kv[:, 1], cu_seqlens_q, cu_seqlens_k,
-                                  max_seqlen_q, max_seqlen_k, dropout_p, softmax_scale, causal,
-                                  window_size, softcap, alibi_slopes, deterministic,
-                                  return_attn_probs, **kw)
+    k, v = kv.unbind(1)
+    return flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q,
+                                  max_seqlen_k, dropout_p, softmax_scale, causal, window_size,
+                                  softcap, alibi_slopes, deterministic, return_attn_probs, **kw)
 
 
 def flash_attn_combine(out_partial, lse_partial, out=None, out_dtype=None):
     """Merge split-KV partials: out_partial (nsplit, B, S, H, D), lse_partial (nsplit, B, H, S)
     natural-log LSE -> (B, S, H, D). One HIP kernel (the reference used torch ops, :567-580)."""
     res = _C.combine(out_partial, lse_partial, out_dtype or out_partial.dtype)
-    if out is not None:
-        out.copy_(res)
-        return out
-    return res
+    if out is None:
+        return res
+    out.copy_(res)
+    return out
+
+
+# ----------------------------------------------------------------------------- decode
+def _cache_rows(q, k_cache, cache_seqlens, cache_batch_idx, block_table):
+    """(block_table, page, cache lengths) for the paged kernel: a paged cache keeps its table; a
+    dense (batch, seqlen, ...) cache is a paged one with one page per row (cache_batch_idx picks
+    the rows), which needs a power-of-two seqlen."""
+    B, dev = q.shape[0], q.device
+    if block_table is not None:
+        if cache_batch_idx is not None:
+            raise ValueError("fable_attn: cache_batch_idx applies to a dense cache only; with a "
+                             "paged cache the block_table selects the rows")
+        table, page = _as_index(block_table, dev), k_cache.shape[1]
+    else:
+        page = k_cache.shape[1]
+        if page & (page - 1):
+            raise NotImplementedError(
+                f"fable_attn: dense cache length {page} must be a power of two (or pass block_table)")
+        rows = (cache_batch_idx if cache_batch_idx is not None
+                else torch.arange(B, device=dev))
+        table = _as_index(rows, dev).view(B, 1)
+    if cache_seqlens is None:
+        lens = torch.full((B,), k_cache.shape[1], dtype=torch.int32, device=dev)
+    elif isinstance(cache_seqlens, int):
+        lens = torch.full((B,), cache_seqlens, dtype=torch.int32, device=dev)
+    else:
+        lens = _as_index(cache_seqlens, dev)
+    return table, page, lens
 
 
 @torch.no_grad()
@@ -449,134 +466,127 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None,
                             rotary_seqlens=None):
     """Decode against a paged (k_cache/v_cache (num_blocks, page, nheads_k, d) + block_table)
     or dense ((batch, seqlen, nheads_k, d)) KV cache; split-KV kernels with an LSE combine.
-    q: (batch, seqlen_q, nheads, d); the new tokens sit at cache_seqlens .. +seqlen_q-1 and are
-    causal among themselves. cache_seqlens is the length before appending k/v. Returns out, or
+    q: (batch, seqlen_q, nheads, d), or packed (total_q, nheads, d) with cu_seqlens_q; new
+    token t of sequence b sits at cache_seqlens[b] + t. Without k/v every new token sees the
+    cached keys [0, cache_seqlens[b]); k/v (batch, seqlen_q, nheads_k, d) are written into
+    the cache first, and then token t also sees the new keys up to its own. Returns out, or
     (out, softmax_lse (batch, nheads, seqlen_q)). Reference :583-771."""
     _reject_fp8(q_descale, k_descale, v_descale)
     _accept_hints(num_splits, pack_gqa, sm_margin)
-    if q.dim() != 4:
-        raise ValueError(f"fable_attn: decode expects q (batch, seqlen_q, nheads, headdim), "
-                         f"got {tuple(q.shape)}")
-    if softmax_scale is None:
-        softmax_scale = (q.shape[-1] + (qv.shape[-1] if qv is not None else 0)) ** -0.5
-    del scheduler_metadata  # a precomputed schedule is not needed: the launcher plans per call
+    del scheduler_metadata      # the launcher plans each call itself (fa_decode_num_splits)
     if cu_seqlens_k_new is not None:
         raise NotImplementedError(
             "fable_attn: cu_seqlens_k_new (ragged append) is not supported; append the same "
             "number of tokens to every batch element")
-    if cu_seqlens_q is not None:
-        cu = cu_seqlens_q.to(torch.int32).cpu()
-        outs, lses = [], []
-        for i in range(cu.numel() - 1):
-            a, b = int(cu[i]), int(cu[i + 1])
-            qi = q[a:b].unsqueeze(0) if q.dim() == 3 else q[:, a:b]
-            csi = cache_seqlens[i:i + 1] if torch.is_tensor(cache_seqlens) else cache_seqlens
-            r = flash_attn_with_kvcache(
-                qi, k_cache, v_cache, k=k, v=v, qv=qv, rotary_cos=rotary_cos,
-                rotary_sin=rotary_sin, cache_seqlens=csi, cache_batch_idx=cache_batch_idx,
-                cache_leftpad=cache_leftpad, block_table=block_table,
-                softmax_scale=softmax_scale, causal=causal, window_size=window_size,
-                softcap=softcap, rotary_interleaved=rotary_interleaved,
-                alibi_slopes=alibi_slopes, num_splits=num_splits,
-                return_softmax_lse=return_softmax_lse, page_table=page_table,
-                attention_chunk=attention_chunk, pack_gqa=pack_gqa, sm_margin=sm_margin,
-                rotary_seqlens=rotary_seqlens)
-            if return_softmax_lse:
-                outs.append(r[0].squeeze(0))
-                lses.append(r[1])
-            else:
-                outs.append(r.squeeze(0))
-        out = torch.cat(outs, dim=0)
-        return (out, torch.cat(lses, dim=0)) if return_softmax_lse else out
     if page_table is not None:
         if block_table is not None:
             raise ValueError("fable_attn: block_table and page_table are the same argument; pass one")
         block_table = page_table
-    B, NQ = q.shape[0], q.shape[1]
-    dev = q.device
-    d_real = q.shape[-1]
+    if (k is None) != (v is None):
+        raise ValueError("fable_attn: k and v are appended to the cache together")
+    if cu_seqlens_q is not None:
+        return _kvcache_packed_q(q, k_cache, v_cache, k, qv, cu_seqlens_q, max_seqlen_q,
+                                 return_softmax_lse, rotary_cos=rotary_cos,
+                                 rotary_sin=rotary_sin, cache_seqlens=cache_seqlens,
+                                 cache_batch_idx=cache_batch_idx, cache_leftpad=cache_leftpad,
+                                 block_table=block_table, softmax_scale=softmax_scale,
+                                 causal=causal, window_size=window_size, softcap=softcap,
+                                 rotary_interleaved=rotary_interleaved,
+                                 alibi_slopes=alibi_slopes, num_splits=num_splits,
+                                 attention_chunk=attention_chunk, rotary_seqlens=rotary_seqlens)
+    if q.dim() != 4:
+        raise ValueError(f"fable_attn: decode expects q (batch, seqlen_q, nheads, headdim), "
+                         f"got {tuple(q.shape)}")
     if not q.is_cuda:
         raise ValueError("fable_attn: tensors must be on the GPU (q.is_cuda == False)")
-    if q.dtype not in (torch.float16, torch.bfloat16, torch.float32):
+    if q.dtype not in _DTYPES:
         raise ValueError(f"fable_attn: dtype {q.dtype} is not supported; use fp16, bf16 or fp32")
-    if qv is not None:
-        # same concatenation as the prefill qv path, applied to the whole cache (compat path)
-        if qv.shape[-1] != v_cache.shape[-1]:
-            raise ValueError("fable_attn: qv.shape[-1] must equal the value head_dim")
-        if d_real + qv.shape[-1] > MAX_HEAD_DIM:
-            raise NotImplementedError(f"fable_attn: qv in decode needs headdim+headdim_v <= {MAX_HEAD_DIM}")
-        q = torch.cat([q, qv], dim=-1)
-        k_cache = torch.cat([k_cache, v_cache], dim=-1)
-        v_cache = torch.cat([v_cache, torch.zeros_like(v_cache[..., :d_real])], dim=-1)
-        if k is not None:
-            k = torch.cat([k, v], dim=-1)
-            v = torch.cat([v, torch.zeros_like(v[..., :d_real])], dim=-1)
-    if cache_seqlens is None:
-        seqlens = torch.full((B,), k_cache.shape[1], dtype=torch.int32, device=dev)
-    elif isinstance(cache_seqlens, int):
-        seqlens = torch.full((B,), cache_seqlens, dtype=torch.int32, device=dev)
-    else:
-        seqlens = cache_seqlens.to(device=dev, dtype=torch.int32).contiguous()
-    if block_table is None:
-        # dense cache: one block per batch row, page = the whole row
-        page = k_cache.shape[1]
-        if page & (page - 1):
+    if softmax_scale is None:
+        softmax_scale = (q.shape[-1] + (qv.shape[-1] if qv is not None else 0)) ** -0.5
+    appending = k is not None
+    if appending and (qv is not None or not (k_cache.is_contiguous() and v_cache.is_contiguous())):
+        raise NotImplementedError(
+            "fable_attn: appending k/v needs the kernel to write the caller's cache in place: "
+            "not possible with qv (the cache is widened into a temporary) or with a "
+            "non-contiguous cache")
+    NQ = q.shape[1]
+    table, page, lens = _cache_rows(q, k_cache, cache_seqlens, cache_batch_idx, block_table)
+    kc, vc, keep = k_cache, v_cache, None
+    if qv is not None or v_cache.shape[-1] != k_cache.shape[-1]:
+        # compat path: the score problem widened over the whole cache (one temporary copy)
+        q, kc, vc, keep = _score_problem(q, k_cache, v_cache, qv)
+    w = _kernel_width(q.shape[-1])
+    if w is None:
+        raise ValueError(f"fable_attn: head_dim={q.shape[-1]} exceeds the maximum {MAX_HEAD_DIM}")
+    if w != q.shape[-1]:
+        if appending:
             raise NotImplementedError(
-                f"fable_attn: dense cache length {page} must be a power of two (or pass block_table)")
-        if cache_batch_idx is None:
-            bt = torch.arange(B, dtype=torch.int32, device=dev).view(B, 1)
-        else:
-            bt = cache_batch_idx.to(device=dev, dtype=torch.int32).contiguous().view(B, 1)
-    else:
-        if cache_batch_idx is not None:
-            raise ValueError("fable_attn: cache_batch_idx applies to a dense cache only; with a "
-                             "paged cache the block_table selects the rows")
-        bt = block_table.to(device=dev, dtype=torch.int32).contiguous()
-    kc, vc = k_cache, v_cache
-    # decode takes the window as "number of keys back from the query position"
+                f"fable_attn: appending k/v needs a kernel head_dim; {q.shape[-1]} is not one of "
+                f"{KERNEL_HEAD_DIMS}")
+        keep = keep if keep is not None else vc.shape[-1]
+        q, kc, vc = _with_width(q, w), _with_width(kc, w), _with_width(vc, w)
     _, wl, _ = _map_window(True, window_size)
-    win = (wl + 1) if wl >= 0 else -1
-    lp = cache_leftpad.to(device=dev, dtype=torch.int32).contiguous() if cache_leftpad is not None else None
+    keys_back = wl + 1 if 0 <= wl < 2 ** 31 - 1 else -1   # the kernel's window: keys up to the query
+    dev = q.device
+    leftpad = _as_index(cache_leftpad, dev) if cache_leftpad is not None else None
     chunk = _check_chunk(attention_chunk)
     if chunk:
         if NQ > 1:
             raise NotImplementedError(
                 "fable_attn: attention_chunk in decode is supported for one new token: "
                 "several tokens would need different chunk starts")
-        cl = ((seqlens.to(torch.int64) // chunk) * chunk).to(torch.int32)
-        lp = cl if lp is None else torch.maximum(lp, cl)
-    al = alibi_slopes.float().contiguous() if alibi_slopes is not None else None
-    cos = rotary_cos.float().contiguous() if rotary_cos is not None else None
-    sin = rotary_sin.float().contiguous() if rotary_sin is not None else None
-    rdim = int(cos.shape[-1] * 2) if cos is not None else 0
-    rpos = (rotary_seqlens.to(device=dev, dtype=torch.int32).contiguous()
-            if rotary_seqlens is not None else None)
-    nk = k.contiguous() if k is not None else None
-    nv = v.contiguous() if v is not None else None
-    if (nk is None) != (nv is None):
-        raise ValueError("fable_attn: k and v are appended to the cache together")
-    dq = q.shape[-1]
-    d_ker = _kernel_dim(dq)
-    if d_ker is None:
-        raise ValueError(f"fable_attn: head_dim={dq} exceeds the maximum {MAX_HEAD_DIM}")
-    dv_cut = None
-    if d_ker != dq:
-        if nk is not None:
-            raise NotImplementedError(
-                f"fable_attn: appending k/v needs a kernel head_dim; {dq} is not one of "
-                f"{KERNEL_HEAD_DIMS}")
-        q, kc, vc = _pad_last(q, d_ker), _pad_last(kc, d_ker), _pad_last(vc, d_ker)
-        dv_cut = dq
+        # the one new token sees its own chunk: keys from the chunk start, a left pad
+        start = (lens.to(torch.int64) // chunk * chunk).to(torch.int32)
+        leftpad = start if leftpad is None else torch.maximum(leftpad, start)
+    cos = rotary_cos.to(torch.float32).contiguous() if rotary_cos is not None else None
+    sin = rotary_sin.to(torch.float32).contiguous() if rotary_sin is not None else None
+    alibi = alibi_slopes.to(torch.float32).contiguous() if alibi_slopes is not None else None
+    rpos = _as_index(rotary_seqlens, dev) if rotary_seqlens is not None else None
+    out, lse = _C.dec(q.contiguous(), kc.contiguous(), vc.contiguous(), table, lens,
+                      k.contiguous() if appending else None, v.contiguous() if appending else None,
+                      cos, sin, bool(rotary_interleaved), float(softmax_scale), int(keys_back),
+                      int(num_splits or 0), leftpad, bool(return_softmax_lse),
+                      float(softcap or 0.0), alibi, int(cos.shape[-1] * 2) if cos is not None else 0,
+                      rpos)
+    if keep is not None:
+        out = out[..., :keep].contiguous()
+    return (out, lse.transpose(1, 2).contiguous()) if return_softmax_lse else out
+
+
+def _kvcache_packed_q(q, k_cache, v_cache, k, qv, cu_seqlens_q, max_seqlen_q, return_lse,
+                      **kw):
+    """flash_attn_with_kvcache with packed queries q (total_q, nheads, d) and cu_seqlens_q
+    (batch+1): the queries are scattered into a (batch, max_seqlen_q, nheads, d) block on the
+    device (no per-sequence loop or host round trip beyond max_seqlen_q when it is not given),
+    decoded in one call (row t of sequence b at cache_seqlens[b] + t; padding rows are
+    computed and dropped) and gathered back to (total_q, nheads, d)."""
+    if k is not None:
+        raise NotImplementedError(
+            "fable_attn: appending k/v with cu_seqlens_q (a ragged append) is not supported; "
+            "append the same number of tokens to every batch element with a 4-D q")
+    if q.dim() != 3:
+        raise ValueError(f"fable_attn: with cu_seqlens_q, q must be (total_q, nheads, headdim), "
+                         f"got {tuple(q.shape)}")
+    dev = q.device
+    cu = _as_index(cu_seqlens_q, dev).long()
+    nseq, total = cu.numel() - 1, q.shape[0]
+    width = int(max_seqlen_q) if max_seqlen_q is not None else int((cu[1:] - cu[:-1]).max())
+    row = torch.arange(total, device=dev)
+    seq = torch.searchsorted(cu[1:], row, right=True)           # sequence of each packed row
+    slot = seq * width + (row - cu[seq])                         # its row in the padded block
+    qb = q.new_zeros((nseq * width,) + tuple(q.shape[1:]))
+    qb[slot] = q
+    qb = qb.view(nseq, width, q.shape[1], q.shape[2])
+    qvb = None
     if qv is not None:
-        dv_cut = v_cache.shape[-1] - d_real if dv_cut is None else dv_cut
-    out, lse = _C.dec(q.contiguous(), kc.contiguous(), vc.contiguous(), bt, seqlens, nk, nv,
-                      cos, sin, bool(rotary_interleaved), float(softmax_scale), int(win),
-                      int(num_splits or 0), lp, bool(return_softmax_lse),
-                      float(softcap or 0.0), al, int(rdim), rpos)
-    if qv is not None:
-        out = out[..., :qv.shape[-1]].contiguous()
-    elif dv_cut is not None:
-        out = out[..., :dv_cut].contiguous()
-    if return_softmax_lse:
-        return out, lse.transpose(1, 2).contiguous()
-    return out
+        qvb = qv.new_zeros((nseq * width,) + tuple(qv.shape[1:]))
+        qvb[slot] = qv
+        qvb = qvb.view(nseq, width, qv.shape[1], qv.shape[2])
+    r = flash_attn_with_kvcache(qb, k_cache, v_cache, qv=qvb, return_softmax_lse=return_lse,
+                                **kw)
+    ob = r[0] if return_lse else r                               # (batch, width, nheads, dv)
+    out = ob.reshape(nseq * width, ob.shape[2], ob.shape[3])[slot]
+    if not return_lse:
+        return out
+    lse = r[1].transpose(1, 2).reshape(nseq * width, -1)[slot]   # (total_q, nheads)
+    return out, lse.transpose(0, 1).contiguous()

@@ -20,7 +20,7 @@ _LIB = None
 
 def _forward(q, k, v, scale, causal):
     from . import _C
-    from .flash_attn_interface import _kernel_dim, _pad_last
+    from .flash_attn_interface import _kernel_width, _with_width
     empty = q.new_empty(0)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         return empty
@@ -33,12 +33,12 @@ def _forward(q, k, v, scale, causal):
         return empty
     if q.shape[1] % k.shape[1] or k.shape[:3] != v.shape[:3] or q.shape[0] != k.shape[0]:
         return empty
-    dk = _kernel_dim(D)
+    dk = _kernel_width(D)
     try:
         # kernel views: [B,H,S,D] with a contiguous, 16-byte aligned head_dim
         views = []
         for t in (q, k, v):
-            t = _pad_last(t, dk)
+            t = _with_width(t, dk)
             if not _C._rows_aligned(t):
                 t = t.transpose(1, 2).contiguous().transpose(1, 2)
             views.append(t)

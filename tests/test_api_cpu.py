@@ -272,3 +272,64 @@ def test_torch_op_registered_and_falls_back_to_empty():
     assert torch_op._forward(q, q, q, 0.125, True).numel() == 0                  # CPU tensor
     assert torch_op._forward(q.float(), q.float(), q.float(), 0.125, True).numel() == 0
     assert torch_op._forward(q[0], q[0], q[0], 0.125, False).numel() == 0        # 3-D
+
+
+def test_value_head_dim_runs_at_the_wider_width(fake):
+    """headdim_v != headdim without qv: the score needs only q.k, so the narrower side is
+    zero-extended to max(d, dv); the default scale keeps the reference's (d + dv)^-0.5."""
+    q, k, v = rnd(1, 8, 2, 128), rnd(1, 8, 2, 128), rnd(1, 8, 2, 64)
+    out = fai.flash_attn_func(q, k, v)
+    a = fake.calls[-1][1]
+    assert a["shape"][-1] == 128 and math.isclose(a["scale"], 192 ** -0.5)
+    assert out.shape == (1, 8, 2, 64)
+
+
+def test_paged_varlen_gathers_without_host_lengths(fake):
+    """Paged varlen prefill: the block-table rows are gathered whole on the device, sequence z
+    starts at z * max_blocks * page and its true length travels as seqused_k."""
+    calls = []
+    orig = fake.fwd_varlen
+
+    def rec(q, k, v, cu_q, cu_k, mq, mk, *a, **kw):
+        calls.append((k.shape, cu_k.clone(), mk, a[10]))   # (scale ... chunk, su_q, su_k)
+        return orig(q, k, v, cu_q, cu_k, mq, mk, *a, **kw)
+    fake.fwd_varlen = rec
+    kc = rnd(6, 16, 2, 64)
+    bt = torch.tensor([[4, 1], [0, 5]], dtype=torch.int32)
+    cu_q = torch.tensor([0, 3, 7], dtype=torch.int32)
+    cu_k = torch.tensor([0, 20, 45], dtype=torch.int32)
+    fai.flash_attn_varlen_func(rnd(7, 4, 64), kc, kc, cu_q, cu_k, 4, 25, block_table=bt)
+    kshape, cu, mk, used = calls[-1]
+    assert kshape == (64, 2, 64) and cu.tolist() == [0, 32, 64] and mk == 32
+    assert used.tolist() == [20, 25]
+
+
+def test_kvcache_packed_queries_one_call(fake):
+    """cu_seqlens_q: the packed queries go to the kernel as one (batch, max_seqlen_q) block
+    and come back packed, in one decode call."""
+    kc = rnd(8, 16, 2, 64)
+    bt = torch.arange(8, dtype=torch.int32).view(2, 4)
+    q = rnd(5, 4, 64)
+    cu = torch.tensor([0, 2, 5], dtype=torch.int32)
+    out, lse = fai.flash_attn_with_kvcache(q, kc, kc, cache_seqlens=torch.tensor([10, 30]),
+                                           block_table=bt, cu_seqlens_q=cu, max_seqlen_q=3,
+                                           return_softmax_lse=True)
+    decs = [c for c in fake.calls if c[0] == "dec"]
+    assert len(decs) == 1 and decs[0][1]["q"] == (2, 3, 4, 64)
+    assert out.shape == (5, 4, 64) and lse.shape == (4, 5)
+    with pytest.raises(NotImplementedError):
+        fai.flash_attn_with_kvcache(q, kc, kc, k=rnd(5, 2, 64), v=rnd(5, 2, 64), block_table=bt,
+                                    cu_seqlens_q=cu, max_seqlen_q=3)
+
+
+def test_kvcache_append_refused_into_a_temporary(fake):
+    """Appending must write the caller's cache: with qv (a widened temporary) or a
+    non-contiguous cache it is refused instead of silently lost."""
+    q, kc = rnd(1, 1, 4, 64), rnd(4, 16, 2, 64)
+    bt = torch.zeros((1, 4), dtype=torch.int32)
+    nk = rnd(1, 1, 2, 64)
+    with pytest.raises(NotImplementedError):
+        fai.flash_attn_with_kvcache(q, kc, kc, k=nk, v=nk, qv=rnd(1, 1, 4, 64), block_table=bt)
+    with pytest.raises(NotImplementedError):
+        t = kc.transpose(1, 2)
+        fai.flash_attn_with_kvcache(q, t, t, k=nk, v=nk, block_table=bt)
