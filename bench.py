@@ -9,12 +9,16 @@ A step is one pass of the hot path over one batch of synthetic input:
   lab/bench_e2e.py:137-138).
 `roofline` reports the dominant kernel (the forward kernel): algorithmic FLOP per launch divided
 by its average duration, measured with HIP events on the stream the kernel is launched on
-(torch's current stream), against the dense fp16 MFMA peak of 2.5 PFLOP/s.
+(torch's current stream), against the dense fp16 MFMA peak of 2.5 PFLOP/s; `traffic` is its HBM
+bytes per launch from the calibrated rocprofv3 PMC tables under profiles/.
 `cpu_baseline` times the exact fp32 torch reference (oracle/torch_ref.py) on the host cores over
-a bounded sample of heads of the same workload and scales to TFLOP/s with the same numerator.
-`extra` holds the other BASELINE.json configs (backward, paged decode, varlen) measured the
-same way (at least 3 warmup and 20 timed steps each), with the mean and the median of the
-per-step HIP-event times; they are not the headline.
+a bounded sample of the same workload and scales to the metric's unit with the same numerator.
+`extra` holds the other BASELINE.json configs (C1, C2 at S=4096/8192, C3 backward, C4 paged
+decode, C5 varlen), each measured the same way (at least 3 warmup and 20 timed steps, mean and
+median of the per-step HIP-event times) and each with its own `roofline` block (over the whole
+step's kernels) and `cpu_baseline` (the same torch reference path on CPU tensors: per-head
+autograd for C3, pages gathered per sequence for C4, per sequence and head for C5); they are
+not the headline.
 """
 import argparse
 import json
@@ -64,6 +68,25 @@ def _median(x):
     return 0.5 * (x[(len(x) - 1) // 2] + x[len(x) // 2])
 
 
+def roofline(bound, work, ms, traffic=None):
+    """Roofline block of one step: algorithmic work (FLOP, or bytes for an HBM-bound step) over
+    the step's HIP-event time, against the MI355X peak; traffic = calibrated HBM bytes per step
+    from the committed PMC tables (None when no table covers the step's kernels)."""
+    if bound == "mfma":
+        ach, peak, unit = work / (ms * 1e-3) / 1e12, PEAK_MFMA_TFLOPS, "TFLOP/s"
+    else:
+        ach, peak, unit = work / (ms * 1e-3) / 1e9, PEAK_HBM_GBS, "GB/s"
+    return {"bound": bound, "achieved": round(ach, 2), "peak": peak, "unit": unit,
+            "frac": round(ach / peak, 4), "traffic": traffic}
+
+
+def _cpu_threads():
+    import torch
+    cores = os.cpu_count() or 1
+    torch.set_num_threads(cores)
+    return cores
+
+
 def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", seed=0):
     import torch
     from fable_attn import flash_attn_func
@@ -78,7 +101,9 @@ def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", see
     return {"S": S, "H": H, "D": D, "B": B, "causal": causal, "dtype": dtype, "flops": flops,
             "ms": wall, "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
             "kernel_tflops": flops / (ev * 1e-3) / 1e12, "kernel_ms_median": _median(per),
-            "tflops_median": flops / (_median(per) * 1e-3) / 1e12}
+            "tflops_median": flops / (_median(per) * 1e-3) / 1e12,
+            "roofline": roofline("mfma", flops, ev, profiled_traffic(
+                FWD_C2_KERNEL if (D == 128 and causal) else FWD_C1_KERNEL))}
 
 
 def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0):
@@ -103,10 +128,33 @@ def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0):
     return {"B": B, "S": S, "H": H, "D": D, "dtype": "bf16", "flops": flops, "ms": wall,
             "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
             "kernel_ms_median": _median(per), "tflops_median": flops / (_median(per) * 1e-3) / 1e12,
-            "bitwise_identical_x3": bool(same)}
+            "bitwise_identical_x3": bool(same),
+            "roofline": roofline("mfma", flops, ev, profiled_traffic(BWD_C3_KERNELS))}
 
 
-def bench_decode(steps, warmup, batch=16, Hq=32, Hk=8, D=128, ctx=32768, page=256, seed=0):
+def cpu_bwd(heads=8, B=2, S=4096, H=32, D=128, seed=0):
+    """C3 on the CPU: torch autograd through the exact fp32 reference, one (batch, head) at a
+    time, `heads` of the B*H heads; the rate uses C3's numerator (2.5x the causal forward)."""
+    import torch
+    from oracle.torch_ref import attention_bhsd
+    cores = _cpu_threads()
+    g = torch.Generator().manual_seed(seed)
+    mk = lambda: torch.randn(1, 1, S, D, generator=g).bfloat16().float()
+    q, k, v, do = mk(), mk(), mk(), mk()
+    t0 = time.perf_counter()
+    for _ in range(heads):
+        qs, ks, vs = (x.clone().requires_grad_() for x in (q, k, v))
+        attention_bhsd(qs, ks, vs, D ** -0.5, causal=True).backward(do)
+    dt = time.perf_counter() - t0
+    flops = 2.5 * 4.0 * heads * S * S * D / 2
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"{heads} of {B * H} (batch, head) pairs of the causal S={S} D={D} "
+                      f"backward (forward + autograd of the fp32 torch reference on CPU tensors), "
+                      f"{dt:.1f} s; extrapolated linearly to all heads"}
+
+
+def bench_decode(steps, warmup, batch=16, Hq=32, Hk=8, D=128, ctx=32768, page=256, seed=0,
+                 cpu_seqs=0):
     """C4: paged-KV decode fp16, block_table = seeded permutation of the physical pages."""
     import torch
     from fable_attn import flash_attn_with_kvcache
@@ -123,14 +171,42 @@ def bench_decode(steps, warmup, batch=16, Hq=32, Hk=8, D=128, ctx=32768, page=25
     per = []
     wall, ev = time_steps(f, steps, warmup, per)
     nbytes = 2.0 * batch * ctx * Hk * D * 2
-    return {"batch": batch, "Hq": Hq, "Hk": Hk, "D": D, "ctx": ctx, "page": page, "bytes": nbytes,
-            "ms": wall, "kernel_ms": ev, "GBs": nbytes / (wall * 1e-3) / 1e9,
-            "kernel_ms_median": _median(per), "GBs_median": nbytes / (_median(per) * 1e-3) / 1e9,
-            "frac_hbm": nbytes / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS,
-            "traffic_partial_kernel": profiled_traffic(DEC_C4_KERNEL)}
+    res = {"batch": batch, "Hq": Hq, "Hk": Hk, "D": D, "ctx": ctx, "page": page, "bytes": nbytes,
+           "ms": wall, "kernel_ms": ev, "GBs": nbytes / (wall * 1e-3) / 1e9,
+           "kernel_ms_median": _median(per), "GBs_median": nbytes / (_median(per) * 1e-3) / 1e9,
+           "frac_hbm": nbytes / (wall * 1e-3) / 1e9 / PEAK_HBM_GBS,
+           "roofline": roofline("hbm", nbytes, ev, profiled_traffic(DEC_C4_KERNELS))}
+    if cpu_seqs:
+        res["cpu_baseline"] = cpu_decode(q, kc, vc, bt, ctx, page, cpu_seqs, nbytes / batch)
+    return res
 
 
-def bench_varlen(steps, warmup, H=16, D=256, seed=0):
+def cpu_decode(q, kc, vc, bt, ctx, page, seqs, bytes_per_seq):
+    """C4 on the CPU: for `seqs` sequences, their pages are gathered into dense K/V (untimed,
+    as a CPU cache would hold them) and the exact fp32 torch reference attends one query token
+    over the ctx keys; the rate uses C4's numerator (K+V bytes in fp16)."""
+    import torch
+    from oracle.torch_ref import attention_bhsd
+    cores = _cpu_threads()
+    Hq, D = q.shape[2], q.shape[3]
+    dt = 0.0
+    for b in range(seqs):
+        pages = bt[b].long()
+        kb = kc[pages].reshape(-1, kc.shape[2], D)[:ctx].float().cpu().transpose(0, 1)[None]
+        vb = vc[pages].reshape(-1, vc.shape[2], D)[:ctx].float().cpu().transpose(0, 1)[None]
+        qb = q[b].float().cpu().transpose(0, 1)[None]                  # [1, Hq, 1, D]
+        t0 = time.perf_counter()
+        attention_bhsd(qb, kb, vb, D ** -0.5)
+        dt += time.perf_counter() - t0
+    return {"value": bytes_per_seq * seqs / dt / 1e9, "unit": "GB/s", "cores": cores,
+            "kind": "port",
+            "sample": f"{seqs} of {bt.shape[0]} sequences (ctx {ctx}, {Hq} q heads, D={D}), pages "
+                      f"gathered to dense fp32 K/V untimed, fp32 torch reference on CPU tensors, "
+                      f"{dt:.2f} s; GB/s of the fp16 K/V bytes those sequences read, extrapolated "
+                      f"linearly to all sequences"}
+
+
+def bench_varlen(steps, warmup, H=16, D=256, seed=0, cpu_heads=0):
     """C5: varlen bf16, 8 sequences with lengths ~U[512, 8192] (seeded), window (512,0) +
     causal, softcap 30; FLOP counts exact unmasked pairs."""
     import torch
@@ -147,9 +223,36 @@ def bench_varlen(steps, warmup, H=16, D=256, seed=0):
     wall, ev = time_steps(f, steps, warmup, per)
     pairs = sum(sum(min(i, 512) + 1 for i in range(L)) for L in lens)
     flops = 4.0 * D * H * pairs
-    return {"lens": lens, "H": H, "D": D, "flops": flops, "ms": wall, "kernel_ms": ev,
-            "tflops": flops / (wall * 1e-3) / 1e12, "kernel_ms_median": _median(per),
-            "tflops_median": flops / (_median(per) * 1e-3) / 1e12}
+    res = {"lens": lens, "H": H, "D": D, "flops": flops, "ms": wall, "kernel_ms": ev,
+           "tflops": flops / (wall * 1e-3) / 1e12, "kernel_ms_median": _median(per),
+           "tflops_median": flops / (_median(per) * 1e-3) / 1e12,
+           "roofline": roofline("mfma", flops, ev, profiled_traffic(VARLEN_C5_KERNEL))}
+    if cpu_heads:
+        res["cpu_baseline"] = cpu_varlen(q, k, v, lens, cpu_heads, H, D)
+    return res
+
+
+def cpu_varlen(q, k, v, lens, heads, H, D):
+    """C5 on the CPU: every sequence, `heads` of its H heads, through the exact fp32 torch
+    reference (window (512, 0), causal, softcap 30) on CPU tensors; the rate uses C5's
+    numerator (exact visible pairs), extrapolated from the sampled heads to all H."""
+    import torch
+    from oracle.torch_ref import attention_bhsd
+    cores = _cpu_threads()
+    dt, pairs, a = 0.0, 0, 0
+    for L in lens:
+        sl = lambda t: t[a:a + L, :heads].float().cpu().transpose(0, 1)[None]  # [1, heads, L, D]
+        qs, ks, vs = sl(q), sl(k), sl(v)
+        t0 = time.perf_counter()
+        attention_bhsd(qs, ks, vs, D ** -0.5, causal=True, win_left=512, win_right=0, softcap=30.0)
+        dt += time.perf_counter() - t0
+        pairs += sum(min(i, 512) + 1 for i in range(L))
+        a += L
+    flops = 4.0 * D * heads * pairs
+    return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
+            "sample": f"all {len(lens)} sequences, {heads} of {H} heads (D={D}, window 512 + causal "
+                      f"+ softcap 30), fp32 torch reference on CPU tensors, {dt:.1f} s; "
+                      f"extrapolated linearly to all heads"}
 
 
 # ---- rocprofv3 summaries (CPU only: they read the CSV files rocprofv3 wrote) ----------------
@@ -259,42 +362,57 @@ def summarize_stats(d, kernel_re=None, skip=0):
     return "\n".join(out)
 
 
-# kernel symbols of the measured workloads (one symbol per workload in the PMC runs, which
-# leave out the fwd extras that share the headline's symbol)
-FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128ELi64ELi8ELi2ELi1EEELb1ELb0ELb0EEEv9FwdParamsi"
-DEC_C4_KERNEL = r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0EEEv9DecParamsiii"
+# kernel symbols of the measured workloads, as regexes over the mangled names in the PMC
+# tables (the headline's kernel; the kernels of one C3, C4 or C5 step)
+FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128ELi64ELi8ELi2ELi1EEELb1ELb0ELb0EEEv14FableFwdParamsi"
+FWD_C1_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi64E.*ELb0ELb0ELb0EEEv14FableFwdParamsi"
+BWD_C3_KERNELS = (r"_ZN2fa15bwd_dsum_kernelIDF16b.*", r"_ZN2fa20bwd_dkdv_pair_kernelIDF16b.*",
+                  r"_ZN2fa16bwd_dq_ds_kernelIDF16b.*")
+DEC_C4_KERNELS = (r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0EEEv14FableDecParamsiii",
+                  r"_ZN2fa17dec_combine_kernelIDF16_Li128EEEv14FableDecParams")
+VARLEN_C5_KERNEL = r"_ZN2fa10fwd_kernelIDF16b_NS_6FwdCfgILi256E.*ELb1ELb1ELb0EEEv14FableFwdParamsi"
 
 
-def profiled_traffic(kernel_re):
-    """HBM bytes per dispatch of the kernel whose symbol matches `kernel_re`, from the calibrated
-    PMC tables committed under profiles/ (None if no table names it)."""
+def profiled_traffic(kernel_res):
+    """Calibrated HBM bytes per step summed over the kernels matching `kernel_res` (one regex or
+    a tuple, one kernel each) from the PMC tables committed under profiles/; None if a kernel
+    is in no table (each table comes from one run of this bench.py)."""
     import glob
+    res = (kernel_res,) if isinstance(kernel_res, str) else tuple(kernel_res)
+    rows = []
     for f in sorted(glob.glob(os.path.join(PROFILES, "*pmc*.md"))):
         for line in open(f):
             m = re.match(r"\| `([^`]+)` \| \d+ \| [\d.]+ \| [\d.]+ \| (\d+) \|", line)
-            if m and re.fullmatch(kernel_re, m.group(1)):
-                return int(m.group(2))
-    return None
+            if m:
+                rows.append((m.group(1), int(m.group(2))))
+    total = 0
+    for r in res:
+        hit = [b for name, b in rows if re.fullmatch(r, name)]
+        if not hit:
+            return None
+        total += hit[0]
+    return total
 
 
-def cpu_baseline(S=16384, H=32, D=128, heads=32, seed=0):
-    """Exact fp32 torch reference on the host cores, `heads` of the H heads of the headline
-    workload (one head at a time to bound memory), scaled to the full workload's FLOP rate."""
+def cpu_baseline(S=16384, H=32, D=128, heads=16, causal=True, seed=0):
+    """Exact fp32 torch reference on the host cores, `heads` of the H heads of a forward
+    workload (one head at a time to bound memory), scaled to the full workload's FLOP rate
+    (the causal half for causal, as the GPU figure)."""
     import torch
     from oracle.torch_ref import attention_bhsd
-    cores = os.cpu_count() or 1
-    torch.set_num_threads(cores)
+    cores = _cpu_threads()
     g = torch.Generator().manual_seed(seed)
     q, k, v = (torch.randn(1, 1, S, D, generator=g).half().float() for _ in range(3))
-    attention_bhsd(q[:, :, :256], k[:, :, :256], v[:, :, :256], D ** -0.5, causal=True)  # warm
+    attention_bhsd(q[:, :, :256], k[:, :, :256], v[:, :, :256], D ** -0.5, causal=causal)  # warm
     t0 = time.perf_counter()
     for _ in range(heads):
-        attention_bhsd(q, k, v, D ** -0.5, causal=True)
+        attention_bhsd(q, k, v, D ** -0.5, causal=causal)
     dt = time.perf_counter() - t0
-    flops = 4.0 * heads * S * S * D / 2
+    flops = 4.0 * heads * S * S * D / (2 if causal else 1)
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"{heads} of {H} heads of the causal S={S} D={D} forward, fp32 torch "
-                      f"reference on CPU tensors, {dt:.1f} s; rate scales linearly to all heads"}
+            "sample": f"{heads} of {H} heads of the {'causal' if causal else 'non-causal'} S={S} "
+                      f"D={D} forward, fp32 torch reference on CPU tensors, {dt:.1f} s"
+                      + ("; extrapolated linearly to all heads" if heads < H else "")}
 
 
 def main():
@@ -303,7 +421,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=32)
+    ap.add_argument("--cpu-heads", type=int, default=16)
     ap.add_argument("--extras", default="fwd,bwd,decode,varlen")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
@@ -338,19 +456,31 @@ def main():
     log("[bench] headline: causal fp16 forward S=16384 H=32 D=128")
     head = bench_fwd(16384, a.steps, a.warmup)
     log(f"[bench] fwd S=16384: {head['ms']:.3f} ms  {head['tflops']:.1f} TFLOP/s")
+    cpu_on = not a.no_cpu
     extra = {}
     for name in [x for x in a.extras.split(",") if x]:
         try:
             if name == "fwd":
                 for S in (4096, 8192):
-                    extra[f"fwd_causal_S{S}"] = bench_fwd(S, max(a.steps, 20), max(3, a.warmup))
-                extra["fwd_C1_S1024_D64_noncausal"] = bench_fwd(1024, 20, 3, causal=False, H=8, D=64)
+                    r = bench_fwd(S, max(a.steps, 20), max(3, a.warmup))
+                    if cpu_on:
+                        r["cpu_baseline"] = cpu_baseline(S=S, heads=4 if S == 4096 else 2)
+                    extra[f"fwd_causal_S{S}"] = r
+                r = bench_fwd(1024, 20, 3, causal=False, H=8, D=64)
+                if cpu_on:
+                    r["cpu_baseline"] = cpu_baseline(S=1024, H=8, D=64, heads=8, causal=False)
+                extra["fwd_C1_S1024_D64_noncausal"] = r
             elif name == "bwd":
-                extra["bwd_C3"] = bench_bwd(max(20, a.steps), max(3, a.warmup))
+                r = bench_bwd(max(20, a.steps), max(3, a.warmup))
+                if cpu_on:
+                    r["cpu_baseline"] = cpu_bwd()
+                extra["bwd_C3"] = r
             elif name == "decode":
-                extra["decode_C4"] = bench_decode(max(a.steps, 20), max(3, a.warmup))
+                extra["decode_C4"] = bench_decode(max(a.steps, 20), max(3, a.warmup),
+                                                  cpu_seqs=4 if cpu_on else 0)
             elif name == "varlen":
-                extra["varlen_C5"] = bench_varlen(max(20, a.steps), max(3, a.warmup))
+                extra["varlen_C5"] = bench_varlen(max(20, a.steps), max(3, a.warmup),
+                                                  cpu_heads=1 if cpu_on else 0)
             log(f"[bench] extra {name} done")
         except RuntimeError as e:
             extra[name] = {"error": str(e)[:300]}

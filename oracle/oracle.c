@@ -14,8 +14,9 @@
  *                   the exact forward, Di = sum(O*dO), dS = P*(z*dP - Di)*softcap'(.), dQ,dK,dV
  *                   with dropout multiplier z (1 when dropout_p == 0).
  *   oracle_bwd_model the same gradients with only the roundings a 16-bit-operand backward must
- *                   make (O before Di, z*P before dV, dS before dK/dQ); not a reference
- *                   routine: it measures the floor of fp16/bf16 kernels against oracle_bwd.
+ *                   make (O before Di, or Di from a given stored O; z*P before dV; dS before
+ *                   dK/dQ); not a reference routine: it measures the floor of fp16/bf16
+ *                   kernels against oracle_bwd.
  *   dropout         kernels/fa_common.hpp:71-88: Philox4x32-10 (Salmon, Moraes, Dror, Shaw,
  *                   "Parallel random numbers: as easy as 1, 2, 3", SC 2011) on counter
  *                   (idx, 0, 0) and key = seed; u = (word0 >> 8) * 2^-24; kept (z = 1/(1-p))
@@ -186,7 +187,7 @@ static double round_mode(double x, int mode) {
  * model from mode 0 is the floor that any 16-bit-operand backward shows against the exact
  * gradients. */
 static void bwd_impl(const float* Q, const float* K, const float* V, const float* dO, double* dQ,
-                     double* dK, double* dV, const OracleCfg* c, int mode) {
+                     double* dK, double* dV, const OracleCfg* c, int mode, const float* Ost) {
   const int gqa = c->H / c->Hk;
   const size_t nq = (size_t)c->B * c->H * c->SQ * c->D, nk = (size_t)c->B * c->Hk * c->SK * c->D;
   memset(dQ, 0, nq * sizeof(double));
@@ -232,7 +233,7 @@ static void bwd_impl(const float* Q, const float* K, const float* V, const float
             double acc = 0.0;
             for (int j = 0; j < c->SK; j++)
               acc += P[j] * drop_mul(c, h, i, j) * (double)Vb[(size_t)j * c->D + d];
-            o[d] = round_mode(acc, mode);
+            o[d] = Ost ? (double)Ost[qo + d] : round_mode(acc, mode);
             Di += o[d] * (double)g[d];
           }
           double* dq = dQ + qo;
@@ -259,13 +260,16 @@ static void bwd_impl(const float* Q, const float* K, const float* V, const float
 /* exact fp64 gradients */
 void oracle_bwd(const float* Q, const float* K, const float* V, const float* dO, double* dQ,
                 double* dK, double* dV, const OracleCfg* c) {
-  bwd_impl(Q, K, V, dO, dQ, dK, dV, c, 0);
+  bwd_impl(Q, K, V, dO, dQ, dK, dV, c, 0, NULL);
 }
 
-/* rounding model of a 16-bit-operand backward (mode 1 fp16, 2 bf16), see bwd_impl */
+/* rounding model of a 16-bit-operand backward (mode 1 fp16, 2 bf16), see bwd_impl; Ost (or
+ * NULL) is a stored forward output [B][H][SQ][D] to take D = rowsum(O*dO) from, as a backward
+ * that reads the forward's stored O does */
 void oracle_bwd_model(const float* Q, const float* K, const float* V, const float* dO,
-                      double* dQ, double* dK, double* dV, const OracleCfg* c, int mode) {
-  bwd_impl(Q, K, V, dO, dQ, dK, dV, c, mode);
+                      double* dQ, double* dK, double* dV, const OracleCfg* c, int mode,
+                      const float* Ost) {
+  bwd_impl(Q, K, V, dO, dQ, dK, dV, c, mode, Ost);
 }
 
 typedef struct OracleDecCfg {

@@ -137,7 +137,7 @@ def test_backward_dropout_vs_oracle(case, dt, ds_max):
     torch.cuda.synchronize()
     args = (q, k, v, do, scale, causal, -1, -1, sc, None)
     ref = orc.bwd(*args, dropout_p=p, seed=SEED)
-    model = orc.bwd(*args, dropout_p=p, seed=SEED, model=dt)
+    model = orc.bwd(*args, dropout_p=p, seed=SEED, model=dt, stored_o=to_np(out))
     for i, gname in enumerate(("dq", "dk", "dv")):
         assert torch.equal(g1[i], g2[i]), f"{gname} differs between runs"
     check_grads("dropout_bwd_" + ("ds" if ds_max is None else "recompute"), name, dt, g1, ref, model)
@@ -165,7 +165,7 @@ def test_autograd_reuses_forward_seed():
     assert orc.rel_rms(bhsd(out), ro) <= TOL["f16"]
     args = (bhsd(q), bhsd(k), bhsd(v), bhsd(dout), D ** -0.5, True)
     ref = orc.bwd(*args, dropout_p=p, seed=seed)
-    model = orc.bwd(*args, dropout_p=p, seed=seed, model="f16")
+    model = orc.bwd(*args, dropout_p=p, seed=seed, model="f16", stored_o=bhsd(out))
     check_grads("dropout_autograd", "causal D64", "f16",
                 [bhsd(x.grad) for x in (q, k, v)], ref, model)
 
@@ -196,6 +196,6 @@ def test_varlen_autograd_dropout():
         assert orc.rel_rms(seq(out), ro) <= TOL["f16"], f"seq {i} O"
         args = (seq(q), seq(k), seq(v), seq(dout), D ** -0.5, True)
         ref = orc.bwd(*args, dropout_p=p, seed=seed)
-        model = orc.bwd(*args, dropout_p=p, seed=seed, model="f16")
+        model = orc.bwd(*args, dropout_p=p, seed=seed, model="f16", stored_o=seq(out))
         check_grads("dropout_varlen_autograd", f"seq {i}", "f16",
                     [seq(x.grad) for x in (q, k, v)], ref, model, vanish_ok=True)
