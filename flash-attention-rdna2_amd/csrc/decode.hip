@@ -17,12 +17,15 @@
 //  * appending new_k/new_v (with rotary on k) is a kernel earlier in the same stream: the
 //    reference's hipDeviceSynchronize() after the append (fa_decode.hip:348-351) is gone.
 // Scores are handled in the log2 domain; partial maxima are stored in log2 units.
+#include <mutex>
 #include <type_traits>
 
 #include "attn_device.hpp"
 #include "status.hpp"
 
 namespace fa {
+
+static int dec_checked(FableDecParams p, int dtype, void* stream, const void* new_k, const void* new_v);
 
 constexpr int kDecChunk = 32;  // keys per wave iteration
 constexpr int kDecWaves = 4;
@@ -608,6 +611,76 @@ extern "C" int fable_attn_dec(FableDecParams p, int dtype, void* stream, const v
   using namespace fa;
   if (!p.q || !p.Kc || !p.Vc || !p.block_table || !p.o || !p.scratch || !p.ctx_len)
     return fail(FA_ERR_ARG, "fable_attn_dec: null pointer");
+  return dec_checked(p, dtype, stream, new_k, new_v);
+}
+
+// ------------------------------------------------------------------ decode without allocation
+// The split partials live in a device array of fixed size that the library owns (one copy per
+// GPU, held until the process ends), for callers that cannot allocate: code under HIP graph
+// capture, tight serving loops, harnesses that forbid hipMalloc. In host code `dec_scratch`
+// names a host-side stand-in, not device memory: its device address on the current GPU comes
+// from hipGetSymbolAddress, once per device, and only that address is ever passed to a kernel.
+// Every partial slot is written before the combine reads it, so nothing needs clearing between
+// calls; calls that overlap on one GPU (two streams, or a graph replay beside an eager call)
+// race on the array and must be serialised by the caller.
+namespace {
+
+constexpr long long kDecScratchFloats = 4ll << 20;  // 16 MiB
+static __device__ __align__(256) float dec_scratch[kDecScratchFloats];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_dec_scratch_mu;
+float* g_dec_scratch_ptr[kMaxDevices] = {};
+
+// device address of dec_scratch on the GPU of `stream` (which must be the current device)
+int dec_scratch_ptr(void* stream, float** out) {
+  using fa::fail;
+  int cur = -1;
+  if (hipGetDevice(&cur) != hipSuccess || cur < 0 || cur >= kMaxDevices)
+    return fail(FA_ERR_LAUNCH, "fable_attn_dec_noalloc: no current device (%d)", cur);
+  if (stream) {
+    hipDevice_t sdev = -1;
+    if (hipStreamGetDevice((hipStream_t)stream, &sdev) != hipSuccess)
+      return fail(FA_ERR_ARG, "fable_attn_dec_noalloc: the stream's device is unknown");
+    if (sdev != cur)
+      return fail(FA_ERR_ARG, "fable_attn_dec_noalloc: the stream belongs to device %d, the current "
+                              "device is %d (make the stream's device current)", (int)sdev, cur);
+  }
+  std::lock_guard<std::mutex> lock(g_dec_scratch_mu);
+  if (!g_dec_scratch_ptr[cur]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(dec_scratch));
+    if (e != hipSuccess || !ptr)
+      return fail(FA_ERR_LAUNCH, "fable_attn_dec_noalloc: hipGetSymbolAddress: %s", hipGetErrorString(e));
+    g_dec_scratch_ptr[cur] = (float*)ptr;
+  }
+  *out = g_dec_scratch_ptr[cur];
+  return FA_OK;
+}
+
+}  // namespace
+
+extern "C" int64_t fable_attn_dec_noalloc_max_floats(void) { return kDecScratchFloats; }
+
+extern "C" int fable_attn_dec_noalloc(FableDecParams p, int dtype, void* stream, const void* new_k,
+                                      const void* new_v) {
+  using namespace fa;
+  if (!p.q || !p.Kc || !p.Vc || !p.block_table || !p.o || !p.ctx_len)
+    return fail(FA_ERR_ARG, "fable_attn_dec_noalloc: null pointer");
+  if (p.batch <= 0) return FA_OK;
+  const long long need = (long long)p.batch * (p.nq < 1 ? 1 : p.nq) * p.NH * p.nsplit * (p.HD + 2);
+  if (p.NH <= 0 || p.nsplit < 1 || p.HD <= 0 || need > kDecScratchFloats)
+    return fail(FA_ERR_ARG, "fable_attn_dec_noalloc: batch*nq*NH*nsplit*(HD+2) = %lld floats of split "
+                            "partials exceed the fixed %lld (lower nsplit, or use fable_attn_dec with a "
+                            "caller-allocated scratch)", need, kDecScratchFloats);
+  if (int rc = dec_scratch_ptr(stream, &p.scratch)) return rc;
+  return dec_checked(p, dtype, stream, new_k, new_v);
+}
+
+namespace fa {
+
+// the checks and dispatch shared by fable_attn_dec and fable_attn_dec_noalloc
+static int dec_checked(FableDecParams p, int dtype, void* stream, const void* new_k, const void* new_v) {
   if (p.page <= 0 || (p.page & (p.page - 1))) return fail(FA_ERR_ARG, "fable_attn_dec: page=%d is not a power of two", p.page);
   if (p.NH <= 0 || p.gqa <= 0 || p.NH % p.gqa) return fail(FA_ERR_ARG, "fable_attn_dec: NH=%d gqa=%d", p.NH, p.gqa);
   if (p.nsplit < 1 || p.nsplit > 512) return fail(FA_ERR_ARG, "fable_attn_dec: nsplit=%d", p.nsplit);
@@ -624,3 +697,5 @@ extern "C" int fable_attn_dec(FableDecParams p, int dtype, void* stream, const v
     default: return fail(FA_ERR_DTYPE, "fable_attn_dec: dtype %d not implemented (fp16/bf16/fp32)", dtype);
   }
 }
+
+}  // namespace fa

@@ -118,7 +118,8 @@ STRUCTS = {0: FableFwdParams, 1: FableBwdParams, 2: FableDecParams, 3: CombinePa
 
 # exported symbols of libfable_attn_hip.so (the C-ABI surface)
 EXPORTS = ("fa_forward_launch", "fable_attn_backward_launch", "fa_decode_launch",
-           "fable_attn_fwd", "fable_attn_bwd", "fable_attn_dec",
+           "fable_attn_fwd", "fable_attn_bwd", "fable_attn_dec", "fable_attn_dec_noalloc",
+           "fable_attn_dec_noalloc_max_floats",
            "fa_decode_num_splits", "fa_combine_launch", "fable_attn_bwd_ds_bytes",
            "fable_attn_abi_version", "fable_attn_struct_size", "fable_attn_last_error")
 
@@ -143,7 +144,10 @@ def load():
     lib.fa_forward_launch.argtypes = [RefFwdParams, c_i32, c_ptr]
     lib.fable_attn_backward_launch.argtypes = [RefBwdParams, c_i32, c_ptr]
     lib.fa_decode_launch.argtypes = [RefDecParams, c_i32, c_ptr, c_ptr, c_ptr]
-    for f in ("fable_attn_fwd", "fable_attn_bwd", "fable_attn_dec", "fa_forward_launch",
+    lib.fable_attn_dec_noalloc.argtypes = [FableDecParams, c_i32, c_ptr, c_ptr, c_ptr]
+    lib.fable_attn_dec_noalloc_max_floats.restype = c_i64
+    for f in ("fable_attn_fwd", "fable_attn_bwd", "fable_attn_dec", "fable_attn_dec_noalloc",
+              "fa_forward_launch",
               "fable_attn_backward_launch", "fa_decode_launch",
               "fa_decode_num_splits", "fa_combine_launch", "fable_attn_abi_version"):
         getattr(lib, f).restype = c_i32

@@ -297,6 +297,19 @@ int64_t fable_attn_bwd_ds_bytes(FableBwdParams p, int dtype);
  * (with rotary on k) before attention, in stream order: no device-wide synchronisation. */
 int fable_attn_dec(FableDecParams p, int dtype, void* stream, const void* new_k, const void* new_v);
 
+/* fable_attn_dec without allocation. No counterpart in the reference: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc). p.scratch is ignored: the split partials go to a fixed device array owned
+ * by the library, one per GPU, kept until the process ends, of
+ * fable_attn_dec_noalloc_max_floats() floats (16 MiB); a call needing more
+ * (batch*nq*NH*nsplit*(HD+2) floats) fails with FA_ERR_ARG. Nothing is allocated or freed.
+ * The stream's device must be the current device. Calls that overlap on one GPU share the
+ * array and race: the caller serialises them. Otherwise exactly fable_attn_dec (same kernels,
+ * same results). */
+int fable_attn_dec_noalloc(FableDecParams p, int dtype, void* stream, const void* new_k,
+                           const void* new_v);
+int64_t fable_attn_dec_noalloc_max_floats(void);
+
 /* split count chosen for a decode call (reference heuristic: dispatch.cpp:182-200, retuned for
  * 256 CUs); num_splits_hint > 0 is honoured (clamped to [1, 512]). */
 int fa_decode_num_splits(int batch, int nq, int NH, int gqa, int64_t ctx_bound, int num_splits_hint);
