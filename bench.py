@@ -132,7 +132,7 @@ def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0):
             "roofline": roofline("mfma", flops, ev, profiled_traffic(BWD_C3_KERNELS))}
 
 
-def cpu_bwd(heads=8, B=2, S=4096, H=32, D=128, seed=0):
+def cpu_bwd(heads=32, B=2, S=4096, H=32, D=128, seed=0):
     """C3 on the CPU: torch autograd through the exact fp32 reference, one (batch, head) at a
     time, `heads` of the B*H heads; the rate uses C3's numerator (2.5x the causal forward)."""
     import torch
@@ -202,8 +202,8 @@ def cpu_decode(q, kc, vc, bt, ctx, page, seqs, bytes_per_seq):
             "kind": "port",
             "sample": f"{seqs} of {bt.shape[0]} sequences (ctx {ctx}, {Hq} q heads, D={D}), pages "
                       f"gathered to dense fp32 K/V untimed, fp32 torch reference on CPU tensors, "
-                      f"{dt:.2f} s; GB/s of the fp16 K/V bytes those sequences read, extrapolated "
-                      f"linearly to all sequences"}
+                      f"{dt:.2f} s; GB/s of the fp16 K/V bytes those sequences read"
+                      + ("; extrapolated linearly to all sequences" if seqs < bt.shape[0] else "")}
 
 
 def bench_varlen(steps, warmup, H=16, D=256, seed=0, cpu_heads=0):
@@ -394,7 +394,7 @@ def profiled_traffic(kernel_res):
     return total
 
 
-def cpu_baseline(S=16384, H=32, D=128, heads=16, causal=True, seed=0):
+def cpu_baseline(S=16384, H=32, D=128, heads=32, causal=True, seed=0):
     """Exact fp32 torch reference on the host cores, `heads` of the H heads of a forward
     workload (one head at a time to bound memory), scaled to the full workload's FLOP rate
     (the causal half for causal, as the GPU figure)."""
@@ -421,7 +421,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--cpu-heads", type=int, default=16)
+    ap.add_argument("--cpu-heads", type=int, default=32)
     ap.add_argument("--extras", default="fwd,bwd,decode,varlen")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
@@ -464,7 +464,7 @@ def main():
                 for S in (4096, 8192):
                     r = bench_fwd(S, max(a.steps, 20), max(3, a.warmup))
                     if cpu_on:
-                        r["cpu_baseline"] = cpu_baseline(S=S, heads=4 if S == 4096 else 2)
+                        r["cpu_baseline"] = cpu_baseline(S=S)
                     extra[f"fwd_causal_S{S}"] = r
                 r = bench_fwd(1024, 20, 3, causal=False, H=8, D=64)
                 if cpu_on:
@@ -477,10 +477,10 @@ def main():
                 extra["bwd_C3"] = r
             elif name == "decode":
                 extra["decode_C4"] = bench_decode(max(a.steps, 20), max(3, a.warmup),
-                                                  cpu_seqs=4 if cpu_on else 0)
+                                                  cpu_seqs=16 if cpu_on else 0)
             elif name == "varlen":
                 extra["varlen_C5"] = bench_varlen(max(20, a.steps), max(3, a.warmup),
-                                                  cpu_heads=1 if cpu_on else 0)
+                                                  cpu_heads=4 if cpu_on else 0)
             log(f"[bench] extra {name} done")
         except RuntimeError as e:
             extra[name] = {"error": str(e)[:300]}

@@ -84,8 +84,11 @@ __device__ __forceinline__ V bitcast(U u) {
 // 16j + 0..7 in lane hh = 0 and 16j + 8..15 in lane hh = 1: each row goes out in 16-byte stores,
 // 32 contiguous bytes per row and instruction, instead of 8-byte ones. Every lane executes the
 // swaps; `ok` (the same for both lanes of a row) only guards the stores.
+// `ncols` (default: all 32) stores only the block's columns below it: a head dim that is not a
+// multiple of 32 (a multiple of 8) ends inside a block.
 template <typename T>
-__device__ __forceinline__ void store_cblock(T* dst, const f32x16& acc, float scale, int hh, bool ok) {
+__device__ __forceinline__ void store_cblock(T* dst, const f32x16& acc, float scale, int hh, bool ok,
+                                             int ncols = 32) {
   using V4 = typename Dt<T>::V4;
 #pragma unroll
   for (int j = 0; j < 2; j++) {
@@ -99,7 +102,7 @@ __device__ __forceinline__ void store_cblock(T* dst, const f32x16& acc, float sc
     const auto r0 = __builtin_amdgcn_permlane32_swap(xd[0], yd[0], false, false);
     const auto r1 = __builtin_amdgcn_permlane32_swap(xd[1], yd[1], false, false);
     const u32x4 o = {r0[0], r1[0], r0[1], r1[1]};
-    if (ok) *(u32x4*)(dst + 16 * j + 8 * hh) = o;
+    if (ok && 16 * j + 8 * hh < ncols) *(u32x4*)(dst + 16 * j + 8 * hh) = o;
   }
 }
 

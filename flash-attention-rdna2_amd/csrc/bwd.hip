@@ -15,7 +15,7 @@
 //     S = Q.K^T and dP = dO.V^T; P and dS stay in registers as B operands of
 //     dV^T += dO^T.P and dK^T += Q^T.dS (dO^T/Q^T by transposing LDS reads).
 // On that recomputing path S and dP are computed in both kernels (the price of no atomics, as in
-// the reference). With a dS workspace (FableBwdParams.ds_ws, fp16/bf16 at head_dim 64/128) the order
+// the reference). With a dS workspace (FableBwdParams.ds_ws, fp16/bf16 at head dims up to 128) the order
 // is instead: a rowsum kernel for D, the dK/dV kernel, which also stores each dS tile once, and
 // a dQ kernel that forms dQ = dS.K from the stored tiles; every product is computed once, still
 // without atomics and in a fixed order.
@@ -100,13 +100,16 @@ bwd_dq_kernel(FableBwdParams p, int nqt) {
   const int kstart = (bk0 / C::BC) * C::BC;
   const int ntiles = bk1 > bk0 ? (bk1 - kstart + C::BC - 1) / C::BC : 0;
 
-  // Q, dO rows as B operands; D = rowsum(O*dO)
+  // Q, dO rows as B operands; D = rowsum(O*dO). A head dim p.D below C::HD (a multiple of 8)
+  // runs with zero columns p.D..C::HD-1 in every operand (they add nothing to any product) and
+  // stores only the first p.D columns.
+  const int HDr = p.D;
   V8 qreg[C::NDS], doreg[C::NDS];
   float dpart = 0.0f;
 #pragma unroll
   for (int ds = 0; ds < C::NDS; ds++) {
     const int d0 = 16 * ds + 8 * hh;
-    if (qi < SQ) {
+    if (qi < SQ && d0 < HDr) {
       qreg[ds] = *(const V8*)(Qg + (long long)qi * p.qs.s + d0);
       doreg[ds] = *(const V8*)(dOg + (long long)qi * p.dos.s + d0);
       const V8 o = *(const V8*)(Og + (long long)qi * p.os.s + d0);
@@ -136,11 +139,15 @@ bwd_dq_kernel(FableBwdParams p, int nqt) {
   const bool kloader = wave < C::NW / 2;
   const int lt = kloader ? tid : tid - C::HALF;
   const long long sstride = kloader ? p.ks.s : p.vs.s;
+  // chunks in the zero columns (>= p.D) load the row's first chunk and are replaced by zeros
+  const bool padded = HDr < C::HD;
   int voff[C::PER];
+  bool cok[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
     const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
-    voff[j] = r * (int)(sstride * 2) + 16 * c;
+    cok[j] = 8 * c < HDr;
+    voff[j] = r * (int)(sstride * 2) + (cok[j] ? 16 * c : 0);
   }
   u32x4 ld[C::PER];
   auto gload = [&](int kb) {
@@ -148,6 +155,10 @@ bwd_dq_kernel(FableBwdParams p, int nqt) {
                             : buf_rsrc(Vg + (long long)kb * p.vs.s, (long long)(SK - kb) * p.vs.s * 2);
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(rs, voff[j]);
+    if (padded) {
+#pragma unroll
+      for (int j = 0; j < C::PER; j++) ld[j] = cok[j] ? ld[j] : u32x4{0, 0, 0, 0};
+    }
   };
   auto lstore = [&](int stage) {
     T* base = lds + stage * C::STAGE + (kloader ? 0 : C::KT);
@@ -237,7 +248,8 @@ bwd_dq_kernel(FableBwdParams p, int nqt) {
   {
     T* row = dQg + (long long)qi * p.dqs.s;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++) store_cblock<T>(row + dbase + 32 * db, dqacc[db], p.scale, hh, qi < SQ);
+    for (int db = 0; db < C::NDB; db++)
+      store_cblock<T>(row + dbase + 32 * db, dqacc[db], p.scale, hh, qi < SQ, HDr - dbase - 32 * db);
   }
 }
 
@@ -285,11 +297,13 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
   const int kw = kb0 + 32 * wave, key = kw + l32;
   const bool wave_keys = kw < SK;
 
+  // a head dim p.D below C::HD runs with zero columns (see bwd_dq_kernel)
+  const int HDr = p.D;
   V8 kreg[C::NDS], vreg[C::NDS];
 #pragma unroll
   for (int ds = 0; ds < C::NDS; ds++) {
     const int d0 = 16 * ds + 8 * hh;
-    if (key < SK) {
+    if (key < SK && d0 < HDr) {
       kreg[ds] = *(const V8*)(Kg + (long long)key * p.ks.s + d0);
       vreg[ds] = *(const V8*)(Vg + (long long)key * p.vs.s + d0);
     } else {
@@ -316,11 +330,14 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
   // unconditionally (clamped row) and turned into log2-domain LSE / D at store time.
   static_assert((C::BQ * C::DCH) % C::NT == 0, "Q/dO slot split");
   constexpr int QJ = C::BQ * C::DCH / C::NT;
+  const bool padded = HDr < C::HD;  // zero-column chunks: first chunk loaded, zeros stored
   int voff[C::PER];
+  bool cok[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
     const int ci = tid + (j < QJ ? j : j - QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
-    voff[j] = r * (int)((j < QJ ? p.qs.s : p.dos.s) * 2) + 16 * c;
+    cok[j] = 8 * c < HDr;
+    voff[j] = r * (int)((j < QJ ? p.qs.s : p.dos.s) * 2) + (cok[j] ? 16 * c : 0);
   }
   u32x4 ld[C::PER];
   float lraw = 0.0f;
@@ -336,6 +353,10 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
                              rows * p.dos.s * 2);
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(j < QJ ? rq : rd, voff[j]);
+    if (padded) {
+#pragma unroll
+      for (int j = 0; j < C::PER; j++) ld[j] = cok[j] ? ld[j] : u32x4{0, 0, 0, 0};
+    }
     const int q = qt0 + (rsel % C::BQ);
     lok = it < total && q < SQ;
     const long long ri = (long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + min(q, SQ - 1);
@@ -435,8 +456,8 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
     T* vrow = (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (sq.ko + key) * p.dvs.s;
 #pragma unroll
     for (int db = 0; db < C::NDB; db++) {
-      store_cblock<T>(krow + dbase + 32 * db, dkacc[db], p.scale, hh, key < SK);
-      store_cblock<T>(vrow + dbase + 32 * db, dvacc[db], 1.0f, hh, key < SK);
+      store_cblock<T>(krow + dbase + 32 * db, dkacc[db], p.scale, hh, key < SK, HDr - dbase - 32 * db);
+      store_cblock<T>(vrow + dbase + 32 * db, dvacc[db], 1.0f, hh, key < SK, HDr - dbase - 32 * db);
     }
   }
 }
@@ -506,11 +527,13 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   const T* Rg = dpw ? (const T*)p.V + (long long)b * p.vs.b + sq.ko * p.vs.s + (long long)kvh * p.vs.h
                     : (const T*)p.K + (long long)b * p.ks.b + sq.ko * p.ks.s + (long long)kvh * p.ks.h;
   const long long rstride = dpw ? p.vs.s : p.ks.s;
+  // a head dim p.D below C::HD runs with zero columns (see bwd_dq_kernel)
+  const int HDr = p.D;
   V8 kv[C::NDS];
 #pragma unroll
   for (int ds = 0; ds < C::NDS; ds++)
-    kv[ds] = key < SK ? *(const V8*)(Rg + (long long)key * rstride + 16 * ds + 8 * hh)
-                      : bitcast<V8>(u32x4{0, 0, 0, 0});
+    kv[ds] = key < SK && 16 * ds + 8 * hh < HDr ? *(const V8*)(Rg + (long long)key * rstride + 16 * ds + 8 * hh)
+                                                : bitcast<V8>(u32x4{0, 0, 0, 0});
   f32x16 acc[C::NDB];  // dV^T (S-wave) or dK^T (dP-wave)
 #pragma unroll
   for (int db = 0; db < C::NDB; db++) acc[db] = f32x16{};
@@ -526,11 +549,16 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   // Q/dO tiles through buffer descriptors over rows qt0..SQ-1 (rows past SQ read as zeros);
   // each thread's first QJ chunk slots are Q, the rest dO. LSE/D row values are loaded
   // unconditionally (clamped row) and turned into log2-domain LSE / D at store time.
+  // (NT is a multiple of DCH, so a thread's chunks all sit in column tid % DCH: one test for
+  // the zero columns, whose chunks load the row's first chunk and are replaced by zeros)
+  static_assert(C::NT % C::DCH == 0, "one column per thread");
+  const bool cok = 8 * (tid % C::DCH) < HDr;
+  const bool zcol = !cok;
   int voff[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
     const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
-    voff[j] = r * (int)((j < C::QJ ? p.qs.s : p.dos.s) * 2) + 16 * c;
+    voff[j] = r * (int)((j < C::QJ ? p.qs.s : p.dos.s) * 2) + (cok ? 16 * c : 0);
   }
   // NSET register sets: tile it+NSET is loaded while tile it+1 (loaded NSET-1 iterations
   // earlier) is stored, so every global load has NSET iterations to land
@@ -559,6 +587,10 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     const auto rd = buf_rsrc(g_do, in ? g_doleft : 0);
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(j < C::QJ ? rq : rd, voff[j]);
+    if (zcol) {
+#pragma unroll
+      for (int j = 0; j < C::PER; j++) ld[S][j] = u32x4{0, 0, 0, 0};
+    }
     const int qr = qstart + g_qi * C::BQ + (rsel % C::BQ);
     lok[S] = in && qr < SQ;
     // unconditional (clamped row; SQ >= 1 whenever the loop runs), so the memory waits of
@@ -775,7 +807,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
                  : (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (sq.ko + key) * p.dvs.s;
     const float sc = dpw ? p.scale : 1.0f;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++) store_cblock<T>(row + 32 * db, acc[db], sc, hh, key < SK);
+    for (int db = 0; db < C::NDB; db++) store_cblock<T>(row + 32 * db, acc[db], sc, hh, key < SK, HDr - 32 * db);
   }
 }
 
@@ -794,8 +826,10 @@ __global__ __launch_bounds__(256) void bwd_dsum_kernel(FableBwdParams p, int rbl
   const BwdSeq sq = bwd_seq(p, b);
   if (sq.SQ <= 0) return;
   const int c = tid % LPR;
-  const T* ob = (const T*)p.O + (long long)b * p.os.b + (long long)h * p.os.h + 8 * c;
-  const T* db = (const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + 8 * c;
+  // chunks past a head dim p.D below HD read the row's first chunk and add nothing
+  const bool cok = 8 * c < p.D;
+  const T* ob = (const T*)p.O + (long long)b * p.os.b + (long long)h * p.os.h + (cok ? 8 * c : 0);
+  const T* db = (const T*)p.dO + (long long)b * p.dos.b + (long long)h * p.dos.h + (cok ? 8 * c : 0);
   V8 o[DSUM_RPT], d[DSUM_RPT];
 #pragma unroll
   for (int r = 0; r < DSUM_RPT; r++) {
@@ -810,6 +844,7 @@ __global__ __launch_bounds__(256) void bwd_dsum_kernel(FableBwdParams p, int rbl
     float acc = 0.0f;
 #pragma unroll
     for (int e = 0; e < 8; e++) acc += (float)o[r][e] * (float)d[r][e];
+    acc = cok ? acc : 0.0f;
 #pragma unroll
     for (int m = LPR / 2; m > 0; m >>= 1) acc += __shfl_xor(acc, m);
     if (c == 0 && q < sq.SQ) p.dsum[(long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + q] = acc;
@@ -917,11 +952,17 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
     d_kb32 += C::NKB;
   };
 
+  // a head dim p.D below C::HD runs with zero columns (see bwd_dq_kernel); NT is a multiple of
+  // DCH, so a thread's chunks all sit in column tid % DCH
+  static_assert(C::NT % C::DCH == 0, "one column per thread");
+  const int HDr = p.D;
+  const bool cok = 8 * (tid % C::DCH) < HDr;
+  const bool zcol = !cok;
   int voff[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
     const int idx = tid + j * C::NT, r = idx / C::DCH, c = idx % C::DCH;
-    voff[j] = r * (int)(p.ks.s * 2) + 16 * c;
+    voff[j] = r * (int)(p.ks.s * 2) + (cok ? 16 * c : 0);
   }
   u32x4 ld[NS][C::PER];
   const T* k_ptr = Kg + (long long)kstart * p.ks.s;
@@ -932,6 +973,10 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
     const auto rs = buf_rsrc(k_ptr, k_left);  // past the last tile the descriptor is empty: zeros
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(rs, voff[j]);
+    if (zcol) {
+#pragma unroll
+      for (int j = 0; j < C::PER; j++) ld[S][j] = u32x4{0, 0, 0, 0};
+    }
     k_ptr += k_step;
     k_left -= 2 * k_step;
   };
@@ -1020,7 +1065,7 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
   {
     T* row = dQg + (long long)qi * p.dqs.s;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++) store_cblock<T>(row + 32 * db, dqacc[db], p.scale, hh, qi < SQ);
+    for (int db = 0; db < C::NDB; db++) store_cblock<T>(row + 32 * db, dqacc[db], p.scale, hh, qi < SQ, HDr - 32 * db);
   }
 }
 
@@ -1089,20 +1134,26 @@ static int launch_bwd(const FableBwdParams& p, hipStream_t st) {
   return feat ? launch_bwd2<T, CQ, CKV, false, true>(p, st) : launch_bwd2<T, CQ, CKV, false, false>(p, st);
 }
 
+// kernel width for head dim D (a multiple of 8 up to 256): the columns past D are zero
+static int bwd_width(int D) { return D <= 64 ? 64 : (D <= 128 ? 128 : 256); }
+
 template <typename T>
 static int bwd_dispatch(const FableBwdParams& p, hipStream_t st) {
-  switch (p.D) {
+  if (p.D <= 0 || p.D > 256 || p.D % 8)
+    return fail(FA_ERR_HEADDIM, "fable_attn_bwd: head_dim=%d has no kernel (multiples of 8 up to 256)", p.D);
+  switch (bwd_width(p.D)) {
     case 64: return launch_bwd<T, BwdQCfg<64, 64, 4, 2>, BwdKVPCfg<64, 2, 3>>(p, st);
     case 128: return launch_bwd<T, BwdQCfg<128, 32, 4, 2>, BwdKVPCfg<128, 4, 2>>(p, st);
-    case 256: return launch_bwd<T, BwdQCfg<256, 32, 4, 1, 2>, BwdKVCfg<256, 4, 1, 4>>(p, st);
-    default: return fail(FA_ERR_HEADDIM, "fable_attn_bwd: head_dim=%d has no kernel (64, 128, 256)", p.D);
+    default: return launch_bwd<T, BwdQCfg<256, 32, 4, 1, 2>, BwdKVCfg<256, 4, 1, 4>>(p, st);
   }
 }
 
 }  // namespace fa
 
 extern "C" int64_t fable_attn_bwd_ds_bytes(FableBwdParams p, int dtype) {
-  if ((dtype != FA_F16 && dtype != FA_BF16) || (p.D != 64 && p.D != 128) || p.B <= 0 || p.Hq <= 0) return 0;
+  if ((dtype != FA_F16 && dtype != FA_BF16) || p.D <= 0 || p.D % 8 || fa::bwd_width(p.D) > 128 || p.B <= 0 ||
+      p.Hq <= 0)
+    return 0;
   return fa::ds_bytes(p);
 }
 

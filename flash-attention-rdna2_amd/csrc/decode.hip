@@ -81,17 +81,21 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
 
   // ---- q rows of this head group -> LDS (fp32): one 16-byte load per thread and chunk,
   // head index clamped (rows past the group are zeroed after the load)
-  const T* qg = (const T*)p.q + ((long long)(b * p.nq + tk) * p.NH + h0) * HD;
+  // A head dim HDr = p.HD below the kernel width HD (a multiple of 8) runs with zero columns
+  // HDr..HD-1 in q, K and V (rows in memory are HDr long); only HDr output columns are kept.
+  const int HDr = p.HD;
+  const T* qg = (const T*)p.q + ((long long)(b * p.nq + tk) * p.NH + h0) * HDr;
   for (int i = tid; i < 16 * RCH; i += 256) {
     const int g = i / RCH, c = i % RCH;
-    const u32x4 raw = *(const u32x4*)(qg + (long long)min(g, hg - 1) * HD + 8 * c);
+    const bool cok = 8 * c < HDr;
+    const u32x4 raw = *(const u32x4*)(qg + (long long)min(g, hg - 1) * HDr + (cok ? 8 * c : 0));
     const V8 v = bitcast<V8>(raw);
 #pragma unroll
-    for (int e = 0; e < 8; e++) qsh[g][8 * c + e] = g < hg ? (float)v[e] : 0.0f;
+    for (int e = 0; e < 8; e++) qsh[g][8 * c + e] = g < hg && cok ? (float)v[e] : 0.0f;
   }
   __syncthreads();
   if (p.rotary) {
-    const int rdim = p.rotary_dim > 0 ? p.rotary_dim : HD, half = rdim / 2;
+    const int rdim = p.rotary_dim > 0 ? p.rotary_dim : HDr, half = rdim / 2;
     const int rp = (p.rotary_pos ? p.rotary_pos[b] : p.ctx_len[b]) + tk;
     for (int i = tid; i < hg * half; i += 256) {
       const int g = i / half, j = i % half;
@@ -146,8 +150,16 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
     for (int i = 0; i < NVI; i++) vblk[i] = bt[vkey(kc0, i) >> page_shift];
   };
   auto row_off = [&](int blk, int key) -> long long {
-    return (((long long)blk * p.page + (key & pmask)) * NKV + kvh) * HD;
+    return (((long long)blk * p.page + (key & pmask)) * NKV + kvh) * HDr;
   };
+  // 16-byte chunks in the zero columns load the row's first chunk and are replaced by zeros
+  const bool padded = HDr < HD;
+  bool kok[NDS];
+#pragma unroll
+  for (int ds = 0; ds < NDS; ds++) kok[ds] = 32 * ds + 8 * lg < HDr;
+  bool vok[NVI];
+#pragma unroll
+  for (int i = 0; i < NVI; i++) vok[i] = 8 * ((64 * i + lane) % RCH) < HDr;
   // K/V rows of the chunk at kc0: K as the A operand (key kc0 + 16*kb + lh, head-dim
   // 32*ds + 8*lg); V load i covers row (64i + lane) / RCH, 16-byte chunk (64i + lane) % RCH
   // The cache rows are read once per step: non-temporal loads keep them from displacing the
@@ -157,12 +169,21 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
     for (int kb = 0; kb < 2; kb++) {
       const long long base = row_off(kblk[kb], kkey(kc0, kb));
 #pragma unroll
-      for (int ds = 0; ds < NDS; ds++) kr[kb][ds] = __builtin_nontemporal_load((const u32x4*)(Kc + base + 32 * ds + 8 * lg));
+      for (int ds = 0; ds < NDS; ds++)
+        kr[kb][ds] = __builtin_nontemporal_load((const u32x4*)(Kc + base + (kok[ds] ? 32 * ds + 8 * lg : 0)));
     }
 #pragma unroll
     for (int i = 0; i < NVI; i++) {
       const int ch = (64 * i + lane) % RCH;
-      vr[i] = __builtin_nontemporal_load((const u32x4*)(Vc + row_off(vblk[i], vkey(kc0, i)) + 8 * ch));
+      vr[i] = __builtin_nontemporal_load((const u32x4*)(Vc + row_off(vblk[i], vkey(kc0, i)) + (vok[i] ? 8 * ch : 0)));
+    }
+    if (padded) {
+#pragma unroll
+      for (int kb = 0; kb < 2; kb++)
+#pragma unroll
+        for (int ds = 0; ds < NDS; ds++) kr[kb][ds] = kok[ds] ? kr[kb][ds] : u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int i = 0; i < NVI; i++) vr[i] = vok[i] ? vr[i] : u32x4{0, 0, 0, 0};
     }
   };
   // Software pipeline: the rows of the next chunk are in flight while this one is computed;
@@ -291,8 +312,8 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
 #pragma unroll
     for (int r = 0; r < 4; r++) red_o[(wave * 16 + lh) * HD + 16 * db + 4 * lg + r] = oacc[db][r];
   __syncthreads();
-  for (int i = tid; i < hg * HD; i += 256) {
-    const int g = i / HD, d = i % HD;
+  for (int i = tid; i < hg * HDr; i += 256) {
+    const int g = i / HDr, d = i % HDr;
     float gm = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kDecWaves; w++) gm = fmaxf(gm, red_m[w][g]);
@@ -305,7 +326,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
         acc += f * red_o[(w * 16 + g) * HD + d];
       }
     }
-    float* out = p.scratch + (((long long)(b * p.nq + tk) * p.NH + h0 + g) * p.nsplit + sp) * (HD + 2);
+    float* out = p.scratch + (((long long)(b * p.nq + tk) * p.NH + h0 + g) * p.nsplit + sp) * (HDr + 2);
     if (d == 0) {
       out[0] = gm;
       out[1] = l;
@@ -481,21 +502,23 @@ __global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, 
 // merge nsplit partials of one (token, head): grid (batch*nq, NH), block HD
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void dec_combine_kernel(FableDecParams p) {
-  const int row = blockIdx.x, h = blockIdx.y, d = threadIdx.x;
-  const float* base = p.scratch + ((long long)row * p.NH + h) * p.nsplit * (HD + 2);
+  // one thread per column of the kernel width HD; the head dim p.HD <= HD sets the strides
+  const int row = blockIdx.x, h = blockIdx.y, d = threadIdx.x, HDr = p.HD;
+  const int dc = min(d, HDr - 1);  // threads past the head dim read a valid column, store nothing
+  const float* base = p.scratch + ((long long)row * p.NH + h) * p.nsplit * (HDr + 2);
   float gm = -INFINITY;
-  for (int s = 0; s < p.nsplit; s++) gm = fmaxf(gm, base[(long long)s * (HD + 2)]);
+  for (int s = 0; s < p.nsplit; s++) gm = fmaxf(gm, base[(long long)s * (HDr + 2)]);
   float l = 0.0f, acc = 0.0f;
   if (gm != -INFINITY) {
     for (int s = 0; s < p.nsplit; s++) {
-      const float* ps = base + (long long)s * (HD + 2);
+      const float* ps = base + (long long)s * (HDr + 2);
       const float w = exp2_fast(ps[0] - gm);
       l += w * ps[1];
-      acc += w * ps[2 + d];
+      acc += w * ps[2 + dc];
     }
   }
   const bool ok = gm != -INFINITY && l > 0.0f;
-  ((T*)p.o)[((long long)row * p.NH + h) * HD + d] = (T)(ok ? acc / l : 0.0f);
+  if (d < HDr) ((T*)p.o)[((long long)row * p.NH + h) * HDr + d] = (T)(ok ? acc / l : 0.0f);
   if (p.lse_out && d == 0) p.lse_out[(long long)row * p.NH + h] = ok ? gm * kLn2 + __logf(l) : -INFINITY;
 }
 
@@ -503,15 +526,16 @@ __global__ __launch_bounds__(256) void dec_combine_kernel(FableDecParams p) {
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void dec_append_kernel(FableDecParams p, const T* nk, const T* nv, int page_shift) {
   __shared__ float ks[HD];
+  // one thread per column of the kernel width HD; rows are p.HD <= HD long
   const int b = blockIdx.x / p.nq, tk = blockIdx.x % p.nq, kvh = blockIdx.y, d = threadIdx.x;
-  const int NKV = p.NH / p.gqa;
+  const int NKV = p.NH / p.gqa, HDr = p.HD;
   const int pos = p.ctx_len[b] + tk;
-  const bool ok = pos >= 0 && (pos >> page_shift) < p.max_blocks;
-  const long long src = ((long long)(b * p.nq + tk) * NKV + kvh) * HD;
-  ks[d] = (float)nk[src + d];
+  const bool ok = pos >= 0 && (pos >> page_shift) < p.max_blocks && d < HDr;
+  const long long src = ((long long)(b * p.nq + tk) * NKV + kvh) * HDr;
+  ks[d] = d < HDr ? (float)nk[src + d] : 0.0f;
   __syncthreads();
   if (p.rotary) {
-    const int rdim = p.rotary_dim > 0 ? p.rotary_dim : HD, half = rdim / 2;
+    const int rdim = p.rotary_dim > 0 ? p.rotary_dim : HDr, half = rdim / 2;
     const int rp = (p.rotary_pos ? p.rotary_pos[b] : p.ctx_len[b]) + tk;
     const bool act = d < half;
     const int ia = p.rotary == 1 ? d : 2 * d, ib = p.rotary == 1 ? d + half : 2 * d + 1;
@@ -531,7 +555,7 @@ __global__ __launch_bounds__(256) void dec_append_kernel(FableDecParams p, const
   }
   if (!ok) return;
   const int blk = p.block_table[(long long)b * p.max_blocks + (pos >> page_shift)];
-  const long long dst = (((long long)blk * p.page + (pos & (p.page - 1))) * NKV + kvh) * HD + d;
+  const long long dst = (((long long)blk * p.page + (pos & (p.page - 1))) * NKV + kvh) * HDr + d;
   ((T*)p.Kc)[dst] = (T)ks[d];
   ((T*)p.Vc)[dst] = nv[src + d];
 }
@@ -564,14 +588,19 @@ static int launch_dec(const FableDecParams& p, hipStream_t st, const void* nk, c
   return launch_status("fable_attn_dec (combine)");
 }
 
+// fp16/bf16: every head dim that is a multiple of 8 up to 256 runs in the kernel of width 64,
+// 128 or 256 with zero columns past it. The loads skip those columns' bytes, so HBM traffic is
+// that of the real head dim; only matrix-core work, which does not bound decode, grows.
+// fp32 has kernels for 64, 128 and 256 exactly.
 template <typename T>
 static int dec_dispatch(const FableDecParams& p, hipStream_t st, const void* nk, const void* nv) {
-  switch (p.HD) {
-    case 64: return launch_dec<T, 64>(p, st, nk, nv);
-    case 128: return launch_dec<T, 128>(p, st, nk, nv);
-    case 256: return launch_dec<T, 256>(p, st, nk, nv);
-    default: return fail(FA_ERR_HEADDIM, "fable_attn_dec: head_dim=%d has no kernel (64, 128, 256)", p.HD);
-  }
+  constexpr bool f32 = std::is_same<T, float>::value;
+  if (p.HD <= 0 || p.HD > 256 || p.HD % 8 || (f32 && p.HD != 64 && p.HD != 128 && p.HD != 256))
+    return fail(FA_ERR_HEADDIM, "fable_attn_dec: head_dim=%d has no kernel (%s)", p.HD,
+                f32 ? "64, 128, 256 for fp32" : "multiples of 8 up to 256");
+  if (p.HD <= 64) return launch_dec<T, 64>(p, st, nk, nv);
+  if (p.HD <= 128) return launch_dec<T, 128>(p, st, nk, nv);
+  return launch_dec<T, 256>(p, st, nk, nv);
 }
 
 }  // namespace fa

@@ -76,10 +76,15 @@ __device__ __forceinline__ bool fwd_visible(const FableFwdParams& p, int i, int 
   return ok;
 }
 
-// the fp16/bf16 forward per head dim (fwd_d64/128/256.hip) and the fp32 forward (fwd_f32.hip),
-// dispatched from fable_attn_fwd
+// the fp16/bf16 forward per kernel width (fwd_d32 ... fwd_d256.hip: head dims up to the width,
+// in steps of 8) and the fp32 forward (fwd_f32.hip), dispatched from fable_attn_fwd
+int launch_fwd_d32(const FableFwdParams& p, int dtype, hipStream_t st);
 int launch_fwd_d64(const FableFwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_d96(const FableFwdParams& p, int dtype, hipStream_t st);
 int launch_fwd_d128(const FableFwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_d160(const FableFwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_d192(const FableFwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_d224(const FableFwdParams& p, int dtype, hipStream_t st);
 int launch_fwd_d256(const FableFwdParams& p, int dtype, hipStream_t st);
 int launch_fwd_f32(const FableFwdParams& p, hipStream_t st);
 

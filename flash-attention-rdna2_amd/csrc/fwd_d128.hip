@@ -1,5 +1,5 @@
-// fwd_d128.hip — the fp16/bf16 forward kernels for head_dim 128 (workgroup shapes C, CF, CN, CS
-// of launch_fwd in fwd_kernel.hpp).
+// fwd_d128.hip — the fp16/bf16 forward kernels of width 128 (head dims 104..128 in steps of 8, the
+// columns past the head dim zero; workgroup shapes C, CF, CN, CS of launch_fwd in fwd_kernel.hpp).
 #include "fwd_kernel.hpp"
 
 namespace fa {

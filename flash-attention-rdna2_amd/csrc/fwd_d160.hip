@@ -1,0 +1,12 @@
+// fwd_d160.hip — the fp16/bf16 forward kernels of width 160 (head dims 136..160 in steps of 8, the
+// columns past the head dim zero; workgroup shapes C, CF, CN of launch_fwd in fwd_kernel.hpp).
+#include "fwd_kernel.hpp"
+
+namespace fa {
+
+int launch_fwd_d160(const FableFwdParams& p, int dtype, hipStream_t st) {
+  if (dtype == FA_F16) return launch_fwd<_Float16, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 2, 1>>(p, st);
+  return launch_fwd<__bf16, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 2, 1>>(p, st);
+}
+
+}  // namespace fa

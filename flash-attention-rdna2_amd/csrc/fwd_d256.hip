@@ -1,5 +1,5 @@
-// fwd_d256.hip — the fp16/bf16 forward kernels for head_dim 256 (workgroup shapes C, CF, CN of
-// launch_fwd in fwd_kernel.hpp).
+// fwd_d256.hip — the fp16/bf16 forward kernels of width 256 (head dims 232..256 in steps of 8, the
+// columns past the head dim zero; workgroup shapes C, CF, CN of launch_fwd in fwd_kernel.hpp).
 #include "fwd_kernel.hpp"
 
 namespace fa {

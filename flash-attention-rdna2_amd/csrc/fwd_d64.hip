@@ -1,5 +1,5 @@
-// fwd_d64.hip — the fp16/bf16 forward kernels for head_dim 64 (workgroup shapes C, CF, CN, CS of
-// launch_fwd in fwd_kernel.hpp).
+// fwd_d64.hip — the fp16/bf16 forward kernels of width 64 (head dims 40..64 in steps of 8, the
+// columns past the head dim zero; workgroup shapes C, CF, CN, CS of launch_fwd in fwd_kernel.hpp).
 #include "fwd_kernel.hpp"
 
 namespace fa {

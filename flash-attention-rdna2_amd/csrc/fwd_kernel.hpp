@@ -56,10 +56,9 @@ struct FwdCfg {
   static constexpr int KTILE = BC * KSTR;
   static constexpr int VTILE = BC * VSTR;
   static constexpr int KCH = BC * DCH;      // chunks per K (or V) tile
-  static constexpr int KJ = KCH / NT;       // chunks each thread loads per K (or V) tile
-  static constexpr int RSTEP = NT / DCH;    // rows between a thread's chunks
+  static constexpr int KJ = (KCH + NT - 1) / NT;  // chunks each thread loads per K (or V) tile
+  static constexpr bool KTAIL = KCH % NT != 0;    // the last round leaves some threads idle
   static_assert(HD % 32 == 0 && BC % 32 == 0, "shape");
-  static_assert(KCH % NT == 0 && NT % DCH == 0, "loader split");
 };
 
 template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
@@ -113,14 +112,18 @@ fwd_kernel(FableFwdParams p, int nqt) {
   const int kstart = (bk0 / C::BC) * C::BC;
   const int ntiles = bk1 > bk0 ? (bk1 - kstart + C::BC - 1) / C::BC : 0;
 
-  // ---- Q (B operands) in registers: lane holds query qw + 32i + l32, head-dim 16ds + 8hh..+7
+  // ---- Q (B operands) in registers: lane holds query qw + 32i + l32, head-dim 16ds + 8hh..+7.
+  // A head dim p.HD below the kernel's C::HD (a multiple of 8) runs with zero columns
+  // p.HD..C::HD-1 in Q, K and V: they add nothing to q.k, and the O columns they produce are
+  // not stored.
+  const int HDr = p.HD;
   V8 qreg[QB][C::NDS];
 #pragma unroll
   for (int i = 0; i < QB; i++) {
     const int qi = qw + 32 * i + l32;
 #pragma unroll
     for (int ds = 0; ds < C::NDS; ds++) {
-      if (qi < SQ)
+      if (qi < SQ && 16 * ds + 8 * hh < HDr)
         qreg[i][ds] = *(const V8*)(Qg + (long long)qi * p.sQ.s + 16 * ds + 8 * hh);
       else
         qreg[i][ds] = bitcast<V8>(u32x4{0, 0, 0, 0});
@@ -174,36 +177,65 @@ fwd_kernel(FableFwdParams p, int nqt) {
   // per-lane condition (a conditional load would make the compiler wait for it at once), and
   // the per-lane byte offsets are loop invariant.
   const int kvalid = min(SK, kstart + ntiles * C::BC);
-  int koff[C::KJ], voff[C::KJ];
+  // chunk j of this thread: ci = tid + j*NT, row ci / DCH, 16-byte column chunk ci % DCH. In the
+  // last round (KTAIL) threads past the tile's chunks load row 0 again and store nothing;
+  // chunks in the zero columns (>= p.HD) are loaded from the row's first chunk and replaced by
+  // zeros (`padded`, uniform), so no load depends on a lane condition.
+  // When NT is a multiple of DCH (every shape whose head dim is a power of two) a thread's
+  // chunks share one column and sit RSTEP rows apart, so the LDS addresses are one base plus
+  // immediate offsets; other shapes keep one address per chunk.
+  constexpr bool kRowStep = C::NT % C::DCH == 0 && !C::KTAIL;
+  constexpr int RSTEP = kRowStep ? C::NT / C::DCH : 0;
+  const bool padded = HDr < C::HD;
+  int koff[C::KJ], voff[C::KJ], lko[C::KJ], lvo[C::KJ];
+  bool cok[C::KJ];
 #pragma unroll
   for (int j = 0; j < C::KJ; j++) {
     const int ci = tid + j * C::NT;
-    const int r = ci / C::DCH, c = ci % C::DCH;
-    koff[j] = r * (int)(p.sK.s * 2) + 16 * c;
-    voff[j] = r * (int)(p.sV.s * 2) + 16 * c;
+    const bool live = !C::KTAIL || ci < C::KCH;
+    const int r = live ? ci / C::DCH : 0, c = live ? ci % C::DCH : 0;
+    cok[j] = 8 * c < HDr;
+    const int cg = cok[j] ? c : 0;
+    koff[j] = r * (int)(p.sK.s * 2) + 16 * cg;
+    voff[j] = r * (int)(p.sV.s * 2) + 16 * cg;
+    if constexpr (kRowStep) {
+      lko[j] = (tid / C::DCH) * C::KSTR + 8 * (tid % C::DCH) + j * RSTEP * C::KSTR;
+      lvo[j] = (tid / C::DCH) * C::VSTR + 8 * (tid % C::DCH) + j * RSTEP * C::VSTR;
+    } else {
+      lko[j] = live ? r * C::KSTR + 8 * c : -1;
+      lvo[j] = live ? r * C::VSTR + 8 * c : -1;
+    }
   }
-  const int lrow = tid / C::DCH, lch = tid % C::DCH;
-  const int lko = lrow * C::KSTR + 8 * lch, lvo = lrow * C::VSTR + 8 * lch;
   u32x4 ldk[C::KJ], ldv[C::KJ];
   auto gload_k = [&](int kb) {
     const auto r = buf_rsrc(Kg + (long long)kb * p.sK.s, (long long)(kvalid - kb) * p.sK.s * 2);
 #pragma unroll
     for (int j = 0; j < C::KJ; j++) ldk[j] = buf_load16(r, koff[j]);
+    if (padded) {
+#pragma unroll
+      for (int j = 0; j < C::KJ; j++) ldk[j] = cok[j] ? ldk[j] : u32x4{0, 0, 0, 0};
+    }
   };
   auto gload_v = [&](int kb) {
     const auto r = buf_rsrc(Vg + (long long)kb * p.sV.s, (long long)(kvalid - kb) * p.sV.s * 2);
 #pragma unroll
     for (int j = 0; j < C::KJ; j++) ldv[j] = buf_load16(r, voff[j]);
+    if (padded) {
+#pragma unroll
+      for (int j = 0; j < C::KJ; j++) ldv[j] = cok[j] ? ldv[j] : u32x4{0, 0, 0, 0};
+    }
   };
   auto lstore_k = [&](int st) {
-    T* b = kl + st * C::KTILE + lko;
+    T* b = kl + st * C::KTILE;
 #pragma unroll
-    for (int j = 0; j < C::KJ; j++) *(u32x4*)(b + j * C::RSTEP * C::KSTR) = ldk[j];
+    for (int j = 0; j < C::KJ; j++)
+      if (!C::KTAIL || j < C::KJ - 1 || lko[j] >= 0) *(u32x4*)(b + lko[j]) = ldk[j];
   };
   auto lstore_v = [&](int st) {
-    T* b = vl + st * C::VTILE + lvo;
+    T* b = vl + st * C::VTILE;
 #pragma unroll
-    for (int j = 0; j < C::KJ; j++) *(u32x4*)(b + j * C::RSTEP * C::VSTR) = ldv[j];
+    for (int j = 0; j < C::KJ; j++)
+      if (!C::KTAIL || j < C::KJ - 1 || lvo[j] >= 0) *(u32x4*)(b + lvo[j]) = ldv[j];
   };
 
   // S^T = K . Q^T for the K tile in stage st, every query block: lane reads key row
@@ -512,7 +544,8 @@ fwd_kernel(FableFwdParams p, int nqt) {
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     T* orow = Og + (long long)qi * p.sO.s;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++) store_cblock<T>(orow + db * 32, oacc[i][db], inv, hh, qi < SQ);
+    for (int db = 0; db < C::NDB; db++)
+      store_cblock<T>(orow + db * 32, oacc[i][db], inv, hh, qi < SQ, HDr - db * 32);
     if (qi < SQ) {
       if (p.LSE && hh == 0)
         p.LSE[sv.lse0 + qi] = l_tot > 0.0f ? m_run[i] * kLn2 + __logf(l_tot) : -INFINITY;

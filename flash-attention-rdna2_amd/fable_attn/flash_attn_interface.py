@@ -27,11 +27,12 @@ import torch
 
 from . import _C
 
-# head dims with kernels (fp16/bf16/fp32 forward, backward and decode); a head dim between
-# two of them runs in the next one with zero columns, which change neither q.k nor the kept
-# output columns
-KERNEL_HEAD_DIMS = (64, 128, 256)
-MAX_HEAD_DIM = KERNEL_HEAD_DIMS[-1]
+# Head dims the kernels take as they are: fp16/bf16 every multiple of 8 up to 256 (rows move in
+# 16-byte accesses; the kernels zero the columns up to their own width), fp32 64, 128 and 256.
+# Any other head dim is zero-padded to the next one it may use: zero columns change neither q.k
+# nor the kept output columns.
+MAX_HEAD_DIM = 256
+F32_HEAD_DIMS = (64, 128, 256)
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
@@ -95,8 +96,13 @@ class _Spec:
         return out if self.keep is None else out[..., :self.keep]
 
 
-def _kernel_width(d):
-    return next((w for w in KERNEL_HEAD_DIMS if w >= d), None)
+def _kernel_width(d, dtype):
+    """The head dim a call of head dim d runs at (None above MAX_HEAD_DIM)."""
+    if d > MAX_HEAD_DIM:
+        return None
+    if dtype == torch.float32:
+        return next(w for w in F32_HEAD_DIMS if w >= d)
+    return -(-d // 8) * 8
 
 
 def _with_width(t, d):
@@ -149,7 +155,7 @@ def _normalize(q, k, v, *, qv=None, softmax_scale=None, causal=False, window_siz
         # the reference scales by the concatenated width whenever qv or headdim_v != headdim
         softmax_scale = (d + dv) ** -0.5 if (qv is not None or dv != d) else d ** -0.5
     q, k, v, keep = _score_problem(q, k, v, qv)
-    w = _kernel_width(q.shape[-1])
+    w = _kernel_width(q.shape[-1], q.dtype)
     if w is None:
         raise ValueError(f"fable_attn: head_dim={q.shape[-1]} exceeds the maximum {MAX_HEAD_DIM}")
     if w != q.shape[-1]:
@@ -515,14 +521,14 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None,
     if qv is not None or v_cache.shape[-1] != k_cache.shape[-1]:
         # compat path: the score problem widened over the whole cache (one temporary copy)
         q, kc, vc, keep = _score_problem(q, k_cache, v_cache, qv)
-    w = _kernel_width(q.shape[-1])
+    w = _kernel_width(q.shape[-1], q.dtype)
     if w is None:
         raise ValueError(f"fable_attn: head_dim={q.shape[-1]} exceeds the maximum {MAX_HEAD_DIM}")
     if w != q.shape[-1]:
         if appending:
             raise NotImplementedError(
-                f"fable_attn: appending k/v needs a kernel head_dim; {q.shape[-1]} is not one of "
-                f"{KERNEL_HEAD_DIMS}")
+                f"fable_attn: appending k/v needs a head_dim the kernels take as it is (a multiple "
+                f"of 8 for fp16/bf16, 64/128/256 for fp32), got {q.shape[-1]}")
         keep = keep if keep is not None else vc.shape[-1]
         q, kc, vc = _with_width(q, w), _with_width(kc, w), _with_width(vc, w)
     _, wl, _ = _map_window(True, window_size)

@@ -6,9 +6,10 @@ it up by name (package/fable_attn/torch_op.py:27-71, registered at import, __ini
 q, k, v are [B, H, S, D] (the layout of F.scaled_dot_product_attention); the result is
 [B, H, S, D]. A shape or dtype the kernels cannot serve returns an EMPTY tensor instead of
 raising: callers test `numel() == 0` and take their own path, so an exception here would break
-their fallback (reference :27-48). Head dims without a kernel are zero-padded to the next one,
-as in flash_attn_func. Registration is idempotent and never raises (a failure is kept in
-LAST_ERROR); an operator of that name that already exists is left alone (reference :51-71).
+their fallback (reference :27-48). fp16/bf16 head dims run as they are when they are multiples
+of 8; others are zero-padded to the next multiple of 8, as in flash_attn_func. Registration is
+idempotent and never raises (a failure is kept in LAST_ERROR); an operator of that name that
+already exists is left alone (reference :51-71).
 """
 import torch
 
@@ -33,7 +34,7 @@ def _forward(q, k, v, scale, causal):
         return empty
     if q.shape[1] % k.shape[1] or k.shape[:3] != v.shape[:3] or q.shape[0] != k.shape[0]:
         return empty
-    dk = _kernel_width(D)
+    dk = _kernel_width(D, q.dtype)
     try:
         # kernel views: [B,H,S,D] with a contiguous, 16-byte aligned head_dim
         views = []

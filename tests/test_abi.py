@@ -102,9 +102,9 @@ def test_launchers_validate_before_device_work():
     assert lib.fable_attn_fwd(p, 0, None) == 3
     assert b"null" in lib.fable_attn_last_error()
     p.Q = p.K = p.V = p.O = 16    # never dereferenced: rejected on head_dim first
-    p.NH, p.gqa, p.batch, p.SQ, p.SK, p.HD = 4, 1, 1, 8, 8, 72
+    p.NH, p.gqa, p.batch, p.SQ, p.SK, p.HD = 4, 1, 1, 8, 8, 100
     assert lib.fable_attn_fwd(p, 0, None) == 2
-    assert b"head_dim=72" in lib.fable_attn_last_error()
+    assert b"head_dim=100" in lib.fable_attn_last_error()
     p.HD = 64
     assert lib.fable_attn_fwd(p, 7, None) == 1          # unknown dtype
     p.dropout_p = 1.0                                      # keeps nothing: rejected
@@ -122,8 +122,8 @@ def test_reference_launchers_validate_before_device_work():
     r = _lib.RefFwdParams()
     assert lib.fa_forward_launch(r, 0, None) == 3          # null tensors
     r.Q = r.K = r.V = r.O = 16
-    r.NH, r.gqa, r.batch, r.SQ, r.SK, r.HD = 4, 1, 1, 8, 8, 72
-    assert lib.fa_forward_launch(r, 0, None) == 2          # no head_dim 72 kernel
+    r.NH, r.gqa, r.batch, r.SQ, r.SK, r.HD = 4, 1, 1, 8, 8, 100
+    assert lib.fa_forward_launch(r, 0, None) == 2          # head_dim 100 is not a multiple of 8
     r.HD, r.batch, r.LSE = 64, 2, 16                       # LSE without a batch stride
     assert lib.fa_forward_launch(r, 0, None) == 3
     assert b"batch == 1" in lib.fable_attn_last_error()

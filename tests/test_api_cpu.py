@@ -124,11 +124,16 @@ def test_forward_argument_mapping(fake):
 
 
 def test_head_dim_padding_and_slicing(fake):
-    q = rnd(1, 16, 2, 80)
-    out = fai.flash_attn_func(q, q, q)
-    assert fake.calls[-1][1]["shape"][-1] == 128        # padded to the next kernel head_dim
-    assert math.isclose(fake.calls[-1][1]["scale"], 80 ** -0.5)   # scale of the real head_dim
-    assert out.shape == (1, 16, 2, 80) and out.is_contiguous()
+    """fp16/bf16 head dims that are multiples of 8 go to the kernels as they are; others are
+    zero-padded to the next multiple of 8, fp32 ones to 64/128/256; the scale and the output
+    keep the real head dim."""
+    for D, dt, width in ((80, torch.float16, 80), (40, torch.bfloat16, 40), (100, torch.float16, 104),
+                         (80, torch.float32, 128), (24, torch.float32, 64)):
+        q = rnd(1, 16, 2, D, dt=dt)
+        out = fai.flash_attn_func(q, q, q)
+        assert fake.calls[-1][1]["shape"][-1] == width, (D, dt)
+        assert math.isclose(fake.calls[-1][1]["scale"], D ** -0.5)   # scale of the real head_dim
+        assert out.shape == (1, 16, 2, D) and out.is_contiguous()
 
 
 def test_qv_fusion_shapes_and_scale(fake):
@@ -187,11 +192,11 @@ def test_varlen_grad_is_one_native_call_each_way(fake):
 
 def test_varlen_grad_padded_head_dim(fake):
     cu = torch.tensor([0, 6, 10], dtype=torch.int32)
-    q, k, v = (rnd(10, 2, 80).requires_grad_() for _ in range(3))
+    q, k, v = (rnd(10, 2, 76).requires_grad_() for _ in range(3))
     out = fai.flash_attn_varlen_func(q, k, v, cu, cu, 6, 6)
-    assert out.shape == (10, 2, 80) and fake.calls[0][1]["shape"] == (10, 2, 128)
+    assert out.shape == (10, 2, 76) and fake.calls[0][1]["shape"] == (10, 2, 80)
     out.sum().backward()
-    assert q.grad.shape == (10, 2, 80) and torch.all(q.grad == 2)
+    assert q.grad.shape == (10, 2, 76) and torch.all(q.grad == 2)
 
 
 def test_varlen_chunk_backward_rejected(fake):

@@ -14,9 +14,9 @@ where that floor exceeds 2/3 of the bound the bound becomes 1.5x the floor (test
 check_grads). Every case logs its errors, its distance from the model and the floor.
 At the full BASELINE.json configs[2] size sampled heads are checked against the fp64 oracle.
 
-Every case runs both backward paths at head_dim 64/128: "ds" (the dK/dV kernel stores dS in a
-workspace and dQ = dS.K is formed from it, the default) and "recompute" (no workspace: the dQ
-kernel recomputes S and dP); head_dim 256 has the recomputing path only.
+Every case runs both backward paths at head dims up to 128: "ds" (the dK/dV kernel stores dS in
+a workspace and dQ = dS.K is formed from it, the default) and "recompute" (no workspace: the dQ
+kernel recomputes S and dP); head dims above 128 have the recomputing path only.
 """
 import math
 
@@ -46,6 +46,14 @@ CASES = [
     ("softcap 30", 1, 4, 4, 128, 128, 64, False, -1, -1, 30.0, False),
     ("alibi causal", 1, 4, 4, 128, 128, 64, True, -1, -1, 0.0, True),
     ("D128 causal B2 S512", 2, 4, 4, 512, 512, 128, True, -1, -1, 0.0, False),
+    # head dims other than 64/128/256 (zero columns inside the 64/128/256-wide kernels)
+    ("D32 causal", 1, 4, 2, 150, 150, 32, True, -1, -1, 0.0, False),
+    ("D48 full", 1, 4, 4, 100, 120, 48, False, -1, -1, 0.0, False),
+    ("D80 causal gqa", 1, 8, 2, 160, 160, 80, True, -1, -1, 0.0, False),
+    ("D96 window (40,0)", 1, 4, 4, 200, 200, 96, False, 40, 0, 0.0, False),
+    ("D160 causal", 1, 2, 2, 96, 96, 160, True, -1, -1, 0.0, False),
+    ("D192 full softcap", 1, 2, 1, 80, 100, 192, False, -1, -1, 20.0, False),
+    ("D224 causal", 1, 2, 2, 70, 70, 224, True, -1, -1, 0.0, False),
 ]
 
 

@@ -122,6 +122,25 @@ def test_decode_parity(case, dt):
                 assert np.array_equal(vcn[blk, pos % page], c["nv"][b, t])
 
 
+# head dims other than 64/128/256 (zero columns inside the 64/128/256-wide kernels; rows in the
+# cache are the real head dim long), with append and rotary; fp16/bf16 (fp32 has 64/128/256)
+DIM_CASES = [
+    ("HD32 append+rotary", 32, 8, 4, [70, 200], -1, 1, True, 0, 2, 0.0, False, 16),
+    ("HD80 append+rotary interleaved", 80, 16, 4, [300], -1, 2, True, 0, 1, 0.0, False, 16),
+    ("HD96 GQA8 window", 96, 16, 8, [500, 77], 64, 0, False, 0, 1, 0.0, False, 32),
+    ("HD112 softcap append nq3", 112, 8, 2, [200], -1, 0, True, 0, 3, 30.0, False, 16),
+    ("HD160 append", 160, 8, 4, [300], -1, 1, True, 0, 1, 0.0, False, 16),
+    ("HD192 leftpad alibi", 192, 8, 8, [400], -1, 0, False, 37, 1, 0.0, True, 16),
+    ("HD200 append rotary", 200, 4, 2, [130], -1, 1, True, 0, 2, 0.0, False, 16),
+]
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("case", DIM_CASES, ids=[c[0] for c in DIM_CASES])
+def test_decode_head_dims(case, dt):
+    test_decode_parity(case, dt)
+
+
 @pytest.mark.parametrize("nsplit", [1, 3, 16, 64])
 def test_decode_split_counts_agree(nsplit):
     c = make_case(("splits", 128, 32, 4, [3000, 1111], -1, 0, False, 0, 1, 0.0, False, 64), "f16")

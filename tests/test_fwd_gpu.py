@@ -54,6 +54,21 @@ CASES = [
     ("d128 wide window + alibi", 1, 2300, 2300, 128, 4, 1, True, 2048, 0, 0.0, True, 0),
     ("d128 narrow window + softcap", 1, 300, 300, 128, 8, 2, True, 100, 0, 20.0, False, 0),
     ("d64 narrow window + alibi", 1, 300, 300, 64, 8, 1, False, 40, 40, 0.0, True, 0),
+    # head dims other than 64/128/256: kernels of width 32, 96, 160, 192, 224, and dims that
+    # are not multiples of 32 (zero columns inside the kernel); the 8-wave and 4-wave shapes
+    # whose loaders leave threads idle in the last round (width 32 and 96)
+    ("d32 causal", 1, 300, 300, 32, 8, 2, True, -1, -1, 0.0, False, 0),
+    ("d16 full", 1, 200, 200, 16, 4, 1, False, -1, -1, 0.0, False, 0),
+    ("d48 window (40,0)", 1, 250, 250, 48, 8, 4, True, 40, 0, 0.0, False, 0),
+    ("d80 causal GQA", 1, 330, 330, 80, 16, 4, True, -1, -1, 0.0, False, 0),
+    ("d96 full SQ<SK", 1, 160, 270, 96, 8, 2, False, -1, -1, 0.0, False, 0),
+    ("d96 causal 8-wave grid", 2, 1100, 1100, 96, 16, 1, True, -1, -1, 0.0, False, 0),
+    ("d112 softcap", 1, 200, 200, 112, 8, 1, True, -1, -1, 30.0, False, 0),
+    ("d160 causal", 1, 200, 200, 160, 8, 2, True, -1, -1, 0.0, False, 0),
+    ("d192 full alibi", 1, 150, 170, 192, 4, 1, False, -1, -1, 0.0, True, 0),
+    ("d200 window (64,0) softcap", 1, 260, 260, 200, 4, 2, True, 64, 0, 20.0, False, 0),
+    ("d224 causal chunk 96", 1, 230, 230, 224, 4, 1, True, -1, -1, 0.0, False, 96),
+    ("d40 causal ragged", 1, 77, 77, 40, 4, 1, True, -1, -1, 0.0, False, 0),
 ]
 
 
