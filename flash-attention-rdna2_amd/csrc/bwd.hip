@@ -155,13 +155,13 @@ bwd_dq_kernel(FableBwdParams p, int nqt) {
                             : buf_rsrc(Vg + (long long)kb * p.vs.s, (long long)(SK - kb) * p.vs.s * 2);
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(rs, voff[j]);
-    if (padded) {
-#pragma unroll
-      for (int j = 0; j < C::PER; j++) ld[j] = cok[j] ? ld[j] : u32x4{0, 0, 0, 0};
-    }
   };
   auto lstore = [&](int stage) {
     T* base = lds + stage * C::STAGE + (kloader ? 0 : C::KT);
+    if (padded) {  // (at the store, which waits for the loads anyway)
+#pragma unroll
+      for (int j = 0; j < C::PER; j++) ld[j] = cok[j] ? ld[j] : u32x4{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
@@ -353,10 +353,6 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
                              rows * p.dos.s * 2);
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(j < QJ ? rq : rd, voff[j]);
-    if (padded) {
-#pragma unroll
-      for (int j = 0; j < C::PER; j++) ld[j] = cok[j] ? ld[j] : u32x4{0, 0, 0, 0};
-    }
     const int q = qt0 + (rsel % C::BQ);
     lok = it < total && q < SQ;
     const long long ri = (long long)b * p.lse_sb + (long long)h * p.lse_sh + sq.qo + min(q, SQ - 1);
@@ -364,6 +360,10 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
   };
   auto lstore = [&](int stage) {
     T* base = lds + stage * C::STAGE;
+    if (padded) {  // zero columns (at the store, which waits for the loads anyway)
+#pragma unroll
+      for (int j = 0; j < C::PER; j++) ld[j] = cok[j] ? ld[j] : u32x4{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int ci = tid + (j < QJ ? j : j - QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
@@ -522,6 +522,14 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
 
   const int kw = kb0 + 32 * pair, key = kw + l32;
   const bool pair_keys = kw < SK;
+  // dS workspace: this pair's key block in the compacted layout (table built by the dsum kernel)
+  int ds_row = 0, ds_T = 0;
+  if constexpr (DSW) {
+    const int nkb = (p.SK + 31) >> 5;
+    const int* tbl = (const int*)p.ds_ws;
+    ds_row = tbl[min(kw >> 5, nkb - 1)];
+    ds_T = tbl[nkb];
+  }
   // B operand rows of this wave's product with the Q (or dO) tile: K for the S-wave, V for the
   // dP-wave; lane holds key `key`, head-dim 16*ds + 8*hh .. +7
   const T* Rg = dpw ? (const T*)p.V + (long long)b * p.vs.b + sq.ko * p.vs.s + (long long)kvh * p.vs.h
@@ -553,7 +561,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   // the zero columns, whose chunks load the row's first chunk and are replaced by zeros)
   static_assert(C::NT % C::DCH == 0, "one column per thread");
   const bool cok = 8 * (tid % C::DCH) < HDr;
-  const bool zcol = !cok;
+  const bool zcol = !cok, padded = HDr < C::HD;
   int voff[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
@@ -587,10 +595,6 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     const auto rd = buf_rsrc(g_do, in ? g_doleft : 0);
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(j < C::QJ ? rq : rd, voff[j]);
-    if (zcol) {
-#pragma unroll
-      for (int j = 0; j < C::PER; j++) ld[S][j] = u32x4{0, 0, 0, 0};
-    }
     const int qr = qstart + g_qi * C::BQ + (rsel % C::BQ);
     lok[S] = in && qr < SQ;
     // unconditional (clamped row; SQ >= 1 whenever the loop runs), so the memory waits of
@@ -618,6 +622,12 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   auto lstore = [&](auto set, int stage) {
     constexpr int S = decltype(set)::value;
     T* base = lds + stage * C::STAGE;
+    // zero columns: stored as zeros (at the store, which waits for the loads anyway; zeroing
+    // the registers at the load would make the compiler wait for the loads there)
+    if (padded) {
+#pragma unroll
+      for (int j = 0; j < C::PER; j++) ld[S][j] = zcol ? u32x4{0, 0, 0, 0} : ld[S][j];
+    }
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
@@ -781,7 +791,8 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     tprod(qs, pS);  // dK^T += Q^T . dS
     if constexpr (DSW) {  // dS tile (32 queries x this pair's 32 keys) to the workspace
       if (act) {
-        T* dst = ds_tile<T>(p, b, kvh * p.gqa + hg, kw >> 5, qt0 >> 5) + 16 * l32 + 8 * hh;
+        T* dst = ds_head_tiles<T>(p, b, kvh * p.gqa + hg, ds_T) + (long long)(ds_row + (qt0 >> 5)) * 1024 +
+                 16 * l32 + 8 * hh;
         // streaming stores: the tiles are read once, by the dQ kernel, and must not push the
         // Q/dO tiles this kernel re-reads out of L2
         __builtin_nontemporal_store(pS[0], (V8*)dst);
@@ -823,6 +834,7 @@ __global__ __launch_bounds__(256) void bwd_dsum_kernel(FableBwdParams p, int rbl
   const int tid = threadIdx.x;
   const int rb = blockIdx.x % rblocks, zh = blockIdx.x / rblocks;
   const int h = zh % p.Hq, b = zh / p.Hq;
+  if (blockIdx.x == 0) ds_build_table(p);  // the dS workspace's tile table, for the next kernels
   const BwdSeq sq = bwd_seq(p, b);
   if (sq.SQ <= 0) return;
   const int c = tid % LPR;
@@ -926,29 +938,37 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
   };
   // Loads are issued unconditionally (from a clamped tile address when the tile was not written;
   // such data is never used), so the memory waits stay exact and the prefetch stays in flight.
-  const int nqb = (p.SQ + 31) >> 5, nkb = (p.SK + 31) >> 5;
-  const T* dsw = ds_tile<T>(p, b, h, 0, min(qw >> 5, nqb - 1)) + 16 * l32 + 8 * hh;
-  const long long kstep = (long long)nqb * 1024;  // elements between key blocks
+  // Tiles of the compacted layout (bwd_common.hpp): key block kb's row starts at tbl[kb], and
+  // tbl[kb+1] = tbl[kb] + qb1(kb) - qb0(kb+1), so after one table read per workgroup the row
+  // advances by scalar integer steps. A tile that was not written is read from a clamped index
+  // inside this head's tiles (its data is never used).
+  const int nkb = (p.SK + 31) >> 5;
+  const int* tbl = (const int*)p.ds_ws;
+  const int ds_T = tbl[nkb];
+  const T* dsw = ds_head_tiles<T>(p, b, h, ds_T) + 16 * l32 + 8 * hh;
+  const int qbw = qw >> 5;
   constexpr int NS = C::NS;
   V8 dsr[NS][2 * C::NKB];  // [register set][key block jb, query half sh] chunks of one K tile
   bool dact[NS][C::NKB];
-  // Tiles are loaded in order; the tile addresses advance by additions (a from-scratch 64-bit
-  // address costs a dozen scalar instructions per tile). Past the last key block the dS
-  // address stays on a valid block.
-  const T* d_ptr = dsw + (kstart >> 5) * kstep;
   int d_kb32 = kstart >> 5;
+  int d_row = tbl[min(d_kb32, nkb - 1)];
   auto dsload = [&](auto set, int t) {
     constexpr int S = decltype(set)::value;
-    const T* src = d_ptr;
 #pragma unroll
     for (int jb = 0; jb < C::NKB; jb++) {
-      dact[S][jb] = t < ntiles && written(d_kb32 + jb);
+      const int kb = d_kb32 + jb;
+      dact[S][jb] = t < ntiles && written(kb);
+      const int idx = min(max(d_row + qbw, 0), ds_T - 1);
+      const T* src = dsw + (long long)idx * 1024;
       dsr[S][2 * jb] = __builtin_nontemporal_load((const V8*)src);
       dsr[S][2 * jb + 1] = __builtin_nontemporal_load((const V8*)(src + 512));
-      if (d_kb32 + jb + 1 < nkb) src += kstep;  // past the last key block: stay on it
+      if (kb + 1 < nkb) {  // the next key block's row (past the last one: stay)
+        int a0, a1, n0, n1;
+        ds_span(p, kb, a0, a1);
+        ds_span(p, kb + 1, n0, n1);
+        d_row += a1 - n0;
+      }
     }
-    if (d_kb32 + C::NKB < nkb) d_ptr += C::NKB * kstep;
-    else d_ptr = dsw + (nkb - 1) * kstep;
     d_kb32 += C::NKB;
   };
 
@@ -957,7 +977,7 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
   static_assert(C::NT % C::DCH == 0, "one column per thread");
   const int HDr = p.D;
   const bool cok = 8 * (tid % C::DCH) < HDr;
-  const bool zcol = !cok;
+  const bool zcol = !cok, padded = HDr < C::HD;
   int voff[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
@@ -973,16 +993,16 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
     const auto rs = buf_rsrc(k_ptr, k_left);  // past the last tile the descriptor is empty: zeros
 #pragma unroll
     for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(rs, voff[j]);
-    if (zcol) {
-#pragma unroll
-      for (int j = 0; j < C::PER; j++) ld[S][j] = u32x4{0, 0, 0, 0};
-    }
     k_ptr += k_step;
     k_left -= 2 * k_step;
   };
   auto lstore = [&](auto set, int stage) {
     constexpr int S = decltype(set)::value;
     T* base = lds + stage * C::KT;
+    if (padded) {  // zero columns stored as zeros (see the pair kernel)
+#pragma unroll
+      for (int j = 0; j < C::PER; j++) ld[S][j] = zcol ? u32x4{0, 0, 0, 0} : ld[S][j];
+    }
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int idx = tid + j * C::NT, r = idx / C::DCH, c = idx % C::DCH;
@@ -1073,8 +1093,11 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
 #define DSQ_NS 3
 #endif
 // bytes of dS workspace for the fp16/bf16 path (2-byte elements)
+// bytes of the compacted dS workspace (bwd_common.hpp): the table, then every (b, h)'s tiles
 static long long ds_bytes(const FableBwdParams& p) {
-  return p.SQ > 0 && p.SK > 0 ? (long long)p.B * p.Hq * ds_tiles_per_head(p.SQ, p.SK) * 2048 : 0;
+  if (p.SQ <= 0 || p.SK <= 0) return 0;
+  const long long t = ds_tiles_per_head(p);  // 0: no query sees any key, the recomputing path serves
+  return t > 0 ? ds_header_bytes((p.SK + 31) >> 5) + (long long)p.B * p.Hq * t * 2048 : 0;
 }
 
 // backward through the dS workspace: D rows, then dK/dV (writing dS), then dQ = dS.K
@@ -1150,10 +1173,20 @@ static int bwd_dispatch(const FableBwdParams& p, hipStream_t st) {
 
 }  // namespace fa
 
+namespace fa {
+// A window at least as long as the sequences bounds nothing: dropping it keeps every mask bound
+// in 32 bits (and the dS workspace layout the same for the size query and the launch).
+static void normalize_windows(FableBwdParams& p) {
+  if (p.win_left >= p.SK) p.win_left = -1;
+  if (p.win_right >= p.SQ) p.win_right = -1;
+}
+}  // namespace fa
+
 extern "C" int64_t fable_attn_bwd_ds_bytes(FableBwdParams p, int dtype) {
   if ((dtype != FA_F16 && dtype != FA_BF16) || p.D <= 0 || p.D % 8 || fa::bwd_width(p.D) > 128 || p.B <= 0 ||
       p.Hq <= 0)
     return 0;
+  fa::normalize_windows(p);
   return fa::ds_bytes(p);
 }
 
@@ -1168,9 +1201,7 @@ extern "C" int fable_attn_bwd(FableBwdParams p, int dtype, void* stream) {
   if ((p.cu_q == nullptr) != (p.cu_k == nullptr))
     return fail(FA_ERR_ARG, "fable_attn_bwd: cu_q and cu_k go together");
   if (p.B <= 0 || p.SQ < 0 || p.SK < 0) return FA_OK;  // empty ranges write zero gradients
-  // a window at least as long as the sequences bounds nothing (keeps mask bounds in 32 bits)
-  if (p.win_left >= p.SK) p.win_left = -1;
-  if (p.win_right >= p.SQ) p.win_right = -1;
+  normalize_windows(p);
   if (!p.cu_q && p.lse_sb == 0 && p.lse_sh == 0) {  // dense [B,Hq,SQ] LSE / dsum
     p.lse_sh = p.SQ;
     p.lse_sb = (int64_t)p.Hq * p.SQ;

@@ -89,19 +89,90 @@ __device__ __forceinline__ BwdSeq bwd_seq(const FableBwdParams& p, int b) {
 
 // With a dS workspace the pair kernel stores each dS tile it computes (32 queries x 32 keys,
 // 2 KiB) and dQ = dS.K is one product per tile, instead of recomputing S, P and dP.
-// Workspace layout: tile (b, h, kb32, qb32) at ((b*Hq + h)*nkb + kb32)*nqb + qb32 (in 1024-element
-// tiles; nkb = ceil(SK/32), nqb = ceil(SQ/32) of the longest sequence). A tile is the pair
-// kernel's register layout, written with two 16-byte stores per lane: half sh (512 elements)
-// holds, for key k, the 16 query slots 16*k .. 16*k+15, and slot 8*hh + e is query
+// Workspace layout: only the tiles some query of the 32-row block sees some key of the 32-key
+// block of are stored (about half the rectangle under a causal mask, a band under a window).
+// Key block kb keeps the query blocks [qb0(kb), qb1(kb)) (ds_span, the query_range_b of the
+// block). The workspace starts with a table of nkb + 1 ints, padded to 256 bytes:
+// tbl[kb] = (tiles of key blocks before kb) - qb0(kb), tbl[nkb] = T, the tiles per (b, h); tile
+// (b, h, kb, qb) follows at ((b*Hq + h)*T + tbl[kb] + qb) tiles of 1024 elements. The dsum kernel
+// writes the table (workgroup 0), before the pair kernel runs. Packed variable-length batches
+// keep every query block of the longest sequence (qb0 = 0, qb1 = ceil(SQ/32)). A tile is the
+// pair kernel's register layout, written with two 16-byte stores per lane: half sh (512
+// elements) holds, for key k, the 16 query slots 16*k .. 16*k+15, and slot 8*hh + e is query
 // 16*sh + 8*(e/4) + 4*hh + e%4 (the MFMA C-row order of the S = Q.K^T product). Slot n of the
 // 32 in a tile (n = 16*sh + 8*hh + e) is therefore query ds_slot_query(n).
-__host__ __device__ inline long long ds_tiles_per_head(int SQ, int SK) {
-  return (long long)((SK + 31) >> 5) * ((SQ + 31) >> 5);
+// (The windows are those fable_attn_bwd normalised: a bound at least as long as the sequences
+// is -1, so every term below stays in 32-bit range.)
+__host__ __device__ inline void ds_span(const FableBwdParams& p, int kb, int& qb0, int& qb1) {
+  const int nqb = (p.SQ + 31) >> 5;
+  if (p.cu_q) {
+    qb0 = 0;
+    qb1 = nqb;
+    return;
+  }
+  const int k0 = 32 * kb, k1 = (k0 + 31 < p.SK - 1 ? k0 + 31 : p.SK - 1), delta = p.SK - p.SQ;
+  int q0 = 0, q1 = p.SQ;
+  if (p.causal && k0 - delta > q0) q0 = k0 - delta;
+  if (p.win_right >= 0 && k0 - delta - p.win_right > q0) q0 = k0 - delta - p.win_right;
+  if (p.win_left >= 0 && k1 - delta + p.win_left + 1 < q1) q1 = k1 - delta + p.win_left + 1;
+  if (q1 <= q0) {
+    qb0 = qb1 = 0;
+  } else {
+    qb0 = q0 >> 5;
+    qb1 = (q1 + 31) >> 5;
+  }
 }
+__host__ __device__ inline long long ds_header_bytes(int nkb) {
+  return ((long long)(nkb + 1) * 4 + 255) / 256 * 256;
+}
+// tiles per (b, h) of the layout above (host side, for the workspace size)
+inline long long ds_tiles_per_head(const FableBwdParams& p) {
+  const int nkb = (p.SK + 31) >> 5;
+  long long t = 0;
+  for (int kb = 0; kb < nkb; kb++) {
+    int a, z;
+    ds_span(p, kb, a, z);
+    t += z - a;
+  }
+  return t;
+}
+// the table of the layout above, built by one workgroup of 256 threads (all of them call it)
+__device__ inline void ds_build_table(const FableBwdParams& p) {
+  __shared__ int part[256];
+  const int nkb = (p.SK + 31) >> 5, t = threadIdx.x;
+  const int per = (nkb + 255) / 256, kb0 = t * per, kb1 = min(kb0 + per, nkb);
+  int sum = 0;
+  for (int kb = kb0; kb < kb1; kb++) {
+    int a, z;
+    ds_span(p, kb, a, z);
+    sum += z - a;
+  }
+  part[t] = sum;
+  __syncthreads();
+  if (t == 0) {
+    int run = 0;
+    for (int i = 0; i < 256; i++) {
+      const int x = part[i];
+      part[i] = run;
+      run += x;
+    }
+  }
+  __syncthreads();
+  int* tbl = (int*)p.ds_ws;
+  int run = part[t];
+  for (int kb = kb0; kb < kb1; kb++) {
+    int a, z;
+    ds_span(p, kb, a, z);
+    tbl[kb] = run - a;
+    run += z - a;
+  }
+  if (t == 255) tbl[nkb] = run;
+}
+// tile (b, h) base and the table of the layout above
 template <typename T>
-__device__ __forceinline__ T* ds_tile(const FableBwdParams& p, int b, int h, int kb32, int qb32) {
-  const long long nqb = (p.SQ + 31) >> 5, nkb = (p.SK + 31) >> 5;
-  return (T*)p.ds_ws + ((((long long)b * p.Hq + h) * nkb + kb32) * nqb + qb32) * 1024;
+__device__ __forceinline__ T* ds_head_tiles(const FableBwdParams& p, int b, int h, int tiles_per_head) {
+  const int nkb = (p.SK + 31) >> 5;
+  return (T*)((char*)p.ds_ws + ds_header_bytes(nkb)) + ((long long)b * p.Hq + h) * tiles_per_head * 1024;
 }
 __device__ __forceinline__ int ds_slot_query(int n) {
   return 16 * (n >> 4) + 8 * ((n >> 2) & 1) + 4 * ((n >> 3) & 1) + (n & 3);

@@ -177,6 +177,10 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
       const int ch = (64 * i + lane) % RCH;
       vr[i] = __builtin_nontemporal_load((const u32x4*)(Vc + row_off(vblk[i], vkey(kc0, i)) + (vok[i] ? 8 * ch : 0)));
     }
+  };
+  // zero columns of a padded head dim, put in where the rows are used (which waits for the
+  // loads anyway; a select right after the loads would make the compiler wait there)
+  auto zero_pad = [&](u32x4 (&kr)[2][NDS], u32x4 (&vr)[NVI]) {
     if (padded) {
 #pragma unroll
       for (int kb = 0; kb < 2; kb++)
@@ -207,6 +211,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
       load(kc0 + kStep, knxt, vnxt);
       table(kc0 + 2 * kStep);
     }
+    zero_pad(kreg, vreg);
     // S^T = K . Q^T
     f32x4 s[2];
 #pragma unroll

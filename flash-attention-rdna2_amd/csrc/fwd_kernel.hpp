@@ -179,8 +179,10 @@ fwd_kernel(FableFwdParams p, int nqt) {
   const int kvalid = min(SK, kstart + ntiles * C::BC);
   // chunk j of this thread: ci = tid + j*NT, row ci / DCH, 16-byte column chunk ci % DCH. In the
   // last round (KTAIL) threads past the tile's chunks load row 0 again and store nothing;
-  // chunks in the zero columns (>= p.HD) are loaded from the row's first chunk and replaced by
-  // zeros (`padded`, uniform), so no load depends on a lane condition.
+  // chunks in the zero columns (>= p.HD) are loaded from the row's first chunk and stored as
+  // zeros (`padded`, uniform), so no load depends on a lane condition. (The zeros are put in at
+  // the LDS store, which waits for the load anyway: a select right after the load would make
+  // the compiler wait for the load there.)
   // When NT is a multiple of DCH (every shape whose head dim is a power of two) a thread's
   // chunks share one column and sit RSTEP rows apart, so the LDS addresses are one base plus
   // immediate offsets; other shapes keep one address per chunk.
@@ -211,28 +213,28 @@ fwd_kernel(FableFwdParams p, int nqt) {
     const auto r = buf_rsrc(Kg + (long long)kb * p.sK.s, (long long)(kvalid - kb) * p.sK.s * 2);
 #pragma unroll
     for (int j = 0; j < C::KJ; j++) ldk[j] = buf_load16(r, koff[j]);
-    if (padded) {
-#pragma unroll
-      for (int j = 0; j < C::KJ; j++) ldk[j] = cok[j] ? ldk[j] : u32x4{0, 0, 0, 0};
-    }
   };
   auto gload_v = [&](int kb) {
     const auto r = buf_rsrc(Vg + (long long)kb * p.sV.s, (long long)(kvalid - kb) * p.sV.s * 2);
 #pragma unroll
     for (int j = 0; j < C::KJ; j++) ldv[j] = buf_load16(r, voff[j]);
-    if (padded) {
-#pragma unroll
-      for (int j = 0; j < C::KJ; j++) ldv[j] = cok[j] ? ldv[j] : u32x4{0, 0, 0, 0};
-    }
   };
   auto lstore_k = [&](int st) {
     T* b = kl + st * C::KTILE;
+    if (padded) {
+#pragma unroll
+      for (int j = 0; j < C::KJ; j++) ldk[j] = cok[j] ? ldk[j] : u32x4{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int j = 0; j < C::KJ; j++)
       if (!C::KTAIL || j < C::KJ - 1 || lko[j] >= 0) *(u32x4*)(b + lko[j]) = ldk[j];
   };
   auto lstore_v = [&](int st) {
     T* b = vl + st * C::VTILE;
+    if (padded) {
+#pragma unroll
+      for (int j = 0; j < C::KJ; j++) ldv[j] = cok[j] ? ldv[j] : u32x4{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int j = 0; j < C::KJ; j++)
       if (!C::KTAIL || j < C::KJ - 1 || lvo[j] >= 0) *(u32x4*)(b + lvo[j]) = ldv[j];

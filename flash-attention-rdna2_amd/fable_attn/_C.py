@@ -21,11 +21,14 @@ Tensor checks raise RuntimeError as TORCH_CHECK does there. torch only allocates
 workspaces and supplies the current stream; all compute is in libfable_attn_hip.so. There is
 no fallback: if the library is missing, importing this module raises ImportError.
 
-Backward dS workspace: for fp16/bf16 at head_dim 64/128 the backward can store dS once and
+Backward dS workspace: for fp16/bf16 at head dims up to 128 the backward can store dS once and
 form dQ = dS.K from it (FableBwdParams.ds_ws) instead of recomputing S and dP in its dQ kernel. The
-workspace is B*Hq*SQ*SK*2 bytes (rounded up to 32x32 tiles); bwd/bwd_varlen allocate it when it
-is at most `ds_max_bytes` (default BWD_DS_MAX_BYTES, 4 GiB, or the environment variable
-FABLE_ATTN_BWD_DS_MAX_BYTES). Both paths give the same gradients to rounding.
+workspace holds 2 bytes per visible (query, key) pair of every q head, in 32x32 tiles (about half
+of B*Hq*SQ*SK*2 bytes under a causal mask; packed varlen batches keep the rectangle of the longest
+sequences); bwd/bwd_varlen allocate it when it is at most `ds_max_bytes` (default
+BWD_DS_MAX_BYTES, 16 GiB, or the environment variable FABLE_ATTN_BWD_DS_MAX_BYTES) and fall back
+to the recomputing path when the allocation fails. Both paths give the same gradients to
+rounding.
 """
 import ctypes
 import os
@@ -37,7 +40,7 @@ from ._lib import FableBwdParams, CombineParams, FableDecParams, FableFwdParams,
 
 _L = _lib.load()
 
-BWD_DS_MAX_BYTES = int(os.environ.get("FABLE_ATTN_BWD_DS_MAX_BYTES", 4 << 30))
+BWD_DS_MAX_BYTES = int(os.environ.get("FABLE_ATTN_BWD_DS_MAX_BYTES", 16 << 30))
 
 
 def _ds_workspace(p, dtype, device, ds_max_bytes):

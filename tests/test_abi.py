@@ -144,19 +144,51 @@ def test_decode_split_plan(hint, expect):
         assert 1 <= n <= 512
 
 
+def _visible_tiles(SQ, SK, causal, wl=-1, wr=-1):
+    """(32-key, 32-query) blocks holding at least one visible pair, counted by brute force over
+    the mask of every (query, key) pair (the reference's visibility rule, bottom-right aligned)."""
+    import numpy as np
+    q = np.arange(SQ)[:, None] + (SK - SQ)
+    k = np.arange(SK)[None, :]
+    vis = np.ones((SQ, SK), bool)
+    if causal:
+        vis &= k <= q
+    if wl >= 0:
+        vis &= k >= q - wl
+    if wr >= 0:
+        vis &= k <= q + wr
+    nqb, nkb = (SQ + 31) // 32, (SK + 31) // 32
+    pad = np.zeros((nqb * 32, nkb * 32), bool)
+    pad[:SQ, :SK] = vis
+    return int(pad.reshape(nqb, 32, nkb, 32).any(axis=(1, 3)).sum())
+
+
 def test_bwd_ds_workspace_size():
-    """fable_attn_bwd_ds_bytes: 2 KiB per (32-query, 32-key) tile of every (batch, q head) for
-    the fp16/bf16 head dims with a dS-workspace path (64, 128); 0 elsewhere (host-only call)."""
+    """fable_attn_bwd_ds_bytes: a 256-byte-padded table of ceil(SK/32)+1 ints, then 2 KiB per
+    (32-query, 32-key) tile that holds a visible pair, for every (batch, q head), for the
+    fp16/bf16 head dims with a dS-workspace path (up to 128); 0 elsewhere (host-only call).
+    The tile count is checked against a brute-force count over the pair mask."""
     from fable_attn import _lib
     lib = _lib.load()
     p = _lib.FableBwdParams()
+    hdr = lambda SK: -(-((SK + 31) // 32 + 1) * 4 // 256) * 256
     p.B, p.Hq, p.Hk, p.gqa, p.SQ, p.SK, p.D = 2, 8, 2, 4, 100, 65, 128
-    want = 2 * 8 * 4 * 3 * 2048
+    p.win_left, p.win_right = -1, -1
+    want = hdr(65) + 2 * 8 * 4 * 3 * 2048                   # no mask: the whole rectangle
     assert lib.fable_attn_bwd_ds_bytes(p, 0) == want and lib.fable_attn_bwd_ds_bytes(p, 1) == want
     p.D = 64
+    assert lib.fable_attn_bwd_ds_bytes(p, 1) == want
+    p.D = 80                                                 # any multiple of 8 up to 128
     assert lib.fable_attn_bwd_ds_bytes(p, 1) == want
     assert lib.fable_attn_bwd_ds_bytes(p, 2) == 0      # fp32 recomputes
     p.D = 256
     assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0
     p.D, p.SQ = 128, 0
     assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0
+    # causal and windowed: only the tiles with a visible pair
+    for SQ, SK, causal, wl, wr in ((4096, 4096, 1, -1, 0), (150, 150, 1, -1, -1), (96, 300, 1, -1, -1),
+                                   (300, 96, 1, -1, -1), (1000, 1000, 0, 100, 0), (500, 700, 0, 64, 64),
+                                   (700, 500, 1, 37, -1), (64, 64, 0, 5000, -1)):
+        p.B, p.Hq, p.SQ, p.SK, p.causal, p.win_left, p.win_right = 1, 3, SQ, SK, causal, wl, wr
+        got = lib.fable_attn_bwd_ds_bytes(p, 0)
+        assert got == hdr(SK) + 3 * _visible_tiles(SQ, SK, causal, wl, wr) * 2048, (SQ, SK, causal, wl, wr)

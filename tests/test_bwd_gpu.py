@@ -169,7 +169,7 @@ def test_backward_ds_workspace_too_small_falls_back():
     p.B, p.Hq, p.Hk, p.SQ, p.SK, p.D, p.gqa = B, Hq, Hk, SQ, SK, D, Hq // Hk
     p.scale, p.causal, p.win_left, p.win_right, p.keep_scale = scale, 1, -1, -1, 1.0
     need = lib.fable_attn_bwd_ds_bytes(p, 1)
-    assert need == B * Hq * 5 * 5 * 2048
+    assert need == 256 + B * Hq * 15 * 2048   # table + the 15 causal tiles of a 5x5 block grid
     ws = torch.full((need + 16,), 0xFF, dtype=torch.uint8, device="cuda")  # NaN bit patterns
     stream = ctypes_stream()
     # too small, then big enough but not 16-byte aligned: both ignored
@@ -196,3 +196,40 @@ def ctypes_stream():
 
     import torch
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def test_backward_long_causal_takes_the_ds_path():
+    """The C2 shape's backward (causal bf16, B=1, S=16384, H=32, D=128): the dS workspace holds
+    only the causal triangle's tiles (~8.6 GB instead of the 17 GB rectangle), fits the default
+    cap, and the dS path gives the recomputing path's dV bit for bit (the same pair kernel, which
+    only adds the tile stores), its dK and dQ to rounding (D = rowsum(O*dO) is summed in another
+    order by the two paths), bitwise reproducibly."""
+    import torch
+
+    from fable_attn import _C, _lib
+    from fable_attn.flash_attn_interface import _bhsd
+    B, S, H, D = 1, 16384, 32, 128
+    lib = _lib.load()
+    p = _lib.FableBwdParams()
+    p.B, p.Hq, p.Hk, p.gqa, p.SQ, p.SK, p.D, p.causal = B, H, H, 1, S, S, D, 1
+    p.win_left, p.win_right = -1, 0
+    need = lib.fable_attn_bwd_ds_bytes(p, 1)
+    assert need == 2304 + B * H * (512 * 513 // 2) * 2048 and need <= _C.BWD_DS_MAX_BYTES
+    g = torch.Generator(device="cuda").manual_seed(4)
+    q, k, v, do = (torch.randn(B, S, H, D, device="cuda", dtype=torch.bfloat16, generator=g)
+                   for _ in range(4))
+    qh, kh, vh, doh = (_bhsd(x) for x in (q, k, v, do))
+    scale = D ** -0.5
+    out, lse = _C.fwd(qh, kh, vh, scale, True, -1, 0, 0.0, None, 0.0, 0)
+    print("[bwd] S=16384 H=32 causal: dS path", flush=True)
+    ds = [_C.bwd(doh, qh, kh, vh, out, lse, scale, True, -1, 0, 0.0, None, 0.0, 0) for _ in range(2)]
+    torch.cuda.synchronize()
+    for a, b in zip(*ds):
+        assert torch.equal(a, b), "dS path differs between runs"
+    print("[bwd] S=16384 H=32 causal: recomputing path", flush=True)
+    rc = _C.bwd(doh, qh, kh, vh, out, lse, scale, True, -1, 0, 0.0, None, 0.0, 0, ds_max_bytes=0)
+    torch.cuda.synchronize()
+    assert torch.equal(ds[0][2], rc[2]), "dV differs between paths"
+    for i, name in ((0, "dQ"), (1, "dK")):
+        e = ((ds[0][i].float() - rc[i].float()).norm() / rc[i].float().norm()).item()
+        assert torch.isfinite(ds[0][i]).all() and e <= 1e-3, f"{name} of the two paths: rel_rms {e:.3e}"
