@@ -176,16 +176,21 @@ __device__ __forceinline__ int kofs(int r, int c, int HD, int KSW) {
 }
 
 // Raw buffer resource over [base, base + nbytes): 16-byte loads at offsets >= nbytes return
-// zeros, so tile loads need no per-lane condition. nbytes is clamped to the 32-bit range; the
-// third descriptor word selects 32-bit raw (untyped) access on gfx9-family parts.
+// zeros, so tile loads need no per-lane condition. nbytes is clamped to [0, kBufMax]; the third
+// descriptor word selects 32-bit raw (untyped) access on gfx9-family parts. kBufMax stays below
+// kBufZero, so a load at offset kBufZero always reads zeros: the zero columns of a padded head
+// dim load from there (no select, no branch).
 // (The clamp tests the high word with 32-bit compares, which stay on the scalar unit; a 64-bit
 // ordered compare has no scalar form and goes to the VALU. The empty asm makes the high word
 // opaque: without it the compiler folds `hi < 0` back into the 64-bit `nbytes < 0`. Its "s"
 // constraint also states that the byte count is uniform, as every descriptor field must be.)
+constexpr unsigned kBufMax = 0xFFFFFF00u;
+constexpr int kBufZero = (int)0xFFFFFFF0u;  // as a byte offset: past every descriptor's range
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, long long nbytes) {
   int hi = (int)(nbytes >> 32);
   asm("" : "+s"(hi));
-  const unsigned n = hi < 0 ? 0u : (hi > 0 ? 0xFFFFFFFFu : (unsigned)nbytes);
+  unsigned n = hi < 0 ? 0u : (hi > 0 ? kBufMax : (unsigned)nbytes);
+  n = n > kBufMax ? kBufMax : n;
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)n, 0x00020000);
 }
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff) {

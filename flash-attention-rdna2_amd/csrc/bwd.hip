@@ -139,15 +139,12 @@ bwd_dq_kernel(FableBwdParams p, int nqt) {
   const bool kloader = wave < C::NW / 2;
   const int lt = kloader ? tid : tid - C::HALF;
   const long long sstride = kloader ? p.ks.s : p.vs.s;
-  // chunks in the zero columns (>= p.D) load the row's first chunk and are replaced by zeros
-  const bool padded = HDr < C::HD;
+  // chunks in the zero columns (>= p.D) load from kBufZero, which reads zeros
   int voff[C::PER];
-  bool cok[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
     const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
-    cok[j] = 8 * c < HDr;
-    voff[j] = r * (int)(sstride * 2) + (cok[j] ? 16 * c : 0);
+    voff[j] = 8 * c < HDr ? r * (int)(sstride * 2) + 16 * c : kBufZero;
   }
   u32x4 ld[C::PER];
   auto gload = [&](int kb) {
@@ -158,10 +155,6 @@ bwd_dq_kernel(FableBwdParams p, int nqt) {
   };
   auto lstore = [&](int stage) {
     T* base = lds + stage * C::STAGE + (kloader ? 0 : C::KT);
-    if (padded) {  // (at the store, which waits for the loads anyway)
-#pragma unroll
-      for (int j = 0; j < C::PER; j++) ld[j] = cok[j] ? ld[j] : u32x4{0, 0, 0, 0};
-    }
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int idx = lt + j * C::HALF, r = idx / C::DCH, c = idx % C::DCH;
@@ -330,14 +323,11 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
   // unconditionally (clamped row) and turned into log2-domain LSE / D at store time.
   static_assert((C::BQ * C::DCH) % C::NT == 0, "Q/dO slot split");
   constexpr int QJ = C::BQ * C::DCH / C::NT;
-  const bool padded = HDr < C::HD;  // zero-column chunks: first chunk loaded, zeros stored
-  int voff[C::PER];
-  bool cok[C::PER];
+  int voff[C::PER];  // zero-column chunks load from kBufZero, which reads zeros
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
     const int ci = tid + (j < QJ ? j : j - QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
-    cok[j] = 8 * c < HDr;
-    voff[j] = r * (int)((j < QJ ? p.qs.s : p.dos.s) * 2) + (cok[j] ? 16 * c : 0);
+    voff[j] = 8 * c < HDr ? r * (int)((j < QJ ? p.qs.s : p.dos.s) * 2) + 16 * c : kBufZero;
   }
   u32x4 ld[C::PER];
   float lraw = 0.0f;
@@ -360,10 +350,6 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
   };
   auto lstore = [&](int stage) {
     T* base = lds + stage * C::STAGE;
-    if (padded) {  // zero columns (at the store, which waits for the loads anyway)
-#pragma unroll
-      for (int j = 0; j < C::PER; j++) ld[j] = cok[j] ? ld[j] : u32x4{0, 0, 0, 0};
-    }
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int ci = tid + (j < QJ ? j : j - QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
@@ -557,16 +543,12 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   // Q/dO tiles through buffer descriptors over rows qt0..SQ-1 (rows past SQ read as zeros);
   // each thread's first QJ chunk slots are Q, the rest dO. LSE/D row values are loaded
   // unconditionally (clamped row) and turned into log2-domain LSE / D at store time.
-  // (NT is a multiple of DCH, so a thread's chunks all sit in column tid % DCH: one test for
-  // the zero columns, whose chunks load the row's first chunk and are replaced by zeros)
-  static_assert(C::NT % C::DCH == 0, "one column per thread");
-  const bool cok = 8 * (tid % C::DCH) < HDr;
-  const bool zcol = !cok, padded = HDr < C::HD;
+  // chunks in the zero columns (>= p.D) load from kBufZero, which reads zeros
   int voff[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
     const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
-    voff[j] = r * (int)((j < C::QJ ? p.qs.s : p.dos.s) * 2) + (cok ? 16 * c : 0);
+    voff[j] = 8 * c < HDr ? r * (int)((j < C::QJ ? p.qs.s : p.dos.s) * 2) + 16 * c : kBufZero;
   }
   // NSET register sets: tile it+NSET is loaded while tile it+1 (loaded NSET-1 iterations
   // earlier) is stored, so every global load has NSET iterations to land
@@ -622,12 +604,6 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   auto lstore = [&](auto set, int stage) {
     constexpr int S = decltype(set)::value;
     T* base = lds + stage * C::STAGE;
-    // zero columns: stored as zeros (at the store, which waits for the loads anyway; zeroing
-    // the registers at the load would make the compiler wait for the loads there)
-    if (padded) {
-#pragma unroll
-      for (int j = 0; j < C::PER; j++) ld[S][j] = zcol ? u32x4{0, 0, 0, 0} : ld[S][j];
-    }
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
@@ -972,17 +948,14 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
     d_kb32 += C::NKB;
   };
 
-  // a head dim p.D below C::HD runs with zero columns (see bwd_dq_kernel); NT is a multiple of
-  // DCH, so a thread's chunks all sit in column tid % DCH
-  static_assert(C::NT % C::DCH == 0, "one column per thread");
+  // a head dim p.D below C::HD runs with zero columns (see bwd_dq_kernel): their chunks load
+  // from kBufZero, which reads zeros
   const int HDr = p.D;
-  const bool cok = 8 * (tid % C::DCH) < HDr;
-  const bool zcol = !cok, padded = HDr < C::HD;
   int voff[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
     const int idx = tid + j * C::NT, r = idx / C::DCH, c = idx % C::DCH;
-    voff[j] = r * (int)(p.ks.s * 2) + (cok ? 16 * c : 0);
+    voff[j] = 8 * c < HDr ? r * (int)(p.ks.s * 2) + 16 * c : kBufZero;
   }
   u32x4 ld[NS][C::PER];
   const T* k_ptr = Kg + (long long)kstart * p.ks.s;
@@ -999,10 +972,6 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
   auto lstore = [&](auto set, int stage) {
     constexpr int S = decltype(set)::value;
     T* base = lds + stage * C::KT;
-    if (padded) {  // zero columns stored as zeros (see the pair kernel)
-#pragma unroll
-      for (int j = 0; j < C::PER; j++) ld[S][j] = zcol ? u32x4{0, 0, 0, 0} : ld[S][j];
-    }
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int idx = tid + j * C::NT, r = idx / C::DCH, c = idx % C::DCH;

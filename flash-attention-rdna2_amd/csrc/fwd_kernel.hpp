@@ -179,27 +179,22 @@ fwd_kernel(FableFwdParams p, int nqt) {
   const int kvalid = min(SK, kstart + ntiles * C::BC);
   // chunk j of this thread: ci = tid + j*NT, row ci / DCH, 16-byte column chunk ci % DCH. In the
   // last round (KTAIL) threads past the tile's chunks load row 0 again and store nothing;
-  // chunks in the zero columns (>= p.HD) are loaded from the row's first chunk and stored as
-  // zeros (`padded`, uniform), so no load depends on a lane condition. (The zeros are put in at
-  // the LDS store, which waits for the load anyway: a select right after the load would make
-  // the compiler wait for the load there.)
+  // chunks in the zero columns (>= p.HD) load from kBufZero, past the descriptor's range, which
+  // reads zeros: no load depends on a lane condition and nothing is selected afterwards.
   // When NT is a multiple of DCH (every shape whose head dim is a power of two) a thread's
   // chunks share one column and sit RSTEP rows apart, so the LDS addresses are one base plus
   // immediate offsets; other shapes keep one address per chunk.
   constexpr bool kRowStep = C::NT % C::DCH == 0 && !C::KTAIL;
   constexpr int RSTEP = kRowStep ? C::NT / C::DCH : 0;
-  const bool padded = HDr < C::HD;
   int koff[C::KJ], voff[C::KJ], lko[C::KJ], lvo[C::KJ];
-  bool cok[C::KJ];
 #pragma unroll
   for (int j = 0; j < C::KJ; j++) {
     const int ci = tid + j * C::NT;
     const bool live = !C::KTAIL || ci < C::KCH;
     const int r = live ? ci / C::DCH : 0, c = live ? ci % C::DCH : 0;
-    cok[j] = 8 * c < HDr;
-    const int cg = cok[j] ? c : 0;
-    koff[j] = r * (int)(p.sK.s * 2) + 16 * cg;
-    voff[j] = r * (int)(p.sV.s * 2) + 16 * cg;
+    const bool cok = 8 * c < HDr;
+    koff[j] = cok ? r * (int)(p.sK.s * 2) + 16 * c : kBufZero;
+    voff[j] = cok ? r * (int)(p.sV.s * 2) + 16 * c : kBufZero;
     if constexpr (kRowStep) {
       lko[j] = (tid / C::DCH) * C::KSTR + 8 * (tid % C::DCH) + j * RSTEP * C::KSTR;
       lvo[j] = (tid / C::DCH) * C::VSTR + 8 * (tid % C::DCH) + j * RSTEP * C::VSTR;
@@ -221,20 +216,12 @@ fwd_kernel(FableFwdParams p, int nqt) {
   };
   auto lstore_k = [&](int st) {
     T* b = kl + st * C::KTILE;
-    if (padded) {
-#pragma unroll
-      for (int j = 0; j < C::KJ; j++) ldk[j] = cok[j] ? ldk[j] : u32x4{0, 0, 0, 0};
-    }
 #pragma unroll
     for (int j = 0; j < C::KJ; j++)
       if (!C::KTAIL || j < C::KJ - 1 || lko[j] >= 0) *(u32x4*)(b + lko[j]) = ldk[j];
   };
   auto lstore_v = [&](int st) {
     T* b = vl + st * C::VTILE;
-    if (padded) {
-#pragma unroll
-      for (int j = 0; j < C::KJ; j++) ldv[j] = cok[j] ? ldv[j] : u32x4{0, 0, 0, 0};
-    }
 #pragma unroll
     for (int j = 0; j < C::KJ; j++)
       if (!C::KTAIL || j < C::KJ - 1 || lvo[j] >= 0) *(u32x4*)(b + lvo[j]) = ldv[j];
@@ -430,10 +417,14 @@ fwd_kernel(FableFwdParams p, int nqt) {
     resc[i] = false;
     corr[i] = 1.0f;
   }
+  // resc is wave-uniform (a ballot); readfirstlane states it, so the branch is a scalar one.
+  // As a divergent (exec-mask) branch, the compiler read every AGPR-held O accumulator into
+  // VGPRs ahead of it on every tile (128 extra VALU per tile at head dim 256) and used the
+  // copies only when the branch was taken.
   auto rescale = [&]() {
 #pragma unroll
     for (int i = 0; i < QB; i++)
-      if (resc[i]) {
+      if (__builtin_amdgcn_readfirstlane((int)resc[i])) {
 #pragma unroll
         for (int db = 0; db < C::NDB; db++) oacc[i][db] *= corr[i];
         resc[i] = false;
