@@ -206,4 +206,20 @@ __device__ __forceinline__ int xcd_remap(int L, int N) {
   return x * per + (x < rem ? x : rem) + idx;
 }
 
+// blockIdx.x -> work index for a grid of N = (groups) x G work items, where the G consecutive
+// items of a group read the same K/V (one head of one sequence, with its GQA siblings): whole
+// groups are dealt round-robin to the XCDs (group g to XCD g % 8) and each XCD runs its groups
+// one after another, so a group's K/V stays in one L2 and every XCD gets every eighth group.
+// (Cutting the grid into 8 contiguous ranges instead gave XCD x the x-th eighth of the
+// groups: with packed sequences of unequal lengths that is one XCD per sequence, and the XCD
+// holding the longest sequence set the run time, 1.6x the balanced one at 8 causal sequences of
+// 1.2k..6.9k rows.) Groups past the last full round of 8 are cut into 8 contiguous ranges.
+__device__ __forceinline__ int xcd_group_remap(int L, int N, int G) {
+  constexpr int kXcd = 8;
+  const int M = (N / G / kXcd) * kXcd * G;  // items of the full rounds
+  if (L >= M) return M + xcd_remap(L - M, N - M);
+  const int x = L % kXcd, k = L / kXcd;
+  return (x + kXcd * (k / G)) * G + k % G;
+}
+
 }  // namespace fa

@@ -1,6 +1,6 @@
 // fwd_kernel.hpp — exact attention forward for gfx950 (MI355X), fp16 and bf16: the kernel and
-// its launcher, instantiated per head dim by fwd_d64.hip / fwd_d128.hip / fwd_d256.hip (one
-// translation unit each, so they compile in parallel).
+// its launcher, instantiated per kernel width by fwd_d32.hip .. fwd_d256.hip (one translation
+// unit each, so they compile in parallel).
 //
 // Replaces the reference forward (kernels/fa_forward.hip:52-313 kernel, :424-451 launcher);
 // same math and masking contract (FableFwdParams in include/fable_attn_abi.h), new design:
@@ -23,14 +23,14 @@
 //    so they carry no per-lane condition and stay in flight across a whole iteration.
 //  * online softmax in the log2 domain (one FMA + v_exp_f32 per score). The running max only
 //    moves when a tile raises it by more than 2^8 (probabilities then stay <= 256, exact in
-//    fp16/bf16 range), so the O rescale is rare; it is skipped when no lane needs it. fp16 row
-//    sums add the rounded probabilities pairwise (v_dot2, fp32 accumulate), the values the PV
-//    product uses.
+//    fp16/bf16 range), so the O rescale is rare; it is skipped when no lane needs it. Row sums
+//    add the fp32 probabilities.
 //  * tiles entirely outside the causal / window / chunk range are never loaded; the leading
 //    tiles every row of the workgroup sees in full run without mask code (template CAUSAL/FEAT
 //    split as in the reference's launch_cfg, fa_forward.hip:409-421).
-//  * the workgroup -> (q tile, head, batch) map is XCD-aware (consecutive work items of one
-//    head share an XCD's L2) and, for causal, starts with the heaviest q tiles.
+//  * the workgroup -> (q tile, head, batch) map is XCD-aware (the q tiles of one K/V head of
+//    one sequence run on one XCD, whose L2 they share; heads are dealt round-robin to the XCDs)
+//    and, for causal, starts with the heaviest q tiles.
 #pragma once
 #include <type_traits>
 
@@ -84,7 +84,7 @@ fwd_kernel(FableFwdParams p, int nqt) {
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
 
   // ---- work item -> (sequence z, head h, q tile)
-  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt * p.gqa);
   const int qti = w % nqt, zh = w / nqt;
   const int h = zh % p.NH, z = zh / p.NH;
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
