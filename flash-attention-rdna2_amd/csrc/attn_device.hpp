@@ -206,20 +206,33 @@ __device__ __forceinline__ int xcd_remap(int L, int N) {
   return x * per + (x < rem ? x : rem) + idx;
 }
 
-// blockIdx.x -> work index for a grid of N = (groups) x G work items, where the G consecutive
-// items of a group read the same K/V (one head of one sequence, with its GQA siblings): whole
-// groups are dealt round-robin to the XCDs (group g to XCD g % 8) and each XCD runs its groups
-// one after another, so a group's K/V stays in one L2 and every XCD gets every eighth group.
-// (Cutting the grid into 8 contiguous ranges instead gave XCD x the x-th eighth of the
-// groups: with packed sequences of unequal lengths that is one XCD per sequence, and the XCD
-// holding the longest sequence set the run time, 1.6x the balanced one at 8 causal sequences of
-// 1.2k..6.9k rows.) Groups past the last full round of 8 are cut into 8 contiguous ranges.
-__device__ __forceinline__ int xcd_group_remap(int L, int N, int G) {
-  constexpr int kXcd = 8;
-  const int M = (N / G / kXcd) * kXcd * G;  // items of the full rounds
+// blockIdx.x -> work index for a grid of N = (K/V groups) x gqa x U work items: work index
+// w = (group * gqa + sibling) * U + u, where a K/V group is one K/V head of one sequence, its
+// gqa query heads (siblings) read the same K/V, and u runs over the U items of one query head
+// (q tiles, heaviest first under a causal mask).
+//  * Whole K/V groups are dealt round-robin to the XCDs (group g to XCD g % 8), so a group's
+//    K/V stays in one L2 and every XCD gets every eighth group. (Cutting the grid into 8
+//    contiguous ranges instead gave XCD x the x-th eighth of the groups: with packed sequences
+//    of unequal lengths that is one XCD per sequence, and the XCD holding the longest one set
+//    the run time, 1.6x the balanced one at 8 causal sequences of 1.2k..6.9k rows.)
+//  * An XCD with at most kUMajorItems items (a few per workgroup slot) runs them u-major (u,
+//    then group, then sibling): the heaviest tiles of all its heads start first and the light
+//    ones fill the end. That balanced causal S=4096 H=32 (two workgroups per slot) 1.24x better
+//    than group after group. A larger share runs group after group, its concurrent workgroups
+//    mostly on one head, whose K/V they then share in L2: u-major over 16 packed
+//    sequence-heads per XCD cost 17% (C5-like windows) to 32% (causal, head dim 256).
+//  * Groups past the last full round of 8 are cut into 8 contiguous ranges.
+__device__ __forceinline__ int xcd_group_remap(int L, int N, int U, int gqa) {
+  constexpr int kXcd = 8, kUMajorItems = 512;
+  const int G = U * gqa;                   // items per K/V group
+  const int R = N / G / kXcd;              // groups per XCD in the full rounds
+  const int M = R * kXcd * G;
   if (L >= M) return M + xcd_remap(L - M, N - M);
-  const int x = L % kXcd, k = L / kXcd;
-  return (x + kXcd * (k / G)) * G + k % G;
+  const int x = L % kXcd, k = L / kXcd;    // k < R * G
+  if (R * G > kUMajorItems) return (x + kXcd * (k / G)) * G + k % G;
+  const int u = k / (R * gqa), v = k % (R * gqa);
+  const int group = x + kXcd * (v / gqa), sib = v % gqa;
+  return (group * gqa + sib) * U + u;
 }
 
 }  // namespace fa
