@@ -735,7 +735,13 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     lstore(std::integral_constant<int, (S + 1) % NSET>{}, (it + 1) & 3);  // tile it+1
     __syncthreads();
   };
-  // dP-wave step `it`: tile t = it-1 (a step behind the S-wave): dP, dS, dK += Q^T . dS
+  // dP-wave step `it`: tile t = it-1 (a step behind the S-wave): dP, dS; dK += Q^T . dS of
+  // tile t-1 (the dS of the step before). Both waves of a SIMD start a step with matrix-core
+  // work after the barrier; deferring the dK product puts the dP-wave's two products first and
+  // its dS VALU work last, beside the S-wave's dV product, instead of both waves running
+  // their VALU work at once. The Q tile of t-1 is still in its stage: the stage is refilled
+  // with tile t+3 at the end of step it+1.
+  V8 pS[2] = {bitcast<V8>(u32x4{0, 0, 0, 0}), bitcast<V8>(u32x4{0, 0, 0, 0})};
   auto d_step = [&](auto set, int it) {
     constexpr int S = decltype(set)::value;
     gload(set);
@@ -745,8 +751,8 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     if (t >= 0) w_next();
     const int st = t & 3;
     const T* qs = lds + st * C::STAGE;
+    tprod(lds + ((t - 1) & 3) * C::STAGE, pS);  // dK^T += Q^T . dS (tile t-1)
     const f32x16 dpv = rowprod(qs + C::TT);
-    V8 pS[2];
 #pragma unroll
     for (int rq = 0; rq < 4; rq++) {
       const f32x4 d4 = *(const f32x4*)&rowv[st][1][8 * rq + 4 * hh];
@@ -764,7 +770,6 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
         pS[r >> 3][r & 7] = (T)ds;
       }
     }
-    tprod(qs, pS);  // dK^T += Q^T . dS
     if constexpr (DSW) {  // dS tile (32 queries x this pair's 32 keys) to the workspace
       if (act) {
         T* dst = ds_head_tiles<T>(p, b, kvh * p.gqa + hg, ds_T) + (long long)(ds_row + (qt0 >> 5)) * 1024 +
@@ -782,8 +787,10 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   // rounds; both roles run the same number of barriers
   if (total > 0) {
     if (dpw) {
-      for (int it = 0; it <= total; it += NSET)
+      int it = 0;
+      for (; it <= total; it += NSET)
         for_sets(std::make_integer_sequence<int, NSET>{}, [&](auto set) { d_step(set, it + decltype(set)::value); });
+      tprod(lds + ((it - 2) & 3) * C::STAGE, pS);  // the last step's tile (it-1 was the last step)
     } else {
       for (int it = 0; it <= total; it += NSET)
         for_sets(std::make_integer_sequence<int, NSET>{}, [&](auto set) { s_step(set, it + decltype(set)::value); });
