@@ -14,11 +14,11 @@ bytes per launch from the calibrated rocprofv3 PMC tables under profiles/.
 `cpu_baseline` times the exact fp32 torch reference (oracle/torch_ref.py) on the host cores over
 a bounded sample of the same workload and scales to the metric's unit with the same numerator.
 `extra` holds the other BASELINE.json configs (C1, C2 at S=4096/8192, C3 backward, C4 paged
-decode, C5 varlen), each measured the same way (at least 3 warmup and 20 timed steps, mean and
-median of the per-step HIP-event times) and each with its own `roofline` block (over the whole
-step's kernels) and `cpu_baseline` (the same torch reference path on CPU tensors: per-head
-autograd for C3, pages gathered per sequence for C4, per sequence and head for C5); they are
-not the headline.
+decode, C5 varlen), each measured the same way (at least 3 untimed steps and 150 ms of untimed
+load, then 20 timed steps; mean and median of the per-step HIP-event times) and each with its
+own `roofline` block (over the whole step's kernels) and `cpu_baseline` (the same torch
+reference path on CPU tensors: per-head autograd for C3, pages gathered per sequence for C4,
+per sequence and head for C5); they are not the headline.
 """
 import argparse
 import json
@@ -40,14 +40,21 @@ def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
 
-def time_steps(fn, steps, warmup, per_step=None):
-    """Returns (wall ms/step, HIP-event ms/step) over exactly `steps` calls after `warmup`.
-    With a list as `per_step`, also appends each step's own HIP-event time to it (an event
-    pair per step, recorded on the same stream, for medians)."""
+def time_steps(fn, steps, warmup, per_step=None, warm_ms=0.0):
+    """Returns (wall ms/step, HIP-event ms/step) over exactly `steps` calls after `warmup`
+    untimed calls, and after that as many more untimed calls as it takes to fill `warm_ms` of
+    wall time (the clocks of an idle MI355X take ~40 ms of load to settle: a 20-step window
+    right after idle read C5 at 363 -> 457 TFLOP/s and S=8192 at 805 -> 976 over its first
+    50 ms). With a list as `per_step`, also appends each step's own HIP-event time to it (an
+    event pair per step, recorded on the same stream, for medians)."""
     import torch
+    t_warm = time.perf_counter()
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    while (time.perf_counter() - t_warm) * 1e3 < warm_ms:
+        fn()
+        torch.cuda.synchronize()
     st = torch.cuda.current_stream()
     ev_all = [torch.cuda.Event(enable_timing=True) for _ in range(steps + 1)]
     t0 = time.perf_counter()
@@ -61,6 +68,9 @@ def time_steps(fn, steps, warmup, per_step=None):
     if per_step is not None:
         per_step += [ev_all[i].elapsed_time(ev_all[i + 1]) for i in range(steps)]
     return wall, ev
+
+
+EXTRA_WARM_MS = 150.0   # untimed warm time of each extra config (not the headline)
 
 
 def _median(x):
@@ -87,7 +97,7 @@ def _cpu_threads():
     return cores
 
 
-def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", seed=0):
+def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", seed=0, warm_ms=0.0):
     import torch
     from fable_attn import flash_attn_func
     dt = torch.float16 if dtype == "fp16" else torch.bfloat16
@@ -97,7 +107,7 @@ def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", see
     v = torch.randn(B, S, H, D, device="cuda", dtype=dt, generator=g)
     flops = 4.0 * B * H * S * S * D / (2 if causal else 1)
     per = []
-    wall, ev = time_steps(lambda: flash_attn_func(q, k, v, causal=causal), steps, warmup, per)
+    wall, ev = time_steps(lambda: flash_attn_func(q, k, v, causal=causal), steps, warmup, per, warm_ms)
     return {"S": S, "H": H, "D": D, "B": B, "causal": causal, "dtype": dtype, "flops": flops,
             "ms": wall, "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
             "kernel_tflops": flops / (ev * 1e-3) / 1e12, "kernel_ms_median": _median(per),
@@ -106,7 +116,7 @@ def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", see
                 FWD_C2_KERNEL if (D == 128 and causal) else FWD_C1_KERNEL))}
 
 
-def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0):
+def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0, warm_ms=EXTRA_WARM_MS):
     """C3: causal bf16 backward, timed without the forward; bitwise-identical check over 3 runs."""
     import torch
     from fable_attn import _C
@@ -123,7 +133,7 @@ def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0):
     ref = step()
     same = all(all(torch.equal(a, b) for a, b in zip(ref, step())) for _ in range(2))
     per = []
-    wall, ev = time_steps(step, steps, warmup, per)
+    wall, ev = time_steps(step, steps, warmup, per, warm_ms)
     flops = 2.5 * 4.0 * B * H * S * S * D / 2
     return {"B": B, "S": S, "H": H, "D": D, "dtype": "bf16", "flops": flops, "ms": wall,
             "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
@@ -169,7 +179,7 @@ def bench_decode(steps, warmup, batch=16, Hq=32, Hk=8, D=128, ctx=32768, page=25
     cs = torch.full((batch,), ctx, dtype=torch.int32, device="cuda")
     f = lambda: flash_attn_with_kvcache(q, kc, vc, cache_seqlens=cs, block_table=bt)
     per = []
-    wall, ev = time_steps(f, steps, warmup, per)
+    wall, ev = time_steps(f, steps, warmup, per, EXTRA_WARM_MS)
     nbytes = 2.0 * batch * ctx * Hk * D * 2
     res = {"batch": batch, "Hq": Hq, "Hk": Hk, "D": D, "ctx": ctx, "page": page, "bytes": nbytes,
            "ms": wall, "kernel_ms": ev, "GBs": nbytes / (wall * 1e-3) / 1e9,
@@ -220,7 +230,7 @@ def bench_varlen(steps, warmup, H=16, D=256, seed=0, cpu_heads=0):
     f = lambda: flash_attn_varlen_func(q, k, v, cu, cu, max(lens), max(lens), causal=True,
                                        window_size=(512, 0), softcap=30.0, softmax_scale=D ** -0.5)
     per = []
-    wall, ev = time_steps(f, steps, warmup, per)
+    wall, ev = time_steps(f, steps, warmup, per, EXTRA_WARM_MS)
     pairs = sum(sum(min(i, 512) + 1 for i in range(L)) for L in lens)
     flops = 4.0 * D * H * pairs
     res = {"lens": lens, "H": H, "D": D, "flops": flops, "ms": wall, "kernel_ms": ev,
@@ -341,6 +351,50 @@ def summarize_mfma(d, kernel_re=None):
     return "\n".join(out)
 
 
+def summarize_counters(dirs, kernel_re):
+    """Markdown table of every counter of one or more `rocprofv3 --pmc` runs, averaged per
+    dispatch of the kernels matching `kernel_re`, with the ratios used to rank what limits a
+    kernel: mean clock, matrix-core busy share, VALU-and-MFMA co-execution share, instructions
+    per MFMA, and the wave-cycle shares spent waiting."""
+    agent = [r for r in _rocprof_rows(dirs[0], "agent_info.csv") if int(r.get("Simd_Count") or 0) > 0][0]
+    simds, nxcc = int(agent["Simd_Count"]), int(agent["Num_Xcc"])
+    acc, ns = {}, {}
+    for d in dirs:
+        for r in _rocprof_rows(d, "counter_collection.csv"):
+            if not re.search(kernel_re, r["Kernel_Name"]):
+                continue
+            acc.setdefault(r["Counter_Name"], []).append(float(r["Counter_Value"]))
+            ns.setdefault((d, r["Dispatch_Id"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    avg = {c: sum(v) / len(v) for c, v in acc.items()}
+    out = ["| counter | average per dispatch |", "|---|---|"]
+    out += [f"| {c} | {v:.4g} |" for c, v in sorted(avg.items())]
+    out += ["", "| derived | value |", "|---|---|"]
+    t = sum(ns.values()) / len(ns)
+    g = avg.get("GRBM_GUI_ACTIVE")
+    if g:
+        cyc = g / nxcc
+        out.append(f"| mean clock (GRBM_GUI_ACTIVE per XCD / duration) | {cyc / t:.2f} GHz |")
+        for c, label in (("SQ_VALU_MFMA_BUSY_CYCLES", "matrix cores busy"),
+                         ("SQ_VALU_MFMA_COEXEC_CYCLES", "VALU and matrix cores busy together")):
+            if c in avg:
+                out.append(f"| {label} (share of SIMD cycles) | {avg[c] / (simds * cyc):.1%} |")
+    m = avg.get("SQ_INSTS_MFMA")
+    if m:
+        for c in ("SQ_INSTS_VALU", "SQ_INSTS_VALU_TRANS_F32", "SQ_INSTS_LDS", "SQ_INSTS_SALU"):
+            if c in avg:
+                out.append(f"| {c} per MFMA instruction | {avg[c] / m:.2f} |")
+    w = avg.get("SQ_WAVE_CYCLES")
+    if w:
+        for c in ("SQ_WAIT_ANY", "SQ_WAIT_INST_ANY", "SQ_WAIT_INST_LDS", "SQ_ACTIVE_INST_VALU",
+                  "SQ_ACTIVE_INST_LDS"):
+            if c in avg:
+                out.append(f"| {c} / SQ_WAVE_CYCLES | {avg[c] / w:.1%} |")
+    out.append("")
+    out.append(f"Agent: {simds} SIMDs, {nxcc} XCDs; {len(ns)} dispatches, {t / 1e3:.1f} us average "
+               f"(counter collection slows a dispatch; read the ratios).")
+    return "\n".join(out)
+
+
 def summarize_stats(d, kernel_re=None, skip=0):
     """Markdown table of the `rocprofv3 --kernel-trace --stats` kernel statistics, with the
     average over the dispatches after the first `skip` of each kernel (bench.py's warmup calls)
@@ -369,8 +423,51 @@ FWD_C1_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi64E.*ELb0ELb0ELb0EEEv14Fa
 BWD_C3_KERNELS = (r"_ZN2fa15bwd_dsum_kernelIDF16b.*", r"_ZN2fa20bwd_dkdv_pair_kernelIDF16b.*",
                   r"_ZN2fa16bwd_dq_ds_kernelIDF16b.*")
 DEC_C4_KERNELS = (r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0EEEv14FableDecParamsiii",
-                  r"_ZN2fa17dec_combine_kernelIDF16_Li128EEEv14FableDecParams")
-VARLEN_C5_KERNEL = r"_ZN2fa10fwd_kernelIDF16b_NS_6FwdCfgILi256E.*ELb1ELb1ELb0EEEv14FableFwdParamsi"
+                  r"_ZN2fa18dec_combine_kernelIDF16_Li128EEEv14FableDecParams")
+VARLEN_C5_KERNEL = r"_ZN2fa10fwd_kernelIDF16bNS_6FwdCfgILi256E.*ELb1ELb1ELb0EEEv14FableFwdParamsi"
+
+
+def summarize_parity(path):
+    """Markdown table of the measured parity errors that the GPU tests log (one JSON line per
+    checked case, tests/helpers.py:log_errors), grouped by test and dtype: cases, the largest
+    rel_rms of O, the largest |LSE| error, and per gradient the largest rel_rms with the bound
+    it was held to (the BASELINE.json bound, or 1.5x the case's rounding-model floor where that
+    floor exceeds 2/3 of it) and the largest floor."""
+    import json
+    tol = {"f16": 5e-4, "bf16": 4e-3, "f32": 1e-5}
+    gtol = {"f16": 5e-4, "bf16": 4e-3, "f32": 1e-4}
+    groups = {}
+    for line in open(path):
+        line = line.strip()
+        if line:
+            r = json.loads(line)
+            groups.setdefault((r["test"], r["dtype"]), []).append(r)
+
+    def worst(rs, key):
+        v = [r[key] for r in rs if r.get(key) is not None]
+        return max(v) if v else None
+
+    def fmt(x):
+        return "-" if x is None else f"{x:.2e}"
+
+    out = ["| test | dtype | cases | O rel_rms (bound) | LSE abs (bound 1e-3) | dQ | dK | dV | "
+           "largest gradient floor |", "|---|---|---|---|---|---|---|---|---|"]
+    for (test, dt), rs in sorted(groups.items()):
+        o = worst(rs, "o")
+        ocol = "-" if o is None else f"{o:.2e} ({tol.get(dt, 0):.0e})"
+        cols = []
+        for g in ("dq", "dk", "dv"):
+            e = [(r[g], max(gtol[dt], 1.5 * r[g + "_floor"]) if (r.get(g + "_floor") or 0) > gtol[dt] * 2 / 3
+                  else gtol[dt]) for r in rs if r.get(g) is not None]
+            if not e:
+                cols.append("-")
+                continue
+            m = max(e, key=lambda t: t[0] / t[1])
+            cols.append(f"{max(x for x, _ in e):.2e} (worst {m[0] / m[1]:.0%} of its bound)")
+        fl = [r[g + "_floor"] for r in rs for g in ("dq", "dk", "dv") if r.get(g + "_floor") is not None]
+        out.append(f"| {test} | {dt} | {len(rs)} | {ocol} | {fmt(worst(rs, 'lse'))} | "
+                   + " | ".join(cols) + f" | {fmt(max(fl) if fl else None)} |")
+    return "\n".join(out)
 
 
 def profiled_traffic(kernel_res):
@@ -419,7 +516,8 @@ def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=3)
+    # 30 untimed headline steps (~65 ms) bring an idle GPU's clocks to their loaded level
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=32)
     ap.add_argument("--extras", default="fwd,bwd,decode,varlen")
@@ -432,6 +530,10 @@ def main():
     ap.add_argument("--summarize-mfma", metavar="DIR",
                     help="print the matrix-core utilisation table of a rocprofv3 --pmc "
                          "SQ_VALU_MFMA_BUSY_CYCLES GRBM_GUI_ACTIVE run and exit")
+    ap.add_argument("--summarize-counters", nargs="+", metavar="DIR",
+                    help="print every counter of rocprofv3 --pmc runs for --kernel-filter and exit")
+    ap.add_argument("--summarize-parity", metavar="JSONL",
+                    help="print the table of the parity errors the GPU tests logged and exit")
     ap.add_argument("--kernel-filter", default=None, help="regex on kernel symbols (summaries)")
     ap.add_argument("--skip", type=int, default=0, help="leading dispatches to skip (summaries)")
     a = ap.parse_args()
@@ -443,6 +545,12 @@ def main():
         return
     if a.summarize_mfma:
         print(summarize_mfma(a.summarize_mfma, a.kernel_filter))
+        return
+    if a.summarize_counters:
+        print(summarize_counters(a.summarize_counters, a.kernel_filter or "."))
+        return
+    if a.summarize_parity:
+        print(summarize_parity(a.summarize_parity))
         return
     if a.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build measures one GPU only (the reference has no multi-GPU "
@@ -462,11 +570,11 @@ def main():
         try:
             if name == "fwd":
                 for S in (4096, 8192):
-                    r = bench_fwd(S, max(a.steps, 20), max(3, a.warmup))
+                    r = bench_fwd(S, max(a.steps, 20), max(3, a.warmup), warm_ms=EXTRA_WARM_MS)
                     if cpu_on:
                         r["cpu_baseline"] = cpu_baseline(S=S)
                     extra[f"fwd_causal_S{S}"] = r
-                r = bench_fwd(1024, 20, 3, causal=False, H=8, D=64)
+                r = bench_fwd(1024, 20, 3, causal=False, H=8, D=64, warm_ms=EXTRA_WARM_MS)
                 if cpu_on:
                     r["cpu_baseline"] = cpu_baseline(S=1024, H=8, D=64, heads=8, causal=False)
                 extra["fwd_C1_S1024_D64_noncausal"] = r
