@@ -395,20 +395,23 @@ def summarize_counters(dirs, kernel_re):
     return "\n".join(out)
 
 
-def summarize_stats(d, kernel_re=None, skip=0):
+def summarize_stats(d, kernel_re=None, skip=0, last=0):
     """Markdown table of the `rocprofv3 --kernel-trace --stats` kernel statistics, with the
-    average over the dispatches after the first `skip` of each kernel (bench.py's warmup calls)
-    from the kernel trace, which is what bench.py's HIP-event average covers."""
+    average over the dispatches after the first `skip` of each kernel (bench.py's warmup calls),
+    or over the last `last` dispatches of each (bench.py's timed steps come last), from the
+    kernel trace: the dispatches bench.py's HIP-event average covers."""
     trace = {}
     for r in _rocprof_rows(d, "kernel_trace.csv"):
         trace.setdefault(r["Kernel_Name"], []).append(
             (int(r["Start_Timestamp"]), int(r["End_Timestamp"]) - int(r["Start_Timestamp"])))
-    out = [f"| kernel | calls | average us | min us | max us | % of GPU time | average us after {skip} |",
+    col = f"average us of the last {last}" if last else f"average us after {skip}"
+    out = [f"| kernel | calls | average us | min us | max us | % of GPU time | {col} |",
            "|---|---|---|---|---|---|---|"]
     for r in _rocprof_rows(d, "kernel_stats.csv"):
         if kernel_re and not re.search(kernel_re, r["Name"]):
             continue
-        ds = [t for _, t in sorted(trace.get(r["Name"], []))][skip:]
+        ds = [t for _, t in sorted(trace.get(r["Name"], []))]
+        ds = ds[-last:] if last else ds[skip:]
         after = f"{sum(ds) / len(ds) / 1e3:.1f}" if ds else "-"
         out.append(f"| `{r['Name'][:100]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                    f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
@@ -536,12 +539,13 @@ def main():
                     help="print the table of the parity errors the GPU tests logged and exit")
     ap.add_argument("--kernel-filter", default=None, help="regex on kernel symbols (summaries)")
     ap.add_argument("--skip", type=int, default=0, help="leading dispatches to skip (summaries)")
+    ap.add_argument("--last", type=int, default=0, help="average only the last N dispatches (summaries)")
     a = ap.parse_args()
     if a.summarize_pmc:
         print(summarize_pmc(*a.summarize_pmc, kernel_re=a.kernel_filter))
         return
     if a.summarize_stats:
-        print(summarize_stats(a.summarize_stats, a.kernel_filter, a.skip))
+        print(summarize_stats(a.summarize_stats, a.kernel_filter, a.skip, a.last))
         return
     if a.summarize_mfma:
         print(summarize_mfma(a.summarize_mfma, a.kernel_filter))

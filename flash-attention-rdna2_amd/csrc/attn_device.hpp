@@ -215,21 +215,26 @@ __device__ __forceinline__ int xcd_remap(int L, int N) {
 //    contiguous ranges instead gave XCD x the x-th eighth of the groups: with packed sequences
 //    of unequal lengths that is one XCD per sequence, and the XCD holding the longest one set
 //    the run time, 1.6x the balanced one at 8 causal sequences of 1.2k..6.9k rows.)
-//  * An XCD with at most kUMajorItems items (a few per workgroup slot) runs them u-major (u,
+//  * An XCD with at most `umajor_max` items (a few per workgroup slot) runs them u-major (u,
 //    then group, then sibling): the heaviest tiles of all its heads start first and the light
 //    ones fill the end. That balanced causal S=4096 H=32 (two workgroups per slot) 1.24x better
-//    than group after group. A larger share runs group after group, its concurrent workgroups
-//    mostly on one head, whose K/V they then share in L2: u-major over 16 packed
-//    sequence-heads per XCD cost 17% (C5-like windows) to 32% (causal, head dim 256).
+//    than group after group, S=8192 1.04x, the C3 backward 1.07x. A larger share runs group
+//    after group, its concurrent workgroups mostly on one head, whose K/V they then share in
+//    L2: u-major over 16 packed sequence-heads per XCD cost 17% (C5-like windows) to 32%
+//    (causal, head dim 256), and over the 4 heads per XCD of causal S=16384 H=32 it read 1.6x
+//    the HBM bytes (1.80 vs 1.12 GB per launch) for the same time.
 //  * Groups past the last full round of 8 are cut into 8 contiguous ranges.
-__device__ __forceinline__ int xcd_group_remap(int L, int N, int U, int gqa) {
-  constexpr int kXcd = 8, kUMajorItems = 512;
+// u-major limits (items per XCD): the forward kernels keep the 4 heads per XCD of long causal
+// sequences group after group; the backward kernels gain from u-major up to 512
+constexpr int kFwdUMajor = 128, kBwdUMajor = 512;
+__device__ __forceinline__ int xcd_group_remap(int L, int N, int U, int gqa, int umajor_max) {
+  constexpr int kXcd = 8;
   const int G = U * gqa;                   // items per K/V group
   const int R = N / G / kXcd;              // groups per XCD in the full rounds
   const int M = R * kXcd * G;
   if (L >= M) return M + xcd_remap(L - M, N - M);
   const int x = L % kXcd, k = L / kXcd;    // k < R * G
-  if (R * G > kUMajorItems) return (x + kXcd * (k / G)) * G + k % G;
+  if (R * G > umajor_max) return (x + kXcd * (k / G)) * G + k % G;
   const int u = k / (R * gqa), v = k % (R * gqa);
   const int group = x + kXcd * (v / gqa), sib = v % gqa;
   return (group * gqa + sib) * U + u;

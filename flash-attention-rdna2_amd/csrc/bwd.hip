@@ -72,7 +72,7 @@ bwd_dq_kernel(FableBwdParams p, int nqt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
 
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, C::DSPLIT * nqt, p.gqa);
+  const int w = xcd_group_remap(blockIdx.x, gridDim.x, C::DSPLIT * nqt, p.gqa, kBwdUMajor);
   const int dpass = w % C::DSPLIT, w2 = w / C::DSPLIT;  // head-dim slice of dQ owned here
   const int qti = w2 % nqt, zh = w2 / nqt;
   const int h = zh % p.Hq, b = zh / p.Hq;
@@ -275,7 +275,7 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
 
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, C::DSPLIT * nkt, 1);
+  const int w = xcd_group_remap(blockIdx.x, gridDim.x, C::DSPLIT * nkt, 1, kBwdUMajor);
   const int dpass = w % C::DSPLIT, w2 = w / C::DSPLIT;  // head-dim slice of dK/dV owned here
   const int kt = w2 % nkt, zh = w2 / nkt;
   const int kvh = zh % p.Hk, b = zh / p.Hk;
@@ -498,7 +498,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   const bool dpw = wave >= C::NP;  // dP-wave (holds V, accumulates dK)
   const int pair = dpw ? wave - C::NP : wave;
 
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nkt, 1);
+  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nkt, 1, kBwdUMajor);
   const int kt = w % nkt, zh = w / nkt;
   const int kvh = zh % p.Hk, b = zh / p.Hk;
   const BwdSeq sq = bwd_seq(p, b);
@@ -891,7 +891,7 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
 
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt, p.gqa);
+  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt, p.gqa, kBwdUMajor);
   const int qti = w % nqt, zh = w / nqt;
   const int h = zh % p.Hq, b = zh / p.Hq;
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;

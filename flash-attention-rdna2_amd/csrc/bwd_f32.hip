@@ -71,7 +71,7 @@ bwd_dq_f32_kernel(FableBwdParams p, int nqt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, g = lane >> 4;
 
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt, p.gqa);
+  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt, p.gqa, kBwdUMajor);
   const int qti = w % nqt, zh = w / nqt;
   const int h = zh % p.Hq, b = zh / p.Hq;
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
@@ -242,7 +242,7 @@ bwd_dkdv_f32_kernel(FableBwdParams p, int nkt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, g = lane >> 4;
 
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, C::DSPLIT * nkt, 1);
+  const int w = xcd_group_remap(blockIdx.x, gridDim.x, C::DSPLIT * nkt, 1, kBwdUMajor);
   const int dpass = w % C::DSPLIT, w2 = w / C::DSPLIT;
   const int dbase = dpass * C::NDB * 16;  // first dK/dV column owned here
   const int kt = w2 % nkt, zh = w2 / nkt;

@@ -62,7 +62,7 @@ fwd_f32_kernel(FableFwdParams p, int nqt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int c16 = lane & 15, g = lane >> 4;
 
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt, p.gqa);
+  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt, p.gqa, kFwdUMajor);
   const int qti = w % nqt, zh = w / nqt;
   const int h = zh % p.NH, z = zh / p.NH;
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;

@@ -84,7 +84,7 @@ fwd_kernel(FableFwdParams p, int nqt) {
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
 
   // ---- work item -> (sequence z, head h, q tile)
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt, p.gqa);
+  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt, p.gqa, kFwdUMajor);
   const int qti = w % nqt, zh = w / nqt;
   const int h = zh % p.NH, z = zh / p.NH;
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
