@@ -112,8 +112,17 @@ def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", see
             "ms": wall, "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
             "kernel_tflops": flops / (ev * 1e-3) / 1e12, "kernel_ms_median": _median(per),
             "tflops_median": flops / (_median(per) * 1e-3) / 1e12,
-            "roofline": roofline("mfma", flops, ev, profiled_traffic(
-                FWD_C2_KERNEL if (D == 128 and causal) else FWD_C1_KERNEL))}
+            "roofline": roofline("mfma", flops, ev, _fwd_traffic(B, S, H, D, causal))}
+
+
+def _fwd_traffic(B, S, H, D, causal):
+    """Profiled HBM bytes per launch of a forward workload: only the profiled shapes (C2 at
+    S=16384 and C1) have them; other sizes share a kernel symbol but not its bytes."""
+    if (B, S, H, D, causal) == (1, 16384, 32, 128, True):
+        return profiled_traffic(FWD_C2_KERNEL)
+    if (B, S, H, D, causal) == (1, 1024, 8, 64, False):
+        return profiled_traffic(FWD_C1_KERNEL)
+    return None
 
 
 def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0, warm_ms=EXTRA_WARM_MS):
