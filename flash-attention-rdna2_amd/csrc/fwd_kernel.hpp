@@ -286,7 +286,17 @@ fwd_kernel(FableFwdParams p, int nqt) {
     const int kq = kb + 4 * hh;  // key of s[jb][r] = kq + 32*jb + 8*(r/4) + (r%4)
     if constexpr (FEAT) {
 #pragma unroll
-      for (int jb = 0; jb < C::NB; jb++)
+      for (int jb = 0; jb < C::NB; jb++) {
+        // masked tiles: the lane's 16 keys of this 32-key block sit at offsets
+        // 8*(r/4) + r%4 from kq + 32*jb; `vis` has bit o set iff offset o is inside the row's
+        // interval [rlo, rlo + rspan), so each score takes one bit extract and one bitfield
+        // insert (the per-score add, compare and select cost one more instruction each)
+        unsigned vis = 0u;
+        if constexpr (decltype(masked)::value) {
+          const int base = kq + 32 * jb - rlo[i];
+          const int a = min(max(-base, 0), 32), b = min(max(rspan[i] - base, 0), 32);
+          vis = (unsigned)(((1ull << b) - 1ull) & ~((1ull << a) - 1ull));
+        }
 #pragma unroll
         for (int r = 0; r < 16; r++) {
           const int key = kq + jb * 32 + 8 * (r >> 2) + (r & 3);
@@ -298,14 +308,17 @@ fwd_kernel(FableFwdParams p, int nqt) {
             x = s[jb][r] * c_log2;
           }
           if constexpr ((decltype(cap)::value & 2) != 0) x = fmaf(aslope2, (float)(key - qi), x);
-          if constexpr (decltype(masked)::value)
-            x = (unsigned)(key - rlo[i]) < (unsigned)rspan[i] ? x : -INFINITY;
+          if constexpr (decltype(masked)::value) {
+            const unsigned keep = (unsigned)__builtin_amdgcn_sbfe((int)vis, 8 * (r >> 2) + (r & 3), 1);
+            x = __builtin_bit_cast(float, (__builtin_bit_cast(unsigned, x) & keep) | (0xFF800000u & ~keep));
+          }
           s[jb][r] = x;
           // bound how many scores the scheduler transforms at once (the softcap transform's
           // register pressure); plain logits are left to the scheduler
           if constexpr ((decltype(cap)::value & 1) != 0)
             if ((r & 7) == 7) __builtin_amdgcn_sched_barrier(0);
         }
+      }
     } else if constexpr (decltype(masked)::value) {
 #pragma unroll
       for (int jb = 0; jb < C::NB; jb++)
