@@ -30,6 +30,7 @@ BWD_DS_MAX_BYTES, 16 GiB, or the environment variable FABLE_ATTN_BWD_DS_MAX_BYTE
 to the recomputing path when the allocation fails. Both paths give the same gradients to
 rounding.
 """
+import contextlib
 import ctypes
 import os
 
@@ -79,8 +80,19 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr()) if t is not None else None
 
 
+def _on(dev):
+    """The device context of a launch: a no-op when dev is already current (the common case;
+    entering torch.cuda.device costs microseconds per call)."""
+    return contextlib.nullcontext() if dev.index == torch.cuda.current_device() else torch.cuda.device(dev)
+
+
 def _stream(t):
-    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+    """The current stream of t's device as a raw handle (the torch call that returns the handle
+    directly costs a fraction of building a Stream object; the public call is the fallback)."""
+    try:
+        return ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(t.device.index))
+    except AttributeError:
+        return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
 
 
 def _bhs(t):
@@ -90,9 +102,13 @@ def _bhs(t):
 
 def _rows_aligned(t):
     """16-byte aligned rows with a contiguous head_dim: what the kernels' vector loads need."""
-    el = t.element_size()
-    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0 and
-            all((s * el) % 16 == 0 for s in t.stride()[:-1]))
+    st, el = t.stride(), t.element_size()
+    if st[-1] != 1 or t.data_ptr() % 16:
+        return False
+    acc = 0
+    for x in st[:-1]:
+        acc |= x * el
+    return acc % 16 == 0
 
 
 def _check_index(name, t, dev, n=None, at_least=False):
@@ -140,6 +156,8 @@ def _alibi(alibi, H, dev):
 
 
 def _check_bhsd(name, t, dtype, dev):
+    if t.dim() == 4 and t.dtype == dtype and t.is_cuda and t.device == dev and _rows_aligned(t):
+        return  # (the common case, checked in one pass; the messages below name the failure)
     _req(t.is_cuda, f"{name}: GPU tensor required")
     _req(t.dim() == 4, f"{name}: expected [B,H,S,D]")
     _req(t.dtype == dtype, f"{name}: dtype {t.dtype} differs from q ({dtype})")
@@ -179,7 +197,7 @@ def fwd(q, k, v, scale, causal, win_left, win_right, softcap, alibi, dropout_p, 
     p.attn_chunk = int(attn_chunk)
     p.seqused_q = p.seqused_k = None
     p.lse_sb, p.lse_sh = Hq * SQ, SQ
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         _lib.check(_L.fable_attn_fwd(p, _dt(q), _stream(q)), "fable_attn_fwd")
     return out, lse
 
@@ -222,7 +240,7 @@ def fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win
     p.seqused_q = seqused_q.data_ptr() if seqused_q is not None else None
     p.seqused_k = seqused_k.data_ptr() if seqused_k is not None else None
     p.lse_sb, p.lse_sh = 0, q.shape[0]
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         _lib.check(_L.fable_attn_fwd(p, _dt(q), _stream(q)), "fable_attn_fwd (varlen)")
     return (out, lse) if return_lse else out
 
@@ -258,7 +276,7 @@ def bwd(dout, q, k, v, out, lse, scale, causal, win_left, win_right, softcap, al
     p.keep_scale = 1.0 / (1.0 - dropout_p) if dropout_p > 0 else 1.0
     p.lse_sb, p.lse_sh = Hq * SQ, SQ
     ws = _ds_workspace(p, _dt(q), q.device, ds_max_bytes)  # noqa: F841  (alive through the launch)
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         _lib.check(_L.fable_attn_bwd(p, _dt(q), _stream(q)), "fable_attn_bwd")
     return dq, dk, dv
 
@@ -304,7 +322,7 @@ def bwd_varlen(dout, q, k, v, out, lse, cu_q, cu_k, max_sq, max_sk, scale, causa
     p.seqused_k = seqused_k.data_ptr() if seqused_k is not None else None
     p.lse_sb, p.lse_sh = 0, q.shape[0]
     ws = _ds_workspace(p, _dt(q), q.device, ds_max_bytes)  # noqa: F841  (alive through the launch)
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         _lib.check(_L.fable_attn_bwd(p, _dt(q), _stream(q)), "fable_attn_bwd (varlen)")
     return dq, dk, dv
 
@@ -379,7 +397,7 @@ def dec(q, k_cache, v_cache, block_table, cache_seqlens, new_k, new_v, rotary_co
     p.alibi = alibi.data_ptr() if alibi is not None else None
     p.nq, p.rotary_dim = NQ, int(rotary_dim)
     p.rotary_pos = rotary_pos.data_ptr() if rotary_pos is not None else None
-    with torch.cuda.device(q.device):
+    with _on(q.device):
         _lib.check(_L.fable_attn_dec(p, _dt(q), _stream(q), _ptr(new_k), _ptr(new_v)),
                    "fable_attn_dec")
     return out, lse
@@ -404,6 +422,6 @@ def combine(out_partial, lse_partial, out_dtype):
                                             out_partial.stride(2), out_partial.stride(3))
     c.lp_split, c.lp_b, c.lp_h, c.lp_seq = lp.stride(0), lp.stride(1), lp.stride(2), lp.stride(3)
     c.in_dtype, c.out_dtype = _dt(out_partial), _dt(out)
-    with torch.cuda.device(out_partial.device):
+    with _on(out_partial.device):
         _lib.check(_L.fa_combine_launch(c, _stream(out_partial)), "fa_combine_launch")
     return out

@@ -179,6 +179,32 @@ def _bhsd(t):
 
 
 # ----------------------------------------------------------------------------- autograd
+def _forward(spec, pack, q, k, v):
+    """One forward launch of a dense ([B,H,S,D] views, pack None) or packed variable-length
+    batch; returns (out, lse, dropout seed)."""
+    seed = random.getrandbits(63) if spec.dropout_p > 0 else 0
+    args = (spec.scale, bool(spec.causal), spec.wl, spec.wr, spec.softcap, spec.alibi,
+            spec.dropout_p, seed)
+    if pack is None:
+        B, H, S, D = q.shape
+        buf = torch.empty((B, S, H, D), dtype=q.dtype, device=q.device).transpose(1, 2)
+        out, lse = _C.fwd(q, k, v, *args, spec.chunk, buf)
+    else:
+        cu_q, cu_k, mq, mk, su_q, su_k = pack
+        out, lse = _C.fwd_varlen(q, k, v, cu_q, cu_k, mq, mk, *args, spec.chunk, su_q, su_k,
+                                 return_lse=True)
+    return out, lse, seed
+
+
+def _run(spec, pack, q, k, v):
+    """(out, lse) through the autograd node when a gradient can flow, else the launch alone
+    (no graph node, no saved tensors: the inference path stays a few microseconds of host time)."""
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        return _Attention.apply(spec, pack, q, k, v)
+    out, lse, _ = _forward(spec, pack, q, k, v)
+    return out, lse
+
+
 class _Attention(torch.autograd.Function):
     """Forward (with LSE) and backward of one dense or packed variable-length batch, one
     kernel launch sequence each way. `pack` is None for dense [B,H,S,D] views, else the tuple
@@ -187,17 +213,7 @@ class _Attention(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, spec, pack, q, k, v):
-        seed = random.getrandbits(63) if spec.dropout_p > 0 else 0
-        args = (spec.scale, bool(spec.causal), spec.wl, spec.wr, spec.softcap, spec.alibi,
-                spec.dropout_p, seed)
-        if pack is None:
-            B, H, S, D = q.shape
-            buf = torch.empty((B, S, H, D), dtype=q.dtype, device=q.device).transpose(1, 2)
-            out, lse = _C.fwd(q, k, v, *args, spec.chunk, buf)
-        else:
-            cu_q, cu_k, mq, mk, su_q, su_k = pack
-            out, lse = _C.fwd_varlen(q, k, v, cu_q, cu_k, mq, mk, *args, spec.chunk, su_q, su_k,
-                                     return_lse=True)
+        out, lse, seed = _forward(spec, pack, q, k, v)
         # (the scalars only: the spec's own tensors are this node's inputs)
         ctx.spec = dataclasses.replace(spec, q=None, k=None, v=None)
         ctx.pack, ctx.seed = pack, seed
@@ -269,7 +285,7 @@ def _dense(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap, alib
                       descale=(q_descale, k_descale, v_descale),
                       hints=(num_splits, pack_gqa, sm_margin))
     qh, kh, vh = _bhsd(spec.q), _bhsd(spec.k), _bhsd(spec.v)
-    out, lse = _Attention.apply(spec, None, qh, kh, vh)
+    out, lse = _run(spec, None, qh, kh, vh)
     res = out.transpose(1, 2)
     if spec.keep is not None:
         res = res[..., :spec.keep].contiguous()
@@ -375,8 +391,7 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
     pack = (_as_index(cu_seqlens_q, dev), _as_index(cu_seqlens_k, dev), int(max_seqlen_q),
             int(max_seqlen_k), _as_index(seqused_q, dev) if seqused_q is not None else None,
             _as_index(seqused_k, dev) if seqused_k is not None else None)
-    out, lse = _Attention.apply(spec, pack, spec.q.contiguous(), spec.k.contiguous(),
-                                spec.v.contiguous())
+    out, lse = _run(spec, pack, spec.q.contiguous(), spec.k.contiguous(), spec.v.contiguous())
     out = spec.cut(out)
     if not return_attn_probs:
         return out
