@@ -183,20 +183,13 @@ def fwd(q, k, v, scale, causal, win_left, win_right, softcap, alibi, dropout_p, 
         _req(_rows_aligned(out), "out: head_dim must be contiguous with 16-byte aligned rows")
     lse = torch.empty((B, Hq, SQ), dtype=torch.float32, device=q.device)
     al = _alibi(alibi, Hq, q.device)
-    p = FableFwdParams()
-    p.Q, p.K, p.V, p.O, p.LSE = q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr()
-    p.sQ, p.sK, p.sV, p.sO = _bhs(q), _bhs(k), _bhs(v), _bhs(out)
-    p.SQ, p.SK, p.HD, p.NH, p.gqa = SQ, SK, D, Hq, Hq // Hk
-    p.scale, p.softcap = float(scale), float(softcap)
-    p.win_left, p.win_right = int(win_left), int(win_right)
-    p.alibi_slopes = al.data_ptr() if al is not None else None
-    p.causal = 1 if causal else 0
-    p.dropout_p, p.philox_seed = float(dropout_p), int(seed) & ((1 << 64) - 1)
-    p.cu_q = p.cu_k = None
-    p.batch = B
-    p.attn_chunk = int(attn_chunk)
-    p.seqused_q = p.seqused_k = None
-    p.lse_sb, p.lse_sh = Hq * SQ, SQ
+    # (one positional construction: a fraction of the host time of 30 field assignments)
+    p = FableFwdParams(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                       _bhs(q), _bhs(k), _bhs(v), _bhs(out), SQ, SK, D, Hq, Hq // Hk,
+                       float(scale), float(softcap), int(win_left), int(win_right),
+                       al.data_ptr() if al is not None else None, 1 if causal else 0,
+                       float(dropout_p), int(seed) & ((1 << 64) - 1), None, None, B, int(attn_chunk),
+                       None, None, Hq * SQ, SQ)
     with _on(q.device):
         _lib.check(_L.fable_attn_fwd(p, _dt(q), _stream(q)), "fable_attn_fwd")
     return out, lse

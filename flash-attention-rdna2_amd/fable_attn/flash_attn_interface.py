@@ -171,9 +171,8 @@ def _bhsd(t):
     """(B,S,H,D) -> the [B,H,S,D] view the kernels take; a copy only when a row is not 16-byte
     aligned (the kernels move rows in 16-byte accesses)."""
     v = t.transpose(1, 2)
-    el = v.element_size()
-    aligned = (v.stride(-1) == 1 and v.data_ptr() % 16 == 0 and
-               all((s * el) % 16 == 0 for s in v.stride()[:-1]))
+    st, el = v.stride(), v.element_size()
+    aligned = st[-1] == 1 and v.data_ptr() % 16 == 0 and (st[0] * el | st[1] * el | st[2] * el) % 16 == 0
     return v if aligned else t.contiguous().transpose(1, 2)
 
 
