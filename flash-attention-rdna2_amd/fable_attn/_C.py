@@ -83,7 +83,9 @@ def _ptr(t):
 def _on(dev):
     """The device context of a launch: a no-op when dev is already current (the common case;
     entering torch.cuda.device costs microseconds per call)."""
-    return contextlib.nullcontext() if dev.index == torch.cuda.current_device() else torch.cuda.device(dev)
+    if dev.index == torch.cuda.current_device():
+        return contextlib.nullcontext()
+    return torch.cuda.device(dev)
 
 
 def _stream(t):

@@ -172,7 +172,8 @@ def _bhsd(t):
     aligned (the kernels move rows in 16-byte accesses)."""
     v = t.transpose(1, 2)
     st, el = v.stride(), v.element_size()
-    aligned = st[-1] == 1 and v.data_ptr() % 16 == 0 and (st[0] * el | st[1] * el | st[2] * el) % 16 == 0
+    aligned = (st[-1] == 1 and v.data_ptr() % 16 == 0
+               and (st[0] * el | st[1] * el | st[2] * el) % 16 == 0)
     return v if aligned else t.contiguous().transpose(1, 2)
 
 
