@@ -622,29 +622,39 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   // (one accumulation chain: dependent MFMAs of one shape issue back to back, and a second
   // chain would cost 16 VALU adds per product)
   auto rowprod = [&](const T* tile) {
+    V8 a[C::NDS];
+#pragma unroll
+    for (int ds = 0; ds < C::NDS; ds++) a[ds] = *(const V8*)(tile + bofs<C::HD>(l32, 2 * ds + hh));
+    __builtin_amdgcn_sched_barrier(0);
     f32x16 x = f32x16{};
 #pragma unroll
-    for (int ds = 0; ds < C::NDS; ds++) x = Dt<T>::mma32(*(const V8*)(tile + bofs<C::HD>(l32, 2 * ds + hh)), kv[ds], x);
+    for (int ds = 0; ds < C::NDS; ds++) x = Dt<T>::mma32(a[ds], kv[ds], x);
     return x;
   };
   // acc^T += tile^T . B (A operand by transposing reads of the tile; B = P or dS)
   auto tprod = [&](const T* tile, const V8 (&bop)[2]) {
+    V4 part[C::NDB][2][2];
 #pragma unroll
     for (int db = 0; db < C::NDB; db++) {
       const int col = 32 * db + 16 * mh + 4 * (j16 & 3);
 #pragma unroll
-      for (int sq = 0; sq < 2; sq++) {
-        V4 part[2];
+      for (int sq = 0; sq < 2; sq++)
 #pragma unroll
         for (int a = 0; a < 2; a++) {
           const int row = 16 * sq + 8 * a + 4 * hh + (j16 >> 2);
-          part[a] = lds_read_tr<T>(tile + bofs<C::HD>(row, col >> 3) + (col & 7));
+          part[db][sq][a] = lds_read_tr<T>(tile + bofs<C::HD>(row, col >> 3) + (col & 7));
         }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int db = 0; db < C::NDB; db++) {
+#pragma unroll
+      for (int sq = 0; sq < 2; sq++) {
         V8 av;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          av[e] = part[0][e];
-          av[4 + e] = part[1][e];
+          av[e] = part[db][sq][0][e];
+          av[4 + e] = part[db][sq][1][e];
         }
         acc[db] = Dt<T>::mma32(av, bop[sq], acc[db]);
       }
@@ -688,12 +698,12 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   // S-wave step `it` (set S holds tile it, stored an iteration ago): S, P, dV += dO^T . P
   auto s_step = [&](auto set, int it) {
     constexpr int S = decltype(set)::value;
-    gload(set);
     const int st = it & 3, hg = w_hg, qt0 = qstart + w_qi * C::BQ;
     w_next();
     const float slope = (FEAT && p.alibi) ? p.alibi[kvh * p.gqa + hg] : 0.0f;
     const T* qs = lds + st * C::STAGE;
     const f32x16 sv = rowprod(qs);
+    gload(set);  // after the product is issued: the loader's scalar work runs beside it
     const bool edge = FEAT || (CAUSAL && kw + 31 > qt0 + delta) || qt0 + C::BQ > SQ || kw + 32 > SK;
     // probabilities; on an edge tile (one uniform branch, no per-score branches) the scores a
     // query does not see are zeroed
@@ -744,7 +754,6 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   V8 pS[2] = {bitcast<V8>(u32x4{0, 0, 0, 0}), bitcast<V8>(u32x4{0, 0, 0, 0})};
   auto d_step = [&](auto set, int it) {
     constexpr int S = decltype(set)::value;
-    gload(set);
     const int t = it - 1;
     const int hg = w_hg, qt0 = qstart + w_qi * C::BQ;
     const bool act = t >= 0 && t < total && active(qt0);
@@ -752,6 +761,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     const int st = t & 3;
     const T* qs = lds + st * C::STAGE;
     tprod(lds + ((t - 1) & 3) * C::STAGE, pS);  // dK^T += Q^T . dS (tile t-1)
+    gload(set);
     const f32x16 dpv = rowprod(qs + C::TT);
 #pragma unroll
     for (int rq = 0; rq < 4; rq++) {
