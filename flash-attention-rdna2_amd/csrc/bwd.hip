@@ -620,7 +620,10 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   // this wave's product of a tile with its B rows: S (S-wave, with Q) or dP (dP-wave, with
   // dO); x[r] is query qt0 + 8*(r/4) + 4*hh + (r%4), key `key`
   // (one accumulation chain: dependent MFMAs of one shape issue back to back, and a second
-  // chain would cost 16 VALU adds per product)
+  // chain would cost 16 VALU adds per product). Both products read all their LDS operands
+  // first: the scheduler otherwise put each read right before its product, through one
+  // register set, so every product waited out a read; with the reads first the kernel takes
+  // 6 fewer registers and runs as fast (the second wave of the SIMD hid those waits).
   auto rowprod = [&](const T* tile) {
     V8 a[C::NDS];
 #pragma unroll
@@ -698,12 +701,12 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   // S-wave step `it` (set S holds tile it, stored an iteration ago): S, P, dV += dO^T . P
   auto s_step = [&](auto set, int it) {
     constexpr int S = decltype(set)::value;
+    gload(set);
     const int st = it & 3, hg = w_hg, qt0 = qstart + w_qi * C::BQ;
     w_next();
     const float slope = (FEAT && p.alibi) ? p.alibi[kvh * p.gqa + hg] : 0.0f;
     const T* qs = lds + st * C::STAGE;
     const f32x16 sv = rowprod(qs);
-    gload(set);  // after the product is issued: the loader's scalar work runs beside it
     const bool edge = FEAT || (CAUSAL && kw + 31 > qt0 + delta) || qt0 + C::BQ > SQ || kw + 32 > SK;
     // probabilities; on an edge tile (one uniform branch, no per-score branches) the scores a
     // query does not see are zeroed
@@ -752,16 +755,29 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   // their VALU work at once. The Q tile of t-1 is still in its stage: the stage is refilled
   // with tile t+3 at the end of step it+1.
   V8 pS[2] = {bitcast<V8>(u32x4{0, 0, 0, 0}), bitcast<V8>(u32x4{0, 0, 0, 0})};
+  // dS workspace cursor (wave-uniform): the tile of step t, advanced like the tile order (the
+  // next q tile of the head, or the first of the next head); rebuilding the address every step
+  // from 64-bit products cost ~25 scalar instructions
+  T* ds_cur = nullptr;
+  long long ds_wrap = 0;
+  if constexpr (DSW) {
+    ds_cur = ds_head_tiles<T>(p, b, kvh * p.gqa, ds_T) + (long long)(ds_row + (qstart >> 5)) * 1024;
+    ds_wrap = ((long long)ds_T - (ntq - 1)) * 1024;
+  }
   auto d_step = [&](auto set, int it) {
     constexpr int S = decltype(set)::value;
+    gload(set);
     const int t = it - 1;
-    const int hg = w_hg, qt0 = qstart + w_qi * C::BQ;
+    const int qt0 = qstart + w_qi * C::BQ;
     const bool act = t >= 0 && t < total && active(qt0);
-    if (t >= 0) w_next();
+    T* const ds_tile = ds_cur;
+    if (t >= 0) {
+      if constexpr (DSW) ds_cur += w_qi + 1 == ntq ? ds_wrap : 1024;
+      w_next();
+    }
     const int st = t & 3;
     const T* qs = lds + st * C::STAGE;
     tprod(lds + ((t - 1) & 3) * C::STAGE, pS);  // dK^T += Q^T . dS (tile t-1)
-    gload(set);
     const f32x16 dpv = rowprod(qs + C::TT);
 #pragma unroll
     for (int rq = 0; rq < 4; rq++) {
@@ -782,8 +798,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     }
     if constexpr (DSW) {  // dS tile (32 queries x this pair's 32 keys) to the workspace
       if (act) {
-        T* dst = ds_head_tiles<T>(p, b, kvh * p.gqa + hg, ds_T) + (long long)(ds_row + (qt0 >> 5)) * 1024 +
-                 16 * l32 + 8 * hh;
+        T* dst = ds_tile + 16 * l32 + 8 * hh;
         // streaming stores: the tiles are read once, by the dQ kernel, and must not push the
         // Q/dO tiles this kernel re-reads out of L2
         __builtin_nontemporal_store(pS[0], (V8*)dst);
