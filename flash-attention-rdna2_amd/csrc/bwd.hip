@@ -462,7 +462,7 @@ __device__ __forceinline__ void for_sets(std::integer_sequence<int, I...>, F&& f
 // half the registers of a wave that owns both accumulators, so two waves fit per SIMD and
 // one's VALU work overlaps the other's MFMAs. The Q/dO tiles sit in a 4-stage LDS ring (the
 // S-wave reads tile t, the dP-wave tile t-1, tile t+1 is stored) and tiles t+2 .. t+NSET are in
-// flight in registers; one barrier per tile.
+// flight in the S-waves' registers; one barrier per tile.
 template <int HD_, int NP_, int NSET_>
 struct BwdKVPCfg {
   static constexpr bool PAIR = true;
@@ -478,9 +478,13 @@ struct BwdKVPCfg {
   static constexpr int TT = BQ * HD;       // elements per Q (or dO) tile
   static constexpr int STAGE = 2 * TT;
   static constexpr int CH = 2 * BQ * DCH;  // chunks per stage (Q and dO)
-  static constexpr int PER = CH / NT;
-  static constexpr int QJ = BQ * DCH / NT; // Q chunk slots per thread (the rest are dO)
-  static_assert(CH % NT == 0 && (BQ * DCH) % NT == 0, "loader split");
+  // loader threads: the S-waves. The dP-waves load nothing and only store dS tiles: loads and
+  // stores share one in-order completion counter, so a dP-wave that also loaded waited on
+  // its earlier dS stores whenever it waited for a tile (C3 +3% with the S-waves loading)
+  static constexpr int LT = NP * 64;
+  static constexpr int PER = CH / LT;
+  static constexpr int QJ = BQ * DCH / LT; // Q chunk slots per thread (the rest are dO)
+  static_assert(CH % LT == 0 && (BQ * DCH) % LT == 0, "loader split");
 };
 
 template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false, bool DSW = false>
@@ -547,7 +551,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   int voff[C::PER];
 #pragma unroll
   for (int j = 0; j < C::PER; j++) {
-    const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
+    const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::LT, r = ci / C::DCH, c = ci % C::DCH;
     voff[j] = 8 * c < HDr ? r * (int)((j < C::QJ ? p.qs.s : p.dos.s) * 2) + 16 * c : kBufZero;
   }
   // NSET register sets: tile it+NSET is loaded while tile it+1 (loaded NSET-1 iterations
@@ -606,7 +610,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     T* base = lds + stage * C::STAGE;
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
-      const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::NT, r = ci / C::DCH, c = ci % C::DCH;
+      const int ci = tid + (j < C::QJ ? j : j - C::QJ) * C::LT, r = ci / C::DCH, c = ci % C::DCH;
       *(u32x4*)(base + (j < C::QJ ? 0 : C::TT) + bofs<C::HD>(r, c)) = ld[S][j];
     }
     if (tid < 2 * C::BQ) {
@@ -683,7 +687,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     for (int i = tid; i < (int)(sizeof(pdx) / 16); i += C::NT) (&pdx[0][0][0][0])[i] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   __syncthreads();  // zeroed before the first tile is stored
-  if (total > 0) {
+  if (total > 0 && !dpw) {
     gload(std::integral_constant<int, 0>{});
     lstore(std::integral_constant<int, 0>{}, 0);
     gload(std::integral_constant<int, 1>{});
@@ -765,8 +769,6 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
     ds_wrap = ((long long)ds_T - (ntq - 1)) * 1024;
   }
   auto d_step = [&](auto set, int it) {
-    constexpr int S = decltype(set)::value;
-    gload(set);
     const int t = it - 1;
     const int qt0 = qstart + w_qi * C::BQ;
     const bool act = t >= 0 && t < total && active(qt0);
@@ -805,7 +807,6 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
         __builtin_nontemporal_store(pS[1], (V8*)(dst + 512));
       }
     }
-    lstore(std::integral_constant<int, (S + 1) % NSET>{}, (it + 1) & 3);  // tile it+1
     __syncthreads();
   };
   // steps 0 .. total (the dP-wave's last tile is total-1), rounded up to whole register-set
