@@ -51,6 +51,10 @@ CASES = [
     ("d256 window (32,32) alibi SQ<SK", 1, 200, 230, 256, 8, 2, False, 32, 32, 0.0, True, 0),
     ("d256 window (40,0) SQ>SK empty rows", 1, 200, 120, 256, 8, 4, True, 40, 0, 0.0, False, 0),
     ("d256 window (300,0) softcap B2", 2, 700, 700, 256, 4, 2, True, 300, 0, 30.0, False, 0),
+    # the one-wave loop's ordered PV/transform steps with both transforms, and on the 64-key
+    # softcap shape (two 32-key blocks per tile)
+    ("d256 causal softcap alibi", 1, 230, 230, 256, 8, 2, True, -1, -1, 30.0, True, 0),
+    ("d256 causal softcap (64-key tiles)", 1, 330, 330, 256, 8, 2, True, -1, -1, 30.0, False, 0),
     ("d128 wide window + alibi", 1, 2300, 2300, 128, 4, 1, True, 2048, 0, 0.0, True, 0),
     ("d128 narrow window + softcap", 1, 300, 300, 128, 8, 2, True, 100, 0, 20.0, False, 0),
     ("d64 narrow window + alibi", 1, 300, 300, 64, 8, 1, False, 40, 40, 0.0, True, 0),
