@@ -196,6 +196,11 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, lon
 __device__ __forceinline__ u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, int voff) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 0);
 }
+// the same with the non-temporal cache policy (cache-policy bit 1 is `nt` on gfx950), for data
+// read once
+__device__ __forceinline__ u32x4 buf_load16_nt(__amdgpu_buffer_rsrc_t r, int voff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, 0, 2);
+}
 
 // blockIdx.x -> work index so that consecutive work items land on the same XCD (one L2).
 // Workgroups are dispatched round-robin over the 8 XCDs of an MI355X.

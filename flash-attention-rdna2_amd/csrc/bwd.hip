@@ -954,7 +954,8 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
   const int nkb = (p.SK + 31) >> 5;
   const int* tbl = (const int*)p.ds_ws;
   const int ds_T = tbl[nkb];
-  const T* dsw = ds_head_tiles<T>(p, b, h, ds_T) + 16 * l32 + 8 * hh;
+  const T* dsb = ds_head_tiles<T>(p, b, h, ds_T);
+  const int dlane = (16 * l32 + 8 * hh) * (int)sizeof(T);
   const int qbw = qw >> 5;
   constexpr int NS = C::NS;
   V8 dsr[NS][2 * C::NKB];  // [register set][key block jb, query half sh] chunks of one K tile
@@ -967,10 +968,13 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
     for (int jb = 0; jb < C::NKB; jb++) {
       const int kb = d_kb32 + jb;
       dact[S][jb] = t < ntiles && written(kb);
+      // a tile that is not used (past the last one, or not written for this wave's rows on
+      // the diagonal) loads through an empty descriptor: zeros, and no memory traffic (its
+      // clamped reads had been ~14% of the dS bytes)
       const int idx = min(max(d_row + qbw, 0), ds_T - 1);
-      const T* src = dsw + (long long)idx * 1024;
-      dsr[S][2 * jb] = __builtin_nontemporal_load((const V8*)src);
-      dsr[S][2 * jb + 1] = __builtin_nontemporal_load((const V8*)(src + 512));
+      const auto rs = buf_rsrc(dsb + (long long)idx * 1024, dact[S][jb] ? 2048 : 0);
+      dsr[S][2 * jb] = bitcast<V8>(buf_load16_nt(rs, dlane));
+      dsr[S][2 * jb + 1] = bitcast<V8>(buf_load16_nt(rs, dlane + 1024));
       if (kb + 1 < nkb) {  // the next key block's row (past the last one: stay)
         int a0, a1, n0, n1;
         ds_span(p, kb, a0, a1);
