@@ -204,15 +204,25 @@ fwd_kernel(FableFwdParams p, int nqt) {
     }
   }
   u32x4 ldk[C::KJ], ldv[C::KJ];
-  auto gload_k = [&](int kb) {
-    const auto r = buf_rsrc(Kg + (long long)kb * p.sK.s, (long long)(kvalid - kb) * p.sK.s * 2);
+  // K and V tiles are loaded in key order, kstart, kstart+BC, ... (each through its own
+  // cursor): the descriptor advances by additions instead of 64-bit products of the tile's key
+  const long long k_step = (long long)C::BC * p.sK.s, v_step = (long long)C::BC * p.sV.s;
+  const T* k_cur = Kg + (long long)kstart * p.sK.s;
+  const T* v_cur = Vg + (long long)kstart * p.sV.s;
+  long long k_left = (long long)(kvalid - kstart) * p.sK.s * 2, v_left = (long long)(kvalid - kstart) * p.sV.s * 2;
+  auto gload_k = [&]() {
+    const auto r = buf_rsrc(k_cur, k_left);
 #pragma unroll
     for (int j = 0; j < C::KJ; j++) ldk[j] = buf_load16(r, koff[j]);
+    k_cur += k_step;
+    k_left -= 2 * k_step;
   };
-  auto gload_v = [&](int kb) {
-    const auto r = buf_rsrc(Vg + (long long)kb * p.sV.s, (long long)(kvalid - kb) * p.sV.s * 2);
+  auto gload_v = [&]() {
+    const auto r = buf_rsrc(v_cur, v_left);
 #pragma unroll
     for (int j = 0; j < C::KJ; j++) ldv[j] = buf_load16(r, voff[j]);
+    v_cur += v_step;
+    v_left -= 2 * v_step;
   };
   auto lstore_k = [&](int st) {
     T* b = kl + st * C::KTILE;
@@ -445,12 +455,12 @@ fwd_kernel(FableFwdParams p, int nqt) {
   if (ntiles > 0) {
 #pragma unroll
     for (int j = 0; j < BP; j++) {
-      gload_k(kstart + j * C::BC);
-      gload_v(kstart + j * C::BC);
+      gload_k();  // tile j
+      gload_v();  // tile j
       lstore_k(j);
       lstore_v(j);
     }
-    gload_k(kstart + BP * C::BC);
+    gload_k();  // tile BP
     lstore_k(BP);
   }
   __syncthreads();
@@ -500,8 +510,8 @@ fwd_kernel(FableFwdParams p, int nqt) {
   for (; t + 1 < nint; t++) {
     rescale();
     const int kb1 = kstart + (t + 1) * C::BC;
-    gload_k(kb1 + BP * C::BC);
-    gload_v(kb1 + (BP - 1) * C::BC);
+    gload_k();  // tile t+1+BP
+    gload_v();  // tile t+BP
     f32x16 s[QB][C::NB];
     // raised wave priority over the S product: +1-3% at D=128; 1.5-6% slower at D=64 and 4-6%
     // slower at D=256 (one wave per SIMD there: nothing to take priority over), so not there
@@ -535,8 +545,8 @@ fwd_kernel(FableFwdParams p, int nqt) {
       for (; t + 1 < ntiles; t++) {
         rescale();
         const int kb1 = kstart + (t + 1) * C::BC;
-        gload_k(kb1 + BP * C::BC);
-        gload_v(kb1 + (BP - 1) * C::BC);
+        gload_k();  // tile t+1+BP
+        gload_v();  // tile t+BP
         f32x16 s[QB][C::NB];
         qk((t + 1) & (NST - 1), s);
         if constexpr (QB == 1 && C::NDB * C::NG == 16 * C::NB) {
@@ -608,8 +618,8 @@ fwd_kernel(FableFwdParams p, int nqt) {
   for (; t < ntiles; t++) {
     rescale();
     const int kb1 = kstart + (t + 1) * C::BC;
-    gload_k(kb1 + BP * C::BC);
-    gload_v(kb1 + (BP - 1) * C::BC);
+    gload_k();  // tile t+1+BP
+    gload_v();  // tile t+BP
     const bool a_next = t + 1 < ntiles && active(t + 1);
     f32x16 s[QB][C::NB];
     if (a_next) qk((t + 1) & (NST - 1), s);
