@@ -7,10 +7,12 @@
 //  * one workgroup (4 waves) per (kv head, 16-head group, sequence*new token, split); the q
 //    heads sharing the kv head are packed into the N=16 dimension of v_mfma_f32_16x16x32, so
 //    K and V are read from HBM once per kv head whatever the GQA ratio;
-//  * S^T = K . Q^T: each lane loads 16 bytes of one key row straight from the paged cache into
-//    the A operand (no LDS); the 16x16 result leaves every lane with one head and four keys;
-//  * P^T is the B operand of O^T = V^T . P^T without leaving registers; V is staged per wave in
-//    LDS (row-major, chunk-swizzled) and read back transposed with ds_read_b64_tr_b16;
+//  * K and V rows are read from the paged cache in whole rows (consecutive lanes cover one
+//    row) and staged per wave in LDS; S^T = K . Q^T reads its A operand (16 bytes of one key
+//    row per lane) back from the K slice, and the 16x16 result leaves every lane with one head
+//    and four keys;
+//  * P^T is the B operand of O^T = V^T . P^T without leaving registers; V is read back from
+//    its slice transposed with ds_read_b64_tr_b16;
 //  * each wave streams its own 32-key chunks (no barriers in the loop); the four waves merge
 //    in LDS at the end and write one (max, sum, acc[HD]) partial per head and split;
 //  * the combine kernel merges the splits (natural-log LSE optional);
@@ -62,8 +64,9 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   constexpr int RCH = HD / 8;   // 16-byte chunks per key row
   static_assert(RCH >= 8, "swizzle needs >= 8 chunks per row");
   // one LDS region, reused: q staging (fp32) before the loop, per-wave V chunks in the loop,
-  // the four waves' accumulators after it
+  // the four waves' accumulators after it; per-wave K chunks in a region of their own
   __shared__ __attribute__((aligned(16))) char vraw[kDecWaves * kDecChunk * HD * 2];
+  __shared__ __attribute__((aligned(16))) char kraw[kDecWaves * kDecChunk * HD * 2];
   __shared__ float red_m[kDecWaves][16], red_l[kDecWaves][16];
   static_assert(16 * HD * 4 <= sizeof(vraw), "q staging fits the V region");
   float (*qsh)[HD] = (float (*)[HD])vraw;
@@ -134,18 +137,16 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   const int* bt = p.block_table + (long long)b * p.max_blocks;
   const int pmask = p.page - 1;
   T* vb = (T*)vraw + wave * kDecChunk * HD;
+  T* kbuf = (T*)kraw + wave * kDecChunk * HD;
 
   // Keys of a chunk are clamped into [start, end-1] (masked in the softmax), so every load is
   // unconditional. Block-table entries are fetched ahead of the row loads that use them, so the
   // K/V row loads of a chunk issue back to back instead of behind their table lookups.
-  constexpr int NVI = kDecChunk * RCH / 64;  // V row loads per lane per chunk
+  constexpr int NVI = kDecChunk * RCH / 64;  // K (and V) row loads per lane per chunk
   const int last = rg.end - 1;
-  auto kkey = [&](int kc0, int kb) { return min(kc0 + 16 * kb + lh, last); };
   auto vkey = [&](int kc0, int i) { return min(kc0 + (64 * i + lane) / RCH, last); };
-  int kblk[2], vblk[NVI];
+  int vblk[NVI];
   auto table = [&](int kc0) {
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++) kblk[kb] = bt[kkey(kc0, kb) >> page_shift];
 #pragma unroll
     for (int i = 0; i < NVI; i++) vblk[i] = bt[vkey(kc0, i) >> page_shift];
   };
@@ -154,48 +155,46 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   };
   // 16-byte chunks in the zero columns load the row's first chunk and are replaced by zeros
   const bool padded = HDr < HD;
-  bool kok[NDS];
-#pragma unroll
-  for (int ds = 0; ds < NDS; ds++) kok[ds] = 32 * ds + 8 * lg < HDr;
   bool vok[NVI];
 #pragma unroll
   for (int i = 0; i < NVI; i++) vok[i] = 8 * ((64 * i + lane) % RCH) < HDr;
-  // K/V rows of the chunk at kc0: K as the A operand (key kc0 + 16*kb + lh, head-dim
-  // 32*ds + 8*lg); V load i covers row (64i + lane) / RCH, 16-byte chunk (64i + lane) % RCH
+  // K/V rows of the chunk at kc0: load i covers row (64i + lane) / RCH, 16-byte chunk
+  // (64i + lane) % RCH of both caches, so consecutive lanes read whole rows. Loading K straight
+  // into the MFMA A layout instead (16 keys x 64 bytes per load) read the cache ~12% slower.
   // The cache rows are read once per step: non-temporal loads keep them from displacing the
   // block table and q in the caches (C4: 368.6 -> 360.3 us for the partial kernel).
-  auto load = [&](int kc0, u32x4 (&kr)[2][NDS], u32x4 (&vr)[NVI]) {
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++) {
-      const long long base = row_off(kblk[kb], kkey(kc0, kb));
-#pragma unroll
-      for (int ds = 0; ds < NDS; ds++)
-        kr[kb][ds] = __builtin_nontemporal_load((const u32x4*)(Kc + base + (kok[ds] ? 32 * ds + 8 * lg : 0)));
-    }
+  auto load = [&](int kc0, u32x4 (&kr)[NVI], u32x4 (&vr)[NVI]) {
 #pragma unroll
     for (int i = 0; i < NVI; i++) {
       const int ch = (64 * i + lane) % RCH;
-      vr[i] = __builtin_nontemporal_load((const u32x4*)(Vc + row_off(vblk[i], vkey(kc0, i)) + (vok[i] ? 8 * ch : 0)));
+      const long long off = row_off(vblk[i], vkey(kc0, i)) + (vok[i] ? 8 * ch : 0);
+      kr[i] = __builtin_nontemporal_load((const u32x4*)(Kc + off));
+      vr[i] = __builtin_nontemporal_load((const u32x4*)(Vc + off));
     }
   };
   // zero columns of a padded head dim, put in where the rows are used (which waits for the
   // loads anyway; a select right after the loads would make the compiler wait there)
-  auto zero_pad = [&](u32x4 (&kr)[2][NDS], u32x4 (&vr)[NVI]) {
+  auto zero_pad = [&](u32x4 (&kr)[NVI], u32x4 (&vr)[NVI]) {
     if (padded) {
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int ds = 0; ds < NDS; ds++) kr[kb][ds] = kok[ds] ? kr[kb][ds] : u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int i = 0; i < NVI; i++) vr[i] = vok[i] ? vr[i] : u32x4{0, 0, 0, 0};
+      for (int i = 0; i < NVI; i++) {
+        kr[i] = vok[i] ? kr[i] : u32x4{0, 0, 0, 0};
+        vr[i] = vok[i] ? vr[i] : u32x4{0, 0, 0, 0};
+      }
     }
   };
+  // K slice: row r holds logical 16-byte chunk c at physical chunk c ^ kswz(r). The rows of
+  // one 256-byte bank line share a pattern and consecutive lines differ, so the 16 lanes of an
+  // A-operand read (16 rows, one chunk) and of a row write hit 16 different bank groups.
+  constexpr int kRowsPerLine = HD >= 128 ? 1 : 128 / HD;
+  constexpr int kSwzMask = (RCH < 16 ? RCH : 16) - 1;
+  auto kswz = [](int r) { return (r / kRowsPerLine) & kSwzMask; };
   // Software pipeline: the rows of the next chunk are in flight while this one is computed;
   // table entries run two chunks ahead. Past the end keys clamp to the last one, so the
   // trailing prefetch reads a valid row.
   constexpr int kStep = kDecChunk * kDecWaves;
   const int kfirst = rg.start + kDecChunk * wave;
-  u32x4 kreg[2][NDS], vreg[NVI];
+  u32x4 kreg[NVI], vreg[NVI];
   if (kfirst < rg.end) {
     table(kfirst);
     load(kfirst, kreg, vreg);
@@ -206,22 +205,35 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   // compute of this one, leaving latency hiding to the other waves.
   constexpr bool kPipe = HD <= 128;
   for (int kc0 = kfirst; kc0 < rg.end; kc0 += kStep) {
-    u32x4 knxt[2][NDS], vnxt[NVI];
+    u32x4 knxt[NVI], vnxt[NVI];
     if constexpr (kPipe) {
       load(kc0 + kStep, knxt, vnxt);
       table(kc0 + 2 * kStep);
     }
     zero_pad(kreg, vreg);
-    // S^T = K . Q^T
+    // K -> this wave's LDS slice; the slice is the wave's own, and LDS operations of one wave
+    // complete in order, so no barrier orders these writes against the reads below or against
+    // the previous chunk's reads
+#pragma unroll
+    for (int i = 0; i < NVI; i++) {
+      const int row = (64 * i + lane) / RCH, ch = (64 * i + lane) % RCH;
+      *(u32x4*)(kbuf + row * HD + 8 * (ch ^ kswz(row))) = kreg[i];
+    }
+    // S^T = K . Q^T, A operand: lane (lg, lh) of block kb reads key row 16*kb + lh, head-dim
+    // chunk 4*ds + lg
     f32x4 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
+      const int row = 16 * kb + lh;
+      V8 ka[NDS];
+#pragma unroll
+      for (int ds = 0; ds < NDS; ds++) ka[ds] = bitcast<V8>(*(const u32x4*)(kbuf + row * HD + 8 * ((4 * ds + lg) ^ kswz(row))));
       s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ds = 0; ds < NDS; ds++) s[kb] = Dt<T>::mma16(bitcast<V8>(kreg[kb][ds]), qb[ds], s[kb]);
+      for (int ds = 0; ds < NDS; ds++) s[kb] = Dt<T>::mma16(ka[ds], qb[ds], s[kb]);
       if (qsplit) {
 #pragma unroll
-        for (int ds = 0; ds < NDS; ds++) s[kb] = Dt<T>::mma16(bitcast<V8>(kreg[kb][ds]), ql[ds], s[kb]);
+        for (int ds = 0; ds < NDS; ds++) s[kb] = Dt<T>::mma16(ka[ds], ql[ds], s[kb]);
       }
     }
     // logits (log2 domain) and masking: s[kb][r] is key kc0 + 16*kb + 4*lg + r, head lh
@@ -293,11 +305,10 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
     }
     if constexpr (kPipe) {
 #pragma unroll
-      for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-        for (int ds = 0; ds < NDS; ds++) kreg[kb][ds] = knxt[kb][ds];
-#pragma unroll
-      for (int i = 0; i < NVI; i++) vreg[i] = vnxt[i];
+      for (int i = 0; i < NVI; i++) {
+        kreg[i] = knxt[i];
+        vreg[i] = vnxt[i];
+      }
     } else {
       load(kc0 + kStep, kreg, vreg);
       table(kc0 + 2 * kStep);
