@@ -56,7 +56,12 @@ __device__ __forceinline__ DecRange dec_range(const FableDecParams& p, int b, in
   return r;
 }
 
-template <typename T, int HD, bool FEAT>
+// SPT (page >= 16): the block-table entries of a chunk are fetched by scalar loads. A chunk of
+// 32 keys touches at most three pages then, and each lane selects its row's entry from the
+// three. Per-lane table loads share the in-order vector-memory counter with the row loads, so
+// a wave waiting for its next entries also waited for the rows issued before them (the chunk
+// in flight): C4 read ~4% slower that way. Smaller pages (a dense cache of < 16 rows) keep them.
+template <typename T, int HD, bool FEAT, bool SPT>
 __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int page_shift, int ngrp, int append) {
   using V8 = typename Dt<T>::V8;
   constexpr int NDS = HD / 32;  // S^T contraction steps
@@ -71,7 +76,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   static_assert(16 * HD * 4 <= sizeof(vraw), "q staging fits the V region");
   float (*qsh)[HD] = (float (*)[HD])vraw;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lg = lane >> 4, lh = lane & 15;  // lane group (0..3), lane in group
   // grid x = (kv head, head group) fastest: the workgroups reading the interleaved heads of the
   // same cache pages are dispatched together
@@ -145,10 +150,26 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   constexpr int NVI = kDecChunk * RCH / 64;  // K (and V) row loads per lane per chunk
   const int last = rg.end - 1;
   auto vkey = [&](int kc0, int i) { return min(kc0 + (64 * i + lane) / RCH, last); };
-  int vblk[NVI];
+  int vblk[SPT ? 1 : NVI], sblk[3];
   auto table = [&](int kc0) {
+    if constexpr (SPT) {
+      const int b0 = kc0 >> page_shift, bl = last >> page_shift;  // wave-uniform
 #pragma unroll
-    for (int i = 0; i < NVI; i++) vblk[i] = bt[vkey(kc0, i) >> page_shift];
+      for (int j = 0; j < 3; j++) sblk[j] = bt[min(b0 + j, bl)];
+    } else {
+#pragma unroll
+      for (int i = 0; i < NVI; i++) vblk[i] = bt[vkey(kc0, i) >> page_shift];
+    }
+  };
+  // entry of load i's row: page (key >> page_shift) - (kc0 >> page_shift) of the chunk's three
+  // (a key clamped to `last` lies in the chunk's last page, whose index the table clamped too)
+  auto blk_of = [&](int kc0, int i) {
+    if constexpr (SPT) {
+      const int j = (vkey(kc0, i) >> page_shift) - (kc0 >> page_shift);
+      return j <= 0 ? sblk[0] : (j == 1 ? sblk[1] : sblk[2]);
+    } else {
+      return vblk[i];
+    }
   };
   auto row_off = [&](int blk, int key) -> long long {
     return (((long long)blk * p.page + (key & pmask)) * NKV + kvh) * HDr;
@@ -167,7 +188,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
 #pragma unroll
     for (int i = 0; i < NVI; i++) {
       const int ch = (64 * i + lane) % RCH;
-      const long long off = row_off(vblk[i], vkey(kc0, i)) + (vok[i] ? 8 * ch : 0);
+      const long long off = row_off(blk_of(kc0, i), vkey(kc0, i)) + (vok[i] ? 8 * ch : 0);
       kr[i] = __builtin_nontemporal_load((const u32x4*)(Kc + off));
       vr[i] = __builtin_nontemporal_load((const u32x4*)(Vc + off));
     }
@@ -594,10 +615,15 @@ static int launch_dec(const FableDecParams& p, hipStream_t st, const void* nk, c
     else
       hipLaunchKernelGGL((dec_partial_f32_kernel<HD, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
   } else {
-    if (feat)
-      hipLaunchKernelGGL((dec_partial_kernel<T, HD, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+    const bool spt = p.page >= 16;
+    if (feat && spt)
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, true, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+    else if (feat)
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, true, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+    else if (spt)
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, false, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
     else
-      hipLaunchKernelGGL((dec_partial_kernel<T, HD, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, false, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
   }
   if (int rc = launch_status("fable_attn_dec (partial)")) return rc;
   hipLaunchKernelGGL((dec_combine_kernel<T, HD>), dim3(p.batch * p.nq, p.NH), dim3(HD), 0, st, p);

@@ -42,6 +42,10 @@ CASES = [
     ("GQA32 two head groups", 128, 64, 32, [700, 300], -1, 0, False, 0, 1, 0.0, False, 32),
     ("batch4 page256 append", 128, 32, 4, [4000, 255, 256, 1], -1, 1, True, 0, 1, 0.0, False, 256),
     ("empty context", 128, 32, 4, [0, 50], -1, 0, False, 0, 1, 0.0, False, 16),
+    # pages under 16 rows (the per-lane block-table path)
+    ("page8 window GQA2 batch2", 128, 16, 2, [300, 45], 70, 0, False, 0, 1, 0.0, False, 8),
+    ("page4 leftpad HD64", 64, 8, 4, [200], -1, 0, False, 13, 1, 0.0, False, 4),
+    ("page1 append+rotary nq2", 128, 8, 4, [40, 3], -1, 1, True, 0, 2, 0.0, False, 1),
 ]
 
 
