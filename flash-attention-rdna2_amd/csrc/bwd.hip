@@ -875,7 +875,7 @@ __global__ __launch_bounds__(256) void bwd_dsum_kernel(FableBwdParams p, int rbl
 template <int HD_, int NW_, int WPE_, int NS_, int BC_ = 64>
 struct BwdDsQCfg {
   static constexpr int HD = HD_, NW = NW_, WPE = WPE_;
-  static constexpr int NS = NS_;       // register sets: K and dS loaded NS-1 tiles ahead
+  static constexpr int NS = NS_;       // dS register sets: dS loaded NS-1 tiles ahead (K one)
   static constexpr int NT = NW * 64;
   static constexpr int BQ = NW * 32;   // queries per workgroup (32 per wave)
   static constexpr int BC = BC_;       // keys per K tile
@@ -899,8 +899,9 @@ __device__ __forceinline__ int dsl_ofs(int r, int n) {
 }
 
 // dQ^T = K^T . dS^T over the dS tiles the pair kernel wrote for this wave's 32 queries. K tiles
-// are double-buffered through LDS and read transposed (A operand). K and dS tiles are loaded
-// NS-1 K tiles ahead (16-byte loads into NS rotating register sets); the dS chunks are staged in
+// are double-buffered through LDS and read transposed (A operand); each is loaded into
+// registers one step ahead and stored to LDS at the end of that step. dS tiles are loaded NS-1
+// K tiles ahead (16-byte loads into NS rotating register sets); the dS chunks are staged in
 // a per-wave LDS block with keys as rows and read back transposed, so each lane gets 8 keys of
 // one query slot (B operand), in the contraction order of the K^T reads. Column n of the product
 // is query slot n, i.e. query ds_slot_query(n). A (key block, query block) tile is read exactly
@@ -954,14 +955,21 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
   const int nkb = (p.SK + 31) >> 5;
   const int* tbl = (const int*)p.ds_ws;
   const int ds_T = tbl[nkb];
-  const T* dsb = ds_head_tiles<T>(p, b, h, ds_T);
   const int dlane = (16 * l32 + 8 * hh) * (int)sizeof(T);
-  const int qbw = qw >> 5;
   constexpr int NS = C::NS;
   V8 dsr[NS][2 * C::NKB];  // [register set][key block jb, query half sh] chunks of one K tile
   bool dact[NS][C::NKB];
   int d_kb32 = kstart >> 5;
-  int d_row = tbl[min(d_kb32, nkb - 1)];
+  // tile (key block d_kb32, this wave's query block): a wave-uniform cursor that advances by
+  // the next row's offset, qb1(kb) - qb0(kb + 1) tiles, from the span of the current key block
+  // (kept) and of the next. It points outside the head's tiles where the tile was not written;
+  // such a tile is never read (below).
+  const T* ds_cur = ds_head_tiles<T>(p, b, h, ds_T) + (long long)(tbl[min(d_kb32, nkb - 1)] + (qw >> 5)) * 1024;
+  int sp1;  // qb1 of key block d_kb32
+  {
+    int sp0;
+    ds_span_k<CAUSAL, FEAT>(p, min(d_kb32, nkb - 1), sp0, sp1);
+  }
   auto dsload = [&](auto set, int t) {
     constexpr int S = decltype(set)::value;
 #pragma unroll
@@ -970,16 +978,15 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
       dact[S][jb] = t < ntiles && written(kb);
       // a tile that is not used (past the last one, or not written for this wave's rows on
       // the diagonal) loads through an empty descriptor: zeros, and no memory traffic (its
-      // clamped reads had been ~14% of the dS bytes)
-      const int idx = min(max(d_row + qbw, 0), ds_T - 1);
-      const auto rs = buf_rsrc(dsb + (long long)idx * 1024, dact[S][jb] ? 2048 : 0);
+      // clamped reads had been ~14% of the dS bytes); its address is never dereferenced
+      const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(ds_cur), (short)0, dact[S][jb] ? 2048 : 0, 0x00020000);
       dsr[S][2 * jb] = bitcast<V8>(buf_load16_nt(rs, dlane));
       dsr[S][2 * jb + 1] = bitcast<V8>(buf_load16_nt(rs, dlane + 1024));
       if (kb + 1 < nkb) {  // the next key block's row (past the last one: stay)
-        int a0, a1, n0, n1;
-        ds_span(p, kb, a0, a1);
-        ds_span(p, kb + 1, n0, n1);
-        d_row += a1 - n0;
+        int n0, n1;
+        ds_span_k<CAUSAL, FEAT>(p, kb + 1, n0, n1);
+        ds_cur += (long long)(sp1 - n0) * 1024;
+        sp1 = n1;
       }
     }
     d_kb32 += C::NKB;
@@ -994,25 +1001,23 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
     const int idx = tid + j * C::NT, r = idx / C::DCH, c = idx % C::DCH;
     voff[j] = 8 * c < HDr ? r * (int)(p.ks.s * 2) + 16 * c : kBufZero;
   }
-  u32x4 ld[NS][C::PER];
+  u32x4 ld[C::PER];
   const T* k_ptr = Kg + (long long)kstart * p.ks.s;
   long long k_left = (long long)(SK - kstart) * p.ks.s * 2;
   const long long k_step = (long long)C::BC * p.ks.s;
-  auto gload = [&](auto set, int t) {
-    constexpr int S = decltype(set)::value;
+  auto gload = [&]() {
     const auto rs = buf_rsrc(k_ptr, k_left);  // past the last tile the descriptor is empty: zeros
 #pragma unroll
-    for (int j = 0; j < C::PER; j++) ld[S][j] = buf_load16(rs, voff[j]);
+    for (int j = 0; j < C::PER; j++) ld[j] = buf_load16(rs, voff[j]);
     k_ptr += k_step;
     k_left -= 2 * k_step;
   };
-  auto lstore = [&](auto set, int stage) {
-    constexpr int S = decltype(set)::value;
+  auto lstore = [&](int stage) {
     T* base = lds + stage * C::KT;
 #pragma unroll
     for (int j = 0; j < C::PER; j++) {
       const int idx = tid + j * C::NT, r = idx / C::DCH, c = idx % C::DCH;
-      *(u32x4*)(base + bofs<C::HD>(r, c)) = ld[S][j];
+      *(u32x4*)(base + bofs<C::HD>(r, c)) = ld[j];
     }
   };
 
@@ -1020,11 +1025,12 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
 #pragma unroll
   for (int db = 0; db < C::NDB; db++) dqacc[db] = f32x16{};
   T* my = dsl[wave];
-  // tile t: K in LDS stage t&1, dS in register set S; tile t+1 goes from set (S+1)%NS to LDS,
-  // tile t+NS-1 is loaded into set (S+NS-1)%NS
+  // tile t: K in LDS stage t&1, dS in register set S; K tile t+1 is loaded into registers and
+  // goes to LDS stage (t+1)&1 at the end of the step, dS tile t+NS-1 is loaded into set
+  // (S+NS-1)%NS
   auto step = [&](auto set, int t) {
     constexpr int S = decltype(set)::value;
-    gload(std::integral_constant<int, (S + NS - 1) % NS>{}, t + NS - 1);
+    gload();
     dsload(std::integral_constant<int, (S + NS - 1) % NS>{}, t + NS - 1);
     // this wave's dS chunks (key rows 32jb + l32, query slots 16sh + 8hh ..) into its LDS block
 #pragma unroll
@@ -1071,16 +1077,14 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
         }
       }
     }
-    lstore(std::integral_constant<int, (S + 1) % NS>{}, (t + 1) & 1);
+    lstore((t + 1) & 1);
     __syncthreads();
   };
 
   if (ntiles > 0) {
-    for_sets(std::make_integer_sequence<int, NS - 1>{}, [&](auto set) {
-      gload(set, decltype(set)::value);
-      dsload(set, decltype(set)::value);
-    });
-    lstore(std::integral_constant<int, 0>{}, 0);
+    gload();
+    for_sets(std::make_integer_sequence<int, NS - 1>{}, [&](auto set) { dsload(set, decltype(set)::value); });
+    lstore(0);
   }
   __syncthreads();
   // whole groups of NS steps (a step past the last tile multiplies nothing): no branch around a
@@ -1095,9 +1099,11 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
   }
 }
 
-// register sets of the dQ-from-dS kernel: tiles loaded one ahead (two ahead measured 1.3%
-// slower on C3 and takes 58 more registers, three ahead the same as two)
-constexpr int kDsqSets = 2;
+// dS register sets of the dQ-from-dS kernel
+#ifndef DSQ_SETS
+#define DSQ_SETS 2
+#endif
+constexpr int kDsqSets = DSQ_SETS;
 // bytes of dS workspace for the fp16/bf16 path (2-byte elements)
 // bytes of the compacted dS workspace (bwd_common.hpp): the table, then every (b, h)'s tiles
 static long long ds_bytes(const FableBwdParams& p) {

@@ -122,6 +122,31 @@ __host__ __device__ inline void ds_span(const FableBwdParams& p, int kb, int& qb
     qb1 = (q1 + 31) >> 5;
   }
 }
+// ds_span inside a kernel instance: CAUSAL is p.causal, and the window terms exist only under
+// FEAT (fable_attn_bwd picks a FEAT instance for every window but the causal right bound 0,
+// which the causal term already covers), so the runtime flag tests drop out
+template <bool CAUSAL, bool FEAT>
+__device__ __forceinline__ void ds_span_k(const FableBwdParams& p, int kb, int& qb0, int& qb1) {
+  const int nqb = (p.SQ + 31) >> 5;
+  if (p.cu_q) {
+    qb0 = 0;
+    qb1 = nqb;
+    return;
+  }
+  const int k0 = 32 * kb, delta = p.SK - p.SQ;
+  int q0 = 0, q1 = p.SQ;
+  if (CAUSAL) q0 = max(q0, k0 - delta);
+  if (FEAT) {
+    if (p.win_right >= 0) q0 = max(q0, k0 - delta - p.win_right);
+    if (p.win_left >= 0) q1 = min(q1, min(k0 + 31, p.SK - 1) - delta + p.win_left + 1);
+  }
+  if (q1 <= q0) {
+    qb0 = qb1 = 0;
+  } else {
+    qb0 = q0 >> 5;
+    qb1 = (q1 + 31) >> 5;
+  }
+}
 __host__ __device__ inline long long ds_header_bytes(int nkb) {
   return ((long long)(nkb + 1) * 4 + 255) / 256 * 256;
 }
