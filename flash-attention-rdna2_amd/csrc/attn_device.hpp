@@ -46,6 +46,10 @@ struct Dt<_Float16> {
   static __device__ __forceinline__ f32x4 mma16(V8 a, V8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
   }
+  // 16x16x16: lane (g, l) holds A[l][4g..4g+3] and B[4g..4g+3][l]
+  static __device__ __forceinline__ f32x4 mma16k16(V4 a, V4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+  }
   static __device__ __forceinline__ float to_f32(_Float16 x) { return (float)x; }
   // c + a.x + a.y with the pair's exact products by one (v_dot2c_f32_f16, fp32 accumulate)
   static __device__ __forceinline__ float sum2(f16x2 a, float c) {
@@ -63,6 +67,10 @@ struct Dt<__bf16> {
   }
   static __device__ __forceinline__ f32x4 mma16(V8 a, V8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ f32x4 mma16k16(V4 a, V4 b, f32x4 c) {
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(s4, a), __builtin_bit_cast(s4, b), c, 0, 0, 0);
   }
   static __device__ __forceinline__ float to_f32(__bf16 x) { return (float)x; }
   static __device__ __forceinline__ float sum2(bf16x2 a, float c) {

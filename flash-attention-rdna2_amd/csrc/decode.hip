@@ -29,7 +29,8 @@ namespace fa {
 
 static int dec_checked(FableDecParams p, int dtype, void* stream, const void* new_k, const void* new_v);
 
-constexpr int kDecChunk = 32;  // keys per wave iteration
+constexpr int kDecChunk = 32;  // keys per wave iteration of the fp32 kernel; splits are multiples
+constexpr int kDecKeys = 16;   // keys per wave iteration of the fp16/bf16 kernel
 constexpr int kDecWaves = 4;
 
 __device__ __forceinline__ float xor16_max(float x) {
@@ -70,10 +71,11 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   static_assert(RCH >= 8, "swizzle needs >= 8 chunks per row");
   // one LDS region, reused: q staging (fp32) before the loop, per-wave V chunks in the loop,
   // the four waves' accumulators after it; per-wave K chunks in a region of their own
-  __shared__ __attribute__((aligned(16))) char vraw[kDecWaves * kDecChunk * HD * 2];
-  __shared__ __attribute__((aligned(16))) char kraw[kDecWaves * kDecChunk * HD * 2];
+  __shared__ __attribute__((aligned(16))) char vraw[kDecWaves * 16 * HD * 4];
+  __shared__ __attribute__((aligned(16))) char kraw[kDecWaves * kDecKeys * HD * 2];
   __shared__ float red_m[kDecWaves][16], red_l[kDecWaves][16];
   static_assert(16 * HD * 4 <= sizeof(vraw), "q staging fits the V region");
+  static_assert(kDecWaves * kDecKeys * HD * 2 <= sizeof(vraw), "the V slices fit the V region");
   float (*qsh)[HD] = (float (*)[HD])vraw;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -141,13 +143,13 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   const T* Vc = (const T*)p.Vc;
   const int* bt = p.block_table + (long long)b * p.max_blocks;
   const int pmask = p.page - 1;
-  T* vb = (T*)vraw + wave * kDecChunk * HD;
-  T* kbuf = (T*)kraw + wave * kDecChunk * HD;
+  T* vb = (T*)vraw + wave * kDecKeys * HD;
+  T* kbuf = (T*)kraw + wave * kDecKeys * HD;
 
   // Keys of a chunk are clamped into [start, end-1] (masked in the softmax), so every load is
   // unconditional. Block-table entries are fetched ahead of the row loads that use them, so the
   // K/V row loads of a chunk issue back to back instead of behind their table lookups.
-  constexpr int NVI = kDecChunk * RCH / 64;  // K (and V) row loads per lane per chunk
+  constexpr int NVI = kDecKeys * RCH / 64;  // K (and V) row loads per lane per chunk
   const int last = rg.end - 1;
   auto vkey = [&](int kc0, int i) { return min(kc0 + (64 * i + lane) / RCH, last); };
   int vblk[SPT ? 1 : NVI], sblk[3];
@@ -210,129 +212,93 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   constexpr int kRowsPerLine = HD >= 128 ? 1 : 128 / HD;
   constexpr int kSwzMask = (RCH < 16 ? RCH : 16) - 1;
   auto kswz = [](int r) { return (r / kRowsPerLine) & kSwzMask; };
-  // Software pipeline: the rows of the next chunk are in flight while this one is computed;
-  // table entries run two chunks ahead. Past the end keys clamp to the last one, so the
-  // trailing prefetch reads a valid row.
-  constexpr int kStep = kDecChunk * kDecWaves;
-  const int kfirst = rg.start + kDecChunk * wave;
+  // Each wave walks 16-key chunks with one register set: a chunk's rows go to LDS, the next
+  // chunk's loads are issued, and the chunk is computed from LDS meanwhile. Table entries run
+  // one chunk ahead. Keys past the end clamp to the last one. Read probes over the C4 cache
+  // streamed fastest with about 8 KiB of rows in flight per wave (16 keys of K and V at
+  // D=128); 32-key chunks with a second register set in flight read ~6% slower there.
+  constexpr int kStep = kDecKeys * kDecWaves;
+  const int kfirst = rg.start + kDecKeys * wave;
   u32x4 kreg[NVI], vreg[NVI];
   if (kfirst < rg.end) {
     table(kfirst);
     load(kfirst, kreg, vreg);
     table(kfirst + kStep);
   }
-
-  // Double-buffered registers fit for HD <= 128; HD = 256 loads the next chunk after the
-  // compute of this one, leaving latency hiding to the other waves.
-  constexpr bool kPipe = HD <= 128;
   for (int kc0 = kfirst; kc0 < rg.end; kc0 += kStep) {
-    u32x4 knxt[NVI], vnxt[NVI];
-    if constexpr (kPipe) {
-      load(kc0 + kStep, knxt, vnxt);
-      table(kc0 + 2 * kStep);
-    }
     zero_pad(kreg, vreg);
-    // K -> this wave's LDS slice; the slice is the wave's own, and LDS operations of one wave
-    // complete in order, so no barrier orders these writes against the reads below or against
-    // the previous chunk's reads
+    // K and V -> this wave's LDS slices; the slices are the wave's own, and LDS operations of
+    // one wave complete in order, so no barrier orders these writes against the reads below or
+    // against the previous chunk's reads
 #pragma unroll
     for (int i = 0; i < NVI; i++) {
       const int row = (64 * i + lane) / RCH, ch = (64 * i + lane) % RCH;
       *(u32x4*)(kbuf + row * HD + 8 * (ch ^ kswz(row))) = kreg[i];
+      *(u32x4*)(vb + row * HD + 8 * (ch ^ (2 * (row & 3)))) = vreg[i];
     }
-    // S^T = K . Q^T, A operand: lane (lg, lh) of block kb reads key row 16*kb + lh, head-dim
-    // chunk 4*ds + lg
-    f32x4 s[2];
-#pragma unroll
-    for (int kb = 0; kb < 2; kb++) {
-      const int row = 16 * kb + lh;
+    // the next chunk's rows are in flight during this chunk's products
+    if (kc0 + kStep < rg.end) {
+      load(kc0 + kStep, kreg, vreg);
+      table(kc0 + 2 * kStep);
+    }
+    // S^T = K . Q^T, A operand: lane (lg, lh) reads key row lh, head-dim chunk 4*ds + lg
+    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+    {
       V8 ka[NDS];
 #pragma unroll
-      for (int ds = 0; ds < NDS; ds++) ka[ds] = bitcast<V8>(*(const u32x4*)(kbuf + row * HD + 8 * ((4 * ds + lg) ^ kswz(row))));
-      s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int ds = 0; ds < NDS; ds++) ka[ds] = bitcast<V8>(*(const u32x4*)(kbuf + lh * HD + 8 * ((4 * ds + lg) ^ kswz(lh))));
 #pragma unroll
-      for (int ds = 0; ds < NDS; ds++) s[kb] = Dt<T>::mma16(ka[ds], qb[ds], s[kb]);
+      for (int ds = 0; ds < NDS; ds++) s = Dt<T>::mma16(ka[ds], qb[ds], s);
       if (qsplit) {
 #pragma unroll
-        for (int ds = 0; ds < NDS; ds++) s[kb] = Dt<T>::mma16(ka[ds], ql[ds], s[kb]);
+        for (int ds = 0; ds < NDS; ds++) s = Dt<T>::mma16(ka[ds], ql[ds], s);
       }
     }
-    // logits (log2 domain) and masking: s[kb][r] is key kc0 + 16*kb + 4*lg + r, head lh
+    // logits (log2 domain) and masking: s[r] is key kc0 + 4*lg + r, head lh
     float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int key = kc0 + 16 * kb + 4 * lg + r;
-        float t;
-        if (FEAT) {
-          float x = s[kb][r] * p.scale;
-          if (p.softcap > 0.0f) x = p.softcap * tanh_exp(x / p.softcap);
-          x += slope * (float)(key - rg.qpos);
-          t = x * kLog2e;
-        } else {
-          t = s[kb][r] * c_log2;
-        }
-        t = key < rg.end ? t : -INFINITY;
-        s[kb][r] = t;
-        mx = fmaxf(mx, t);
+    for (int r = 0; r < 4; r++) {
+      const int key = kc0 + 4 * lg + r;
+      float t;
+      if (FEAT) {
+        float x = s[r] * p.scale;
+        if (p.softcap > 0.0f) x = p.softcap * tanh_exp(x / p.softcap);
+        x += slope * (float)(key - rg.qpos);
+        t = x * kLog2e;
+      } else {
+        t = s[r] * c_log2;
       }
+      t = key < rg.end ? t : -INFINITY;
+      s[r] = t;
+      mx = fmaxf(mx, t);
+    }
     mx = half_max(xor16_max(mx));
     const float m_new = fmaxf(m_run, mx);
     const float m_use = m_new == -INFINITY ? 0.0f : m_new;
     const float corr = exp2_fast(m_run - m_use);
     float rs = 0.0f;
-    V8 pb;
+    typename Dt<T>::V4 pb;  // P^T, the B operand of the k=16 product: keys 4*lg + r, head lh
 #pragma unroll
-    for (int kb = 0; kb < 2; kb++)
-#pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const float e = exp2_fast(s[kb][r] - m_use);
-        rs += e;
-        pb[4 * kb + r] = (T)e;
-      }
+    for (int r = 0; r < 4; r++) {
+      const float e = exp2_fast(s[r] - m_use);
+      rs += e;
+      pb[r] = (T)e;
+    }
     l_run = l_run * corr + rs;
     m_run = m_new;
 #pragma unroll
     for (int db = 0; db < NDB; db++) oacc[db] *= corr;
-    // V -> this wave's LDS slice, chunk-swizzled: physical chunk = chunk ^ 2*(row % 4)
-#pragma unroll
-    for (int i = 0; i < NVI; i++) {
-      const int row = (64 * i + lane) / RCH, ch = (64 * i + lane) % RCH;
-      *(u32x4*)(vb + row * HD + 8 * (ch ^ (2 * (row & 3)))) = vreg[i];
-    }
-    // O^T += V^T . P^T, A operand by transposing LDS reads: lane lh of group lg addresses
-    // row 16*half + 4*lg + lh/4, head-dim 16*db + 4*(lh%4); it receives V[16*half+4*lg+r][16*db+lh]
+    // O^T += V^T . P^T, A operand by transposing LDS reads: lane lh of group lg addresses row
+    // 4*lg + lh/4, head-dim 16*db + 4*(lh%4); it receives V[4*lg + r][16*db + lh]
 #pragma unroll
     for (int db = 0; db < NDB; db++) {
-      typename Dt<T>::V4 part[2];
-#pragma unroll
-      for (int hf = 0; hf < 2; hf++) {
-        const int row = 16 * hf + 4 * lg + (lh >> 2);
-        const int col = 16 * db + 4 * (lh & 3);
-        const int off = row * HD + 8 * ((col >> 3) ^ (2 * (row & 3))) + (col & 7);
-        typedef short s4 __attribute__((ext_vector_type(4)));
-        s4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) s4*)((__attribute__((address_space(3))) T*)vb + off));
-        part[hf] = bitcast<typename Dt<T>::V4>(t);
-      }
-      V8 a;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        a[e] = part[0][e];
-        a[4 + e] = part[1][e];
-      }
-      oacc[db] = Dt<T>::mma16(a, pb, oacc[db]);
-    }
-    if constexpr (kPipe) {
-#pragma unroll
-      for (int i = 0; i < NVI; i++) {
-        kreg[i] = knxt[i];
-        vreg[i] = vnxt[i];
-      }
-    } else {
-      load(kc0 + kStep, kreg, vreg);
-      table(kc0 + 2 * kStep);
+      const int row = 4 * lg + (lh >> 2);
+      const int col = 16 * db + 4 * (lh & 3);
+      const int off = row * HD + 8 * ((col >> 3) ^ (2 * (row & 3))) + (col & 7);
+      typedef short s4 __attribute__((ext_vector_type(4)));
+      const s4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) s4*)((__attribute__((address_space(3))) T*)vb + off));
+      oacc[db] = Dt<T>::mma16k16(bitcast<typename Dt<T>::V4>(t), pb, oacc[db]);
     }
   }
 
