@@ -11,10 +11,11 @@
 //    row) and staged per wave in LDS; S^T = K . Q^T reads its A operand (16 bytes of one key
 //    row per lane) back from the K slice, and the 16x16 result leaves every lane with one head
 //    and four keys;
-//  * P^T is the B operand of O^T = V^T . P^T without leaving registers; V is read back from
-//    its slice transposed with ds_read_b64_tr_b16;
-//  * each wave streams its own 32-key chunks (no barriers in the loop); the four waves merge
-//    in LDS at the end and write one (max, sum, acc[HD]) partial per head and split;
+//  * P^T is the B operand of O^T = V^T . P^T (v_mfma_f32_16x16x16) without leaving registers;
+//    V is read back from its slice transposed with ds_read_b64_tr_b16;
+//  * each wave streams its own 16-key chunks (fp32: 32-key) with no barriers in the loop; the
+//    four waves merge in LDS at the end and write one (max, sum, acc[HD]) partial per head and
+//    split;
 //  * the combine kernel merges the splits (natural-log LSE optional);
 //  * appending new_k/new_v (with rotary on k) is a kernel earlier in the same stream: the
 //    reference's hipDeviceSynchronize() after the append (fa_decode.hip:348-351) is gone.
@@ -32,6 +33,7 @@ static int dec_checked(FableDecParams p, int dtype, void* stream, const void* ne
 constexpr int kDecChunk = 32;  // keys per wave iteration of the fp32 kernel; splits are multiples
 constexpr int kDecKeys = 16;   // keys per wave iteration of the fp16/bf16 kernel
 constexpr int kDecWaves = 4;
+static_assert(kDecKeys <= 16, "a chunk spans at most two pages of >= 16 rows (SPT)");
 
 __device__ __forceinline__ float xor16_max(float x) {
   return fmaxf(x, __shfl_xor(x, 16));
@@ -58,10 +60,11 @@ __device__ __forceinline__ DecRange dec_range(const FableDecParams& p, int b, in
 }
 
 // SPT (page >= 16): the block-table entries of a chunk are fetched by scalar loads. A chunk of
-// 32 keys touches at most three pages then, and each lane selects its row's entry from the
-// three. Per-lane table loads share the in-order vector-memory counter with the row loads, so
-// a wave waiting for its next entries also waited for the rows issued before them (the chunk
-// in flight): C4 read ~4% slower that way. Smaller pages (a dense cache of < 16 rows) keep them.
+// 16 keys touches at most two pages then, and each lane selects its row's entry from the two.
+// Per-lane table loads share the in-order vector-memory counter with the row loads, so a wave
+// waiting for its next entries also waited for the rows issued before them (the chunk in
+// flight): C4 +1% with the scalar loads (+4% in a read probe). Smaller pages (a dense cache of
+// fewer than 16 rows) keep per-lane loads.
 template <typename T, int HD, bool FEAT, bool SPT>
 __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int page_shift, int ngrp, int append) {
   using V8 = typename Dt<T>::V8;
@@ -152,23 +155,23 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   constexpr int NVI = kDecKeys * RCH / 64;  // K (and V) row loads per lane per chunk
   const int last = rg.end - 1;
   auto vkey = [&](int kc0, int i) { return min(kc0 + (64 * i + lane) / RCH, last); };
-  int vblk[SPT ? 1 : NVI], sblk[3];
+  int vblk[SPT ? 1 : NVI], sblk[2];
   auto table = [&](int kc0) {
     if constexpr (SPT) {
       const int b0 = kc0 >> page_shift, bl = last >> page_shift;  // wave-uniform
 #pragma unroll
-      for (int j = 0; j < 3; j++) sblk[j] = bt[min(b0 + j, bl)];
+      for (int j = 0; j < 2; j++) sblk[j] = bt[min(b0 + j, bl)];
     } else {
 #pragma unroll
       for (int i = 0; i < NVI; i++) vblk[i] = bt[vkey(kc0, i) >> page_shift];
     }
   };
-  // entry of load i's row: page (key >> page_shift) - (kc0 >> page_shift) of the chunk's three
+  // entry of load i's row: page (key >> page_shift) - (kc0 >> page_shift) of the chunk's two
   // (a key clamped to `last` lies in the chunk's last page, whose index the table clamped too)
   auto blk_of = [&](int kc0, int i) {
     if constexpr (SPT) {
       const int j = (vkey(kc0, i) >> page_shift) - (kc0 >> page_shift);
-      return j <= 0 ? sblk[0] : (j == 1 ? sblk[1] : sblk[2]);
+      return j <= 0 ? sblk[0] : sblk[1];
     } else {
       return vblk[i];
     }
