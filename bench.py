@@ -434,7 +434,7 @@ FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128ELi64ELi8ELi2ELi1EEELb
 FWD_C1_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi64E.*ELb0ELb0ELb0EEEv14FableFwdParamsi"
 BWD_C3_KERNELS = (r"_ZN2fa15bwd_dsum_kernelIDF16b.*", r"_ZN2fa20bwd_dkdv_pair_kernelIDF16b.*",
                   r"_ZN2fa16bwd_dq_ds_kernelIDF16b.*")
-DEC_C4_KERNELS = (r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0EEEv14FableDecParamsiii",
+DEC_C4_KERNELS = (r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0ELb1EEEv14FableDecParamsiii",
                   r"_ZN2fa18dec_combine_kernelIDF16_Li128EEEv14FableDecParams")
 VARLEN_C5_KERNEL = r"_ZN2fa10fwd_kernelIDF16bNS_6FwdCfgILi256E.*ELb1ELb1ELb0EEEv14FableFwdParamsi"
 
