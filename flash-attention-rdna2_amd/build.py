@@ -28,12 +28,16 @@ FLAGS = ["--offload-arch=" + ARCH, "-O3", "-std=c++17", "-fPIC",
 
 
 # per-source extra flags
-EXTRA = {"bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+def _extra(name):
+    # the fp16/bf16 backward kernels (bwd_dNN.hip) keep MFMA accumulators in VGPR form
+    if name.startswith("bwd_d") and name.endswith(".hip"):
+        return ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]
+    return []
 
 
 def _compile(src):
     obj = os.path.join(OBJ, os.path.basename(src).replace(".hip", ".o"))
-    cmd = [HIPCC] + FLAGS + EXTRA.get(os.path.basename(src), []) + ["-c", src, "-o", obj]
+    cmd = [HIPCC] + FLAGS + _extra(os.path.basename(src)) + ["-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"compile failed: {' '.join(cmd)}\n{r.stdout}\n{r.stderr}")

@@ -206,4 +206,16 @@ __device__ __forceinline__ int ds_slot_query(int n) {
 // the fp32 backward (bwd_f32.hip), dispatched from fable_attn_bwd
 int launch_bwd_f32(const FableBwdParams& p, hipStream_t st);
 
+// kernel width for head dim D (a multiple of 8 up to 256): the next multiple of 32
+inline int bwd_width(int D) { return (D + 31) / 32 * 32; }
+// the fp16/bf16 kernels of each width (bwd_dNN.hip), dispatched from fable_attn_bwd
+int launch_bwd_d32(const FableBwdParams& p, int dtype, hipStream_t st);
+int launch_bwd_d64(const FableBwdParams& p, int dtype, hipStream_t st);
+int launch_bwd_d96(const FableBwdParams& p, int dtype, hipStream_t st);
+int launch_bwd_d128(const FableBwdParams& p, int dtype, hipStream_t st);
+int launch_bwd_d160(const FableBwdParams& p, int dtype, hipStream_t st);
+int launch_bwd_d192(const FableBwdParams& p, int dtype, hipStream_t st);
+int launch_bwd_d224(const FableBwdParams& p, int dtype, hipStream_t st);
+int launch_bwd_d256(const FableBwdParams& p, int dtype, hipStream_t st);
+
 }  // namespace fa

@@ -46,8 +46,12 @@ CASES = [
     ("softcap 30", 1, 4, 4, 128, 128, 64, False, -1, -1, 30.0, False),
     ("alibi causal", 1, 4, 4, 128, 128, 64, True, -1, -1, 0.0, True),
     ("D128 causal B2 S512", 2, 4, 4, 512, 512, 128, True, -1, -1, 0.0, False),
-    # head dims other than 64/128/256 (zero columns inside the 64/128/256-wide kernels)
+    # every kernel width (multiples of 32), and head dims below their width (zero columns)
+    ("D16 causal", 1, 4, 2, 130, 130, 16, True, -1, -1, 0.0, False),
     ("D32 causal", 1, 4, 2, 150, 150, 32, True, -1, -1, 0.0, False),
+    ("D136 full gqa", 1, 4, 2, 90, 110, 136, False, -1, -1, 0.0, False),
+    ("D176 causal", 1, 2, 2, 100, 100, 176, True, -1, -1, 0.0, False),
+    ("D200 window (30,10)", 1, 2, 1, 90, 90, 200, False, 30, 10, 0.0, False),
     ("D48 full", 1, 4, 4, 100, 120, 48, False, -1, -1, 0.0, False),
     ("D80 causal gqa", 1, 8, 2, 160, 160, 80, True, -1, -1, 0.0, False),
     ("D96 window (40,0)", 1, 4, 4, 200, 200, 96, False, 40, 0, 0.0, False),
