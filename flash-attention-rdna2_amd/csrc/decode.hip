@@ -212,9 +212,15 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
   // K slice: row r holds logical 16-byte chunk c at physical chunk c ^ kswz(r). The rows of
   // one 256-byte bank line share a pattern and consecutive lines differ, so the 16 lanes of an
   // A-operand read (16 rows, one chunk) and of a row write hit 16 different bank groups.
+  // (A width whose chunk count is not a power of two XORs within aligned groups of the largest
+  // power of two that divides it, so a chunk never leaves its row: 12 chunks at width 96 swizzle
+  // in groups of 4.)
   constexpr int kRowsPerLine = HD >= 128 ? 1 : 128 / HD;
-  constexpr int kSwzMask = (RCH < 16 ? RCH : 16) - 1;
+  constexpr int kSwzGroup = (RCH & -RCH) < 16 ? (RCH & -RCH) : 16;
+  constexpr int kSwzMask = kSwzGroup - 1;
   auto kswz = [](int r) { return (r / kRowsPerLine) & kSwzMask; };
+  // V slice: chunk c of row r at c ^ vswz(r), pairs of chunks for the transposing reads
+  auto vswz = [](int r) { return kSwzGroup >= 8 ? 2 * (r & 3) : 2 * (r & 1); };
   // Each wave walks 16-key chunks with one register set: a chunk's rows go to LDS, the next
   // chunk's loads are issued, and the chunk is computed from LDS meanwhile. Table entries run
   // one chunk ahead. Keys past the end clamp to the last one. Read probes over the C4 cache
@@ -237,7 +243,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
     for (int i = 0; i < NVI; i++) {
       const int row = (64 * i + lane) / RCH, ch = (64 * i + lane) % RCH;
       *(u32x4*)(kbuf + row * HD + 8 * (ch ^ kswz(row))) = kreg[i];
-      *(u32x4*)(vb + row * HD + 8 * (ch ^ (2 * (row & 3)))) = vreg[i];
+      *(u32x4*)(vb + row * HD + 8 * (ch ^ vswz(row))) = vreg[i];
     }
     // the next chunk's rows are in flight during this chunk's products
     if (kc0 + kStep < rg.end) {
@@ -297,7 +303,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
     for (int db = 0; db < NDB; db++) {
       const int row = 4 * lg + (lh >> 2);
       const int col = 16 * db + 4 * (lh & 3);
-      const int off = row * HD + 8 * ((col >> 3) ^ (2 * (row & 3))) + (col & 7);
+      const int off = row * HD + 8 * ((col >> 3) ^ vswz(row)) + (col & 7);
       typedef short s4 __attribute__((ext_vector_type(4)));
       const s4 t = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
           (__attribute__((address_space(3))) s4*)((__attribute__((address_space(3))) T*)vb + off));
@@ -599,9 +605,9 @@ static int launch_dec(const FableDecParams& p, hipStream_t st, const void* nk, c
   return launch_status("fable_attn_dec (combine)");
 }
 
-// fp16/bf16: every head dim that is a multiple of 8 up to 256 runs in the kernel of width 64,
-// 128 or 256 with zero columns past it. The loads skip those columns' bytes, so HBM traffic is
-// that of the real head dim; only matrix-core work, which does not bound decode, grows.
+// fp16/bf16: every head dim that is a multiple of 8 up to 256 runs in the kernel of the next
+// multiple of 32 (64 at least: the K slice swizzle needs 8 chunks per row) with zero columns
+// past it. The loads skip those columns' bytes, so HBM traffic is that of the real head dim.
 // fp32 has kernels for 64, 128 and 256 exactly.
 template <typename T>
 static int dec_dispatch(const FableDecParams& p, hipStream_t st, const void* nk, const void* nv) {
@@ -609,9 +615,21 @@ static int dec_dispatch(const FableDecParams& p, hipStream_t st, const void* nk,
   if (p.HD <= 0 || p.HD > 256 || p.HD % 8 || (f32 && p.HD != 64 && p.HD != 128 && p.HD != 256))
     return fail(FA_ERR_HEADDIM, "fable_attn_dec: head_dim=%d has no kernel (%s)", p.HD,
                 f32 ? "64, 128, 256 for fp32" : "multiples of 8 up to 256");
-  if (p.HD <= 64) return launch_dec<T, 64>(p, st, nk, nv);
-  if (p.HD <= 128) return launch_dec<T, 128>(p, st, nk, nv);
-  return launch_dec<T, 256>(p, st, nk, nv);
+  if constexpr (f32) {
+    if (p.HD == 64) return launch_dec<T, 64>(p, st, nk, nv);
+    if (p.HD == 128) return launch_dec<T, 128>(p, st, nk, nv);
+    return launch_dec<T, 256>(p, st, nk, nv);
+  } else {
+    switch (p.HD <= 64 ? 2 : (p.HD + 31) / 32) {
+      case 2: return launch_dec<T, 64>(p, st, nk, nv);
+      case 3: return launch_dec<T, 96>(p, st, nk, nv);
+      case 4: return launch_dec<T, 128>(p, st, nk, nv);
+      case 5: return launch_dec<T, 160>(p, st, nk, nv);
+      case 6: return launch_dec<T, 192>(p, st, nk, nv);
+      case 7: return launch_dec<T, 224>(p, st, nk, nv);
+      default: return launch_dec<T, 256>(p, st, nk, nv);
+    }
+  }
 }
 
 }  // namespace fa

@@ -126,8 +126,9 @@ def test_decode_parity(case, dt):
                 assert np.array_equal(vcn[blk, pos % page], c["nv"][b, t])
 
 
-# head dims other than 64/128/256 (zero columns inside the 64/128/256-wide kernels; rows in the
-# cache are the real head dim long), with append and rotary; fp16/bf16 (fp32 has 64/128/256)
+# head dims other than 64/128/256: fp16/bf16 kernels of every width that is a multiple of 32
+# from 64 up, zero columns past the head dim (rows in the cache are the real head dim long), with
+# append and rotary; fp32 has 64/128/256
 DIM_CASES = [
     ("HD32 append+rotary", 32, 8, 4, [70, 200], -1, 1, True, 0, 2, 0.0, False, 16),
     ("HD80 append+rotary interleaved", 80, 16, 4, [300], -1, 2, True, 0, 1, 0.0, False, 16),
@@ -136,6 +137,9 @@ DIM_CASES = [
     ("HD160 append", 160, 8, 4, [300], -1, 1, True, 0, 1, 0.0, False, 16),
     ("HD192 leftpad alibi", 192, 8, 8, [400], -1, 0, False, 37, 1, 0.0, True, 16),
     ("HD200 append rotary", 200, 4, 2, [130], -1, 1, True, 0, 2, 0.0, False, 16),
+    ("HD224 GQA4 window", 224, 8, 4, [260, 33], 100, 0, False, 0, 1, 0.0, False, 16),
+    ("HD136 page8 append", 136, 4, 2, [90], -1, 0, True, 0, 1, 0.0, False, 8),
+    ("HD88 page4 softcap", 88, 8, 4, [150], -1, 0, False, 0, 2, 20.0, False, 4),
 ]
 
 
