@@ -382,8 +382,14 @@ fwd_kernel(FableFwdParams p, int nqt) {
     const float m_cand = fmaxf(m_run[i], FEAT ? mx : mx * c_log2);
     const bool need = m_cand > m_run[i] + kLazyMax;
     const float corr = need ? exp2_fast(m_run[i] - m_cand) : 1.0f;
+    // While a row's running max is -inf no key has been visible to it and its O accumulators
+    // are still zero: the first tile a row sees moves the max but needs no rescale. The feature
+    // kernels skip it (at head dim 256 a rescale is 384 VALU instructions, a tenth of a 512-key
+    // window's work: C5 +1.3%); on the long rows of the plain kernels the extra test per tile
+    // cost more than the one rescale (D=160/192 0.98x)
+    const bool scale_o = FEAT ? need && m_run[i] != -INFINITY : need;
     m_run[i] = need ? m_cand : m_run[i];
-    resc = __builtin_amdgcn_ballot_w64(need) != 0;
+    resc = __builtin_amdgcn_ballot_w64(scale_o) != 0;
     const float m_use = m_run[i] == -INFINITY ? 0.0f : m_run[i];
     // The row sum adds the fp32 probabilities (not the rounded ones the PV product takes): the
     // LSE is then exact to fp32 rounding, and the backward, which rebuilds P = exp(s - LSE),
