@@ -1107,9 +1107,8 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
 #define DSQ_SETS 2
 #endif
 constexpr int kDsqSets = DSQ_SETS;
-// bytes of dS workspace for the fp16/bf16 path (2-byte elements)
 // bytes of the compacted dS workspace (bwd_common.hpp): the table, then every (b, h)'s tiles
-static long long ds_bytes(const FableBwdParams& p) {
+inline long long ds_bytes(const FableBwdParams& p) {
   if (p.SQ <= 0 || p.SK <= 0) return 0;
   const long long t = ds_tiles_per_head(p);  // 0: no query sees any key, the recomputing path serves
   return t > 0 ? ds_header_bytes((p.SK + 31) >> 5) + (long long)p.B * p.Hq * t * 2048 : 0;
