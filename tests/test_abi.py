@@ -181,8 +181,12 @@ def test_bwd_ds_workspace_size():
     p.D = 80                                                 # any multiple of 8 up to 128
     assert lib.fable_attn_bwd_ds_bytes(p, 1) == want
     assert lib.fable_attn_bwd_ds_bytes(p, 2) == 0      # fp32 recomputes
-    p.D = 256
-    assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0
+    for d in (8, 16, 32, 96, 120):                         # widths 32 and 96 have the path too
+        p.D = d
+        assert lib.fable_attn_bwd_ds_bytes(p, 1) == want, d
+    for d in (136, 160, 192, 224, 256):                    # one-wave-per-SIMD widths recompute
+        p.D = d
+        assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0, d
     p.D, p.SQ = 128, 0
     assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0
     # causal and windowed: only the tiles with a visible pair
