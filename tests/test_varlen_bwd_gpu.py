@@ -32,6 +32,12 @@ CASES = [
     ("sq!=sk causal D128", [40, 96, 33], [64, 96, 17], 4, 4, 128, True, -1, -1, 0.0),
     ("window softcap D64", [150, 90], None, 4, 2, 64, True, 31, 0, 20.0),
     ("D256 causal", [70, 33], None, 2, 2, 256, True, -1, -1, 0.0),
+    # the other kernel widths (multiples of 32; 88 runs in the 96-wide kernel)
+    ("D32 ragged causal gqa", [50, 3, 97], None, 4, 2, 32, True, -1, -1, 0.0),
+    ("D88 window", [120, 64], None, 2, 2, 88, False, 20, 5, 0.0),
+    ("D160 ragged full", [45, 80], [60, 33], 2, 1, 160, False, -1, -1, 0.0),
+    ("D192 causal softcap", [66, 31], None, 2, 2, 192, True, -1, -1, 15.0),
+    ("D224 causal", [40, 70], None, 2, 2, 224, True, -1, -1, 0.0),
 ]
 
 
