@@ -34,6 +34,11 @@ CASES = [
     ("D128 causal SQ<SK", 1, 4, 4, 100, 160, 128, True, 0.3, 0.0),
     ("D128 softcap gqa", 1, 4, 2, 128, 128, 128, False, 0.2, 20.0),
     ("D256 causal", 1, 2, 2, 80, 80, 256, True, 0.25, 0.0),
+    # dropout kernels of the other widths
+    ("D32 causal", 1, 4, 2, 100, 100, 32, True, 0.15, 0.0),
+    ("D96 full", 1, 2, 2, 70, 90, 96, False, 0.2, 0.0),
+    ("D160 causal", 1, 2, 1, 64, 64, 160, True, 0.1, 0.0),
+    ("D192 full softcap", 1, 2, 2, 60, 60, 192, False, 0.3, 10.0),
 ]
 
 
