@@ -65,8 +65,12 @@ __device__ __forceinline__ DecRange dec_range(const FableDecParams& p, int b, in
 // waiting for its next entries also waited for the rows issued before them (the chunk in
 // flight): C4 +1% with the scalar loads (+4% in a read probe). Smaller pages (a dense cache of
 // fewer than 16 rows) keep per-lane loads.
+// flags: bit 0 new keys were appended (kDecAppend), bit 1 the kernel writes the final output and
+// LSE itself (kDecFinal: one split, no combine launch)
+constexpr int kDecAppend = 1, kDecFinal = 2;
 template <typename T, int HD, bool FEAT, bool SPT>
-__global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int page_shift, int ngrp, int append) {
+__global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int page_shift, int ngrp, int flags) {
+  const int append = flags & kDecAppend;
   using V8 = typename Dt<T>::V8;
   constexpr int NDS = HD / 32;  // S^T contraction steps
   constexpr int NDB = HD / 16;  // 16-row blocks of O^T
@@ -324,6 +328,7 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
 #pragma unroll
     for (int r = 0; r < 4; r++) red_o[(wave * 16 + lh) * HD + 16 * db + 4 * lg + r] = oacc[db][r];
   __syncthreads();
+  const bool final_out = (flags & kDecFinal) != 0;
   for (int i = tid; i < hg * HDr; i += 256) {
     const int g = i / HDr, d = i % HDr;
     float gm = -INFINITY;
@@ -337,6 +342,14 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
         l += f * red_l[w][g];
         acc += f * red_o[(w * 16 + g) * HD + d];
       }
+    }
+    if (final_out) {
+      // what the combine kernel computes from one split (its weight exp2(0) is exactly 1)
+      const long long row = (long long)(b * p.nq + tk) * p.NH + h0 + g;
+      const bool ok = gm != -INFINITY && l > 0.0f;
+      ((T*)p.o)[row * HDr + d] = (T)(ok ? acc / l : 0.0f);
+      if (p.lse_out && d == 0) p.lse_out[row] = ok ? gm * kLn2 + __logf(l) : -INFINITY;
+      continue;
     }
     float* out = p.scratch + (((long long)(b * p.nq + tk) * p.NH + h0 + g) * p.nsplit + sp) * (HDr + 2);
     if (d == 0) {
@@ -591,14 +604,18 @@ static int launch_dec(const FableDecParams& p, hipStream_t st, const void* nk, c
       hipLaunchKernelGGL((dec_partial_f32_kernel<HD, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
   } else {
     const bool spt = p.page >= 16;
+    // one split: the partial kernel writes the output and LSE, and no combine is launched
+    const int flags = (nk ? kDecAppend : 0) | (p.nsplit == 1 ? kDecFinal : 0);
     if (feat && spt)
-      hipLaunchKernelGGL((dec_partial_kernel<T, HD, true, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, true, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, flags);
     else if (feat)
-      hipLaunchKernelGGL((dec_partial_kernel<T, HD, true, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, true, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, flags);
     else if (spt)
-      hipLaunchKernelGGL((dec_partial_kernel<T, HD, false, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, false, true>), grid, dim3(256), 0, st, p, page_shift, ngrp, flags);
     else
-      hipLaunchKernelGGL((dec_partial_kernel<T, HD, false, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, nk ? 1 : 0);
+      hipLaunchKernelGGL((dec_partial_kernel<T, HD, false, false>), grid, dim3(256), 0, st, p, page_shift, ngrp, flags);
+    if (int rc = launch_status("fable_attn_dec (partial)")) return rc;
+    if (p.nsplit == 1) return FA_OK;
   }
   if (int rc = launch_status("fable_attn_dec (partial)")) return rc;
   hipLaunchKernelGGL((dec_combine_kernel<T, HD>), dim3(p.batch * p.nq, p.NH), dim3(HD), 0, st, p);
