@@ -16,7 +16,7 @@
 //     S = Q.K^T and dP = dO.V^T; P and dS stay in registers as B operands of
 //     dV^T += dO^T.P and dK^T += Q^T.dS (dO^T/Q^T by transposing LDS reads).
 // On that recomputing path S and dP are computed in both kernels (the price of no atomics, as in
-// the reference). With a dS workspace (FableBwdParams.ds_ws, fp16/bf16 at head dims up to 128) the order
+// the reference). With a dS workspace (FableBwdParams.ds_ws, fp16/bf16 at kernel widths up to 128) the order
 // is instead: a rowsum kernel for D, the dK/dV kernel, which also stores each dS tile once, and
 // a dQ kernel that forms dQ = dS.K from the stored tiles; every product is computed once, still
 // without atomics and in a fixed order.

@@ -1,5 +1,5 @@
 // fwd.hip — fable_attn_fwd, the forward's C-ABI entry point: argument checks and dispatch to
-// the per-head-dim fp16/bf16 kernels (fwd_d64/128/256.hip, kernel in fwd_kernel.hpp) and the
+// the per-width fp16/bf16 kernels (fwd_d32.hip .. fwd_d256.hip, kernel in fwd_kernel.hpp) and the
 // fp32 kernels (fwd_f32.hip). Reference launcher: kernels/fa_forward.hip:424-451.
 #include "attn_device.hpp"
 #include "fwd_common.hpp"
