@@ -479,6 +479,23 @@ def summarize_parity(path):
         fl = [r[g + "_floor"] for r in rs for g in ("dq", "dk", "dv") if r.get(g + "_floor") is not None]
         out.append(f"| {test} | {dt} | {len(rs)} | {ocol} | {fmt(worst(rs, 'lse'))} | "
                    + " | ".join(cols) + f" | {fmt(max(fl) if fl else None)} |")
+    # every gradient whose bound is not the flat one (floor above 2/3 of it)
+    raised = []
+    for (test, dt), rs in sorted(groups.items()):
+        for r in rs:
+            for g in ("dq", "dk", "dv"):
+                f = r.get(g + "_floor")
+                if r.get(g) is not None and f is not None and f > gtol[dt] * 2 / 3:
+                    raised.append((test, r.get("case", ""), dt, g, r[g], f, 1.5 * f, gtol[dt]))
+    out += ["", f"Gradients held to 1.5x their floor instead of the flat bound: {len(raised)} "
+            f"(of {sum(1 for rs in groups.values() for r in rs for g in ('dq', 'dk', 'dv') if r.get(g) is not None)} "
+            "checked gradients).", ""]
+    if raised:
+        out += ["| test | case | dtype | gradient | rel_rms | floor | bound (1.5x floor) | "
+                "above the flat bound |", "|---|---|---|---|---|---|---|---|"]
+        for test, case, dt, g, e, f, b, flat in raised:
+            out.append(f"| {test} | {case} | {dt} | {g} | {e:.2e} | {f:.2e} | {max(b, flat):.2e} | "
+                       f"{'yes' if e > flat else 'no'} ({flat:.0e}) |")
     return "\n".join(out)
 
 

@@ -201,8 +201,9 @@ def bwd(q, k, v, do, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0
     model=None gives the exact gradients. model='f16'/'bf16' gives the rounding model of a
     backward whose matrix products take 16-bit operands (oracle.c bwd_impl): O rounded before
     D = rowsum(O*dO), z*P rounded before the dV product, dS rounded before the dK/dQ products;
-    its distance from the exact gradients is the floor of any such kernel. stored_o (model
-    only): the forward output [B,H,SQ,D] a kernel stored, to take D = rowsum(O*dO) from."""
+    its distance from the exact gradients is the floor of any such kernel. stored_o: the
+    forward output [B,H,SQ,D] a kernel stored, to take D = rowsum(O*dO) from (with model=None
+    the arithmetic stays exact and only D comes from stored_o)."""
     q, k, v, do = _f32(q), _f32(k), _f32(v), _f32(do)
     B, H, SQ, D = q.shape
     Hk, SK = k.shape[1], k.shape[2]
@@ -215,7 +216,7 @@ def bwd(q, k, v, do, scale, causal=False, win_left=-1, win_right=-1, softcap=0.0
                     al.ctypes.data if al is not None else None, _f32s(dropout_p),
                     int(seed) & ((1 << 64) - 1))
     mode = {None: 0, "f32": 0, "f16": 1, "bf16": 2}[model]
-    if mode:
+    if mode or stored_o is not None:
         so = _f32(stored_o) if stored_o is not None else None
         lib().oracle_bwd_model(_p(q), _p(k), _p(v), _p(do), _p(dq), _p(dk), _p(dv),
                                ctypes.byref(cfg), ctypes.c_int(mode), _p(so))

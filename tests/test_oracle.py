@@ -9,6 +9,10 @@ The oracle is trusted only after these checks:
   * backward: torch.autograd on an fp64 CPU attention and central finite differences of an
     fp64 forward, including softcap (whose derivative a plausible bug would drop), GQA and
     windows;
+  * backward rounding model (the dtype roundings of a 16-bit-operand backward, which sets the
+    floor of the gradient bounds): bit-exact where one key per query makes dS vanish, the
+    closed-form shift of dQ/dK (and none of dV) when the stored O moves, and a distance from
+    the exact gradients that is a fraction of the unit roundoff and ~8x larger in bf16;
   * decode: the forward oracle on gathered pages (no append, append, window, leftpad, nq > 1),
     rotary against a complex-multiplication rotation, invariance under page permutation;
   * combine: merging two key halves equals attention over all keys;
@@ -458,3 +462,110 @@ def test_dropout_backward_finite_differences():
                 am[pos][idx] -= eps
                 fd = (loss(*ap) - loss(*am)) / (2 * eps)
                 assert abs(fd - g[idx]) <= 1e-5 + 1e-4 * abs(fd), ("qkv"[pos], idx, fd, g[idx])
+
+
+# ----------------------------------------------------------------------------- rounding model
+# oracle.bwd(..., model=dt) is the backward in the roundings of a 16-bit-operand kernel (D from
+# the stored O, z*P and dS rounded to the dtype); the GPU gradient tests raise a case's bound to
+# 1.5x its distance from the exact gradients (its floor) when that floor is large. The checks
+# below pin the model by what the mathematics fixes, so a misplaced or missing rounding, a D
+# taken from the wrong O, or a dropped term changes a result here.
+def _np_probs(q, k, scale, causal, wl=-1, wr=-1, softcap=0.0):
+    """fp64 softmax probabilities P [B,H,SQ,SK] and the softcap derivative of the logit
+    (1 - tanh^2, or 1), textbook numpy, GQA by head repetition."""
+    H, Hk = q.shape[1], k.shape[1]
+    kk = np.repeat(k, H // Hk, axis=1).astype(np.float64)
+    x = np.einsum("bhid,bhjd->bhij", q.astype(np.float64), kk) * scale
+    deriv = np.ones_like(x)
+    if softcap > 0:
+        t = np.tanh(x / softcap)
+        x, deriv = softcap * t, 1.0 - t * t
+    SQ, SK = q.shape[2], k.shape[2]
+    i, j, d = np.arange(SQ)[:, None], np.arange(SK)[None, :], SK - SQ
+    m = np.zeros((SQ, SK), dtype=bool)
+    if causal:
+        m |= j > i + d
+    if wl >= 0:
+        m |= j < i + d - wl
+    if wr >= 0:
+        m |= j > i + d + wr
+    x = np.where(m, -np.inf, x)
+    p = np.exp(x - x.max(-1, keepdims=True))
+    return p / p.sum(-1, keepdims=True), deriv
+
+
+def _rounded(shapes, seed, dt):
+    rng = np.random.default_rng(seed)
+    return [orc.round_to(rng.standard_normal(s), dt) for s in shapes]
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+def test_bwd_model_single_visible_key_is_exact(dt):
+    """Window (0, 0) leaves each query one key: P = 1, O = that V row (already in the dtype, so
+    rounding O changes nothing), dP = dO.V = D, so dS = 0 exactly and dV_j = the sum of dO over
+    the query heads that see key j. The model must reproduce the exact gradients bit for bit; a
+    rounding of dP but not of D (or of D's O before the sum differently) would leave dS != 0."""
+    B, H, Hk, S, D = 1, 4, 2, 20, 16
+    q, k, v, do = _rounded(((B, H, S, D), (B, Hk, S, D), (B, Hk, S, D), (B, H, S, D)), 11, dt)
+    ex = orc.bwd(q, k, v, do, 0.25, False, 0, 0)
+    md = orc.bwd(q, k, v, do, 0.25, False, 0, 0, model=dt)
+    for a, b in zip(ex, md):
+        assert np.array_equal(a, b)
+    assert not md[0].any() and not md[1].any()
+    want_dv = do.astype(np.float64).reshape(B, Hk, H // Hk, S, D).sum(2)
+    assert np.array_equal(md[2], want_dv)
+
+
+@pytest.mark.parametrize("model", [None, "f16", "bf16"])
+def test_bwd_model_stored_o_shifts_ds(model):
+    """D = rowsum(O*dO) comes from the stored O: replacing O by O + delta changes D_i by
+    dO_i.delta_i, hence dS_ij by -P_ij*(dO_i.delta_i)*deriv_ij, dQ_i by scale*sum_j dS_ij K_j and
+    dK_j by scale*sum_i dS_ij Q_i (GQA heads summed), and leaves dV unchanged. In exact
+    arithmetic this holds to fp64 rounding; in a dtype model each dS is rounded, so the shift
+    holds to a few unit roundoffs. Softcap and a causal window make deriv and the mask matter."""
+    B, H, Hk, SQ, SK, D = 1, 4, 2, 24, 40, 16
+    scale, sc, causal, wl = float(np.float32(0.3)), 4.0, True, 9   # the oracle takes fp32 scalars
+    dt = model or "f16"
+    q, k, v, do = _rounded(((B, H, SQ, D), (B, Hk, SK, D), (B, Hk, SK, D), (B, H, SQ, D)), 12, dt)
+    o1, _ = orc.fwd(q, k, v, scale, causal, wl, -1, sc)
+    rng = np.random.default_rng(13)
+    o2 = (o1 + rng.standard_normal(o1.shape)).astype(np.float32)
+    delta = o2.astype(np.float64) - o1.astype(np.float64)
+    g1 = orc.bwd(q, k, v, do, scale, causal, wl, -1, sc, model=model, stored_o=o1)
+    g2 = orc.bwd(q, k, v, do, scale, causal, wl, -1, sc, model=model, stored_o=o2)
+    p, deriv = _np_probs(q, k, scale, causal, wl, -1, sc)
+    dD = (do.astype(np.float64) * delta).sum(-1)                 # [B,H,SQ]
+    dds = -p * dD[..., None] * deriv                              # [B,H,SQ,SK]
+    kk = np.repeat(k, H // Hk, axis=1).astype(np.float64)
+    want_dq = scale * np.einsum("bhij,bhjd->bhid", dds, kk)
+    want_dk = (scale * np.einsum("bhij,bhid->bhjd", dds, q.astype(np.float64))
+               ).reshape(B, Hk, H // Hk, SK, D).sum(2)
+    assert np.array_equal(g1[2], g2[2])
+    tol = 1e-9 if model is None else 2 * {"f16": 2.0 ** -11, "bf16": 2.0 ** -8}[dt]  # measured 0.5u
+    assert orc.rel_rms(g2[0] - g1[0], want_dq) <= tol
+    assert orc.rel_rms(g2[1] - g1[1], want_dk) <= tol
+    if model is None:   # D from the forward's own O: the stored-O form equals the exact gradients
+        ex = orc.bwd(q, k, v, do, scale, causal, wl, -1, sc)
+        for a, b in zip(g1, ex):
+            assert orc.rel_rms(a, b) <= 1e-6
+
+
+@pytest.mark.parametrize("causal,wl,wr,sc", [(False, -1, -1, 0.0), (True, -1, -1, 5.0),
+                                             (False, 6, 3, 0.0)])
+def test_bwd_model_floor_scales_with_unit_roundoff(causal, wl, wr, sc):
+    """The model differs from the exact gradients only by roundings to the dtype, so its
+    distance (the floor) is a fraction of the unit roundoff u (2^-11 fp16, 2^-8 bf16) and the
+    bf16 floor is about 8x the fp16 one on the same inputs. A dropped term would make the floor
+    O(1); a rounding to the wrong dtype would make the ratio 1 (or 1/8); no rounding at all
+    would make the floor ~1e-16."""
+    B, H, Hk, SQ, SK, D = 1, 4, 2, 48, 64, 32
+    q, k, v, do = _rounded(((B, H, SQ, D), (B, Hk, SK, D), (B, Hk, SK, D), (B, H, SQ, D)), 14, "f16")
+    ex = orc.bwd(q, k, v, do, 0.3, causal, wl, wr, sc)
+    floor = {}
+    for dt, u in (("f16", 2.0 ** -11), ("bf16", 2.0 ** -8)):
+        md = orc.bwd(q, k, v, do, 0.3, causal, wl, wr, sc, model=dt)
+        floor[dt] = [orc.rel_rms(a, b) for a, b in zip(md, ex)]
+        for f in floor[dt]:
+            assert 0.2 * u <= f <= 1.5 * u, (dt, floor[dt])
+    for f16, bf16 in zip(floor["f16"], floor["bf16"]):
+        assert 5.0 <= bf16 / f16 <= 12.0, (floor["f16"], floor["bf16"])
