@@ -15,7 +15,9 @@
 //     (with their LSE/D rows) of every q head sharing the kv head, in a fixed order:
 //     S = Q.K^T and dP = dO.V^T put queries 4g..4g+3 of each 16-query block in lane (key, g),
 //     the B operands of dV^T += dO^T.(z*P) and dK^T += Q^T.dS.
-// Softcap uses tanhf (fp32 needs its accuracy).
+// Softcap uses tanhf (fp32 needs its accuracy). Kernel widths 64, 128 and 256 serve every head
+// dim p.D that is a multiple of 8: 16-byte chunks past it are not loaded (zeros) and gradient
+// columns past it are not stored.
 #include "attn_device.hpp"
 #include "bwd_common.hpp"
 #include "status.hpp"
@@ -77,7 +79,7 @@ bwd_dq_f32_kernel(FableBwdParams p, int nqt) {
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
   const int kvh = h / p.gqa;
   const BwdSeq sq = bwd_seq(p, b);
-  const int SQ = sq.SQ, SK = sq.SK, delta = SK - SQ;
+  const int SQ = sq.SQ, SK = sq.SK, delta = SK - SQ, HDr = p.D;
   const int qb = qt * C::BQ;
   if (qb >= SQ) return;
 
@@ -103,8 +105,8 @@ bwd_dq_f32_kernel(FableBwdParams p, int nqt) {
 #pragma unroll
   for (int u = 0; u < C::NQ / 4; u++) {
     f32x4 a = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, d = a;
-    if (qi < SQ) {
-      const int c = g * C::NQ + 4 * u;
+    const int c = g * C::NQ + 4 * u;
+    if (qi < SQ && c < HDr) {
       a = *(const f32x4*)(Qg + (long long)qi * p.qs.s + c);
       d = *(const f32x4*)(dOg + (long long)qi * p.dos.s + c);
       const f32x4 o = *(const f32x4*)(Og + (long long)qi * p.os.s + c);
@@ -139,7 +141,7 @@ bwd_dq_f32_kernel(FableBwdParams p, int nqt) {
     for (int j = 0; j < C::KJ; j++) {
       const int r = kb + lrow + j * C::RSTEP;
       ldk[j] = ldv[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (r < SK) {
+      if (r < SK && lcol < HDr) {
         ldk[j] = *(const f32x4*)(Kg + (long long)r * p.ks.s + lcol);
         ldv[j] = *(const f32x4*)(Vg + (long long)r * p.vs.s + lcol);
       }
@@ -211,7 +213,8 @@ bwd_dq_f32_kernel(FableBwdParams p, int nqt) {
   if (qi < SQ) {
     float* row = dQg + (long long)qi * p.dqs.s + 4 * g;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++) *(f32x4*)(row + 16 * db) = dqacc[db] * p.scale;
+    for (int db = 0; db < C::NDB; db++)
+      if (16 * db + 4 * g < HDr) *(f32x4*)(row + 16 * db) = dqacc[db] * p.scale;
   }
 }
 
@@ -248,7 +251,7 @@ bwd_dkdv_f32_kernel(FableBwdParams p, int nkt) {
   const int kt = w2 % nkt, zh = w2 / nkt;
   const int kvh = zh % p.Hk, b = zh / p.Hk;
   const BwdSeq sq = bwd_seq(p, b);
-  const int SQ = sq.SQ, SK = sq.SK, delta = SK - SQ;
+  const int SQ = sq.SQ, SK = sq.SK, delta = SK - SQ, HDr = p.D;
   const int kb0 = kt * C::BK;
   if (kb0 >= SK) return;
 
@@ -261,7 +264,7 @@ bwd_dkdv_f32_kernel(FableBwdParams p, int nkt) {
 #pragma unroll
   for (int u = 0; u < C::NQ / 4; u++) {
     f32x4 a = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, v = a;
-    if (key < SK) {
+    if (key < SK && g * C::NQ + 4 * u < HDr) {
       a = *(const f32x4*)(Kg + (long long)key * p.ks.s + g * C::NQ + 4 * u);
       v = *(const f32x4*)(Vg + (long long)key * p.vs.s + g * C::NQ + 4 * u);
     }
@@ -297,7 +300,7 @@ bwd_dkdv_f32_kernel(FableBwdParams p, int nkt) {
     for (int j = 0; j < C::QJ; j++) {
       const int q = qt0 + lrow + j * C::RSTEP;
       ldq[j] = ldd[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (q < SQ) {
+      if (q < SQ && lcol < HDr) {
         ldq[j] = *(const f32x4*)(Qh + (long long)q * p.qs.s + lcol);
         ldd[j] = *(const f32x4*)(dOh + (long long)q * p.dos.s + lcol);
       }
@@ -398,10 +401,11 @@ bwd_dkdv_f32_kernel(FableBwdParams p, int nkt) {
     float* dkrow = (float*)p.dK + (long long)b * p.dks.b + (sq.ko + key) * p.dks.s + (long long)kvh * p.dks.h + dbase + 4 * g;
     float* dvrow = (float*)p.dV + (long long)b * p.dvs.b + (sq.ko + key) * p.dvs.s + (long long)kvh * p.dvs.h + dbase + 4 * g;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++) {
-      *(f32x4*)(dkrow + 16 * db) = dkacc[db] * p.scale;
-      *(f32x4*)(dvrow + 16 * db) = dvacc[db];
-    }
+    for (int db = 0; db < C::NDB; db++)
+      if (dbase + 16 * db + 4 * g < HDr) {
+        *(f32x4*)(dkrow + 16 * db) = dkacc[db] * p.scale;
+        *(f32x4*)(dvrow + 16 * db) = dvacc[db];
+      }
   }
 }
 
@@ -434,13 +438,13 @@ static int launch_bwd_f32_1(const FableBwdParams& p, hipStream_t st) {
   return feat ? launch_bwd_f32_2<CQ, CKV, false, true, false>(p, st) : launch_bwd_f32_2<CQ, CKV, false, false, false>(p, st);
 }
 
+// every head dim that is a multiple of 8 up to 256, in the kernels of width 64, 128 or 256
 int launch_bwd_f32(const FableBwdParams& p, hipStream_t st) {
-  switch (p.D) {
-    case 64: return launch_bwd_f32_1<F32BwdQCfg<64, 64, 8, 2>, F32BwdKVCfg<64, 64, 8, 2>>(p, st);
-    case 128: return launch_bwd_f32_1<F32BwdQCfg<128, 64, 8, 2>, F32BwdKVCfg<128, 32, 8, 2>>(p, st);
-    case 256: return launch_bwd_f32_1<F32BwdQCfg<256, 32, 4, 1>, F32BwdKVCfg<256, 32, 4, 1, 2>>(p, st);
-    default: return fail(FA_ERR_HEADDIM, "fable_attn_bwd: head_dim=%d has no fp32 kernel (64, 128, 256)", p.D);
-  }
+  if (p.D <= 0 || p.D > 256 || p.D % 8)
+    return fail(FA_ERR_HEADDIM, "fable_attn_bwd: head_dim=%d has no fp32 kernel (multiples of 8 up to 256)", p.D);
+  if (p.D <= 64) return launch_bwd_f32_1<F32BwdQCfg<64, 64, 8, 2>, F32BwdKVCfg<64, 64, 8, 2>>(p, st);
+  if (p.D <= 128) return launch_bwd_f32_1<F32BwdQCfg<128, 64, 8, 2>, F32BwdKVCfg<128, 32, 8, 2>>(p, st);
+  return launch_bwd_f32_1<F32BwdQCfg<256, 32, 4, 1>, F32BwdKVCfg<256, 32, 4, 1, 2>>(p, st);
 }
 
 }  // namespace fa

@@ -365,7 +365,14 @@ __global__ __launch_bounds__(256) void dec_partial_kernel(FableDecParams p, int 
 // lg*HD/4 + t as the B operand of S^T = K . Q^T, whose A operand is loaded straight from the
 // paged cache (16 bytes of one key row per lane); P^T is the B operand of O^T = V^T . P^T,
 // whose A operand is one float per lane (V[key 16kb + 4lg + j][16db + lh]), read from the cache
-// as well (four 64-byte row segments per load). Rotation of q stays exact in fp32.
+// as well (four 64-byte row segments per load). Rotation of q stays exact in fp32. Kernel
+// widths HD = 64, 128, 256 serve every head dim p.HD that is a multiple of 8: rows are p.HD
+// floats apart and the partial record holds the p.HD real columns. Columns past p.HD are read
+// at a clamped column of the same row (always in bounds, no branch): for K the product meets
+// q columns that are zero there, and for V it only fills O^T rows past p.HD, which are never
+// stored. (Per-load branches here raised the kernel's scalar registers past the file and the
+// 256-wide alibi variant then computed wrong logits; the clamped form keeps the register use
+// of the full-width kernel.)
 template <int HD, bool FEAT>
 __global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, int page_shift, int ngrp, int append) {
   constexpr int NQ = HD / 4;    // S^T contraction steps (q floats per lane)
@@ -382,19 +389,20 @@ __global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, 
   const int kvh = blockIdx.x / ngrp, hgi = blockIdx.x % ngrp;
   const int h0 = kvh * p.gqa + 16 * hgi, hg = min(16, p.gqa - 16 * hgi);
   const int sp = blockIdx.z;
-  const int NKV = p.NH / p.gqa;
+  const int NKV = p.NH / p.gqa, HDr = p.HD;
   const DecRange rg = dec_range(p, b, tk, sp, append);
 
-  const float* qg = (const float*)p.q + ((long long)(b * p.nq + tk) * p.NH + h0) * HD;
+  const float* qg = (const float*)p.q + ((long long)(b * p.nq + tk) * p.NH + h0) * HDr;
   for (int i = tid; i < 16 * NQ; i += 256) {
     const int g = i / NQ, c = i % NQ;
-    const f32x4 v = *(const f32x4*)(qg + (long long)min(g, hg - 1) * HD + 4 * c);
+    f32x4 v = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (g < hg && 4 * c < HDr) v = *(const f32x4*)(qg + (long long)g * HDr + 4 * c);
 #pragma unroll
-    for (int e = 0; e < 4; e++) qsh[g][4 * c + e] = g < hg ? v[e] : 0.0f;
+    for (int e = 0; e < 4; e++) qsh[g][4 * c + e] = v[e];
   }
   __syncthreads();
   if (p.rotary) {
-    const int rdim = p.rotary_dim > 0 ? p.rotary_dim : HD, half = rdim / 2;
+    const int rdim = p.rotary_dim > 0 ? p.rotary_dim : HDr, half = rdim / 2;
     const int rp = (p.rotary_pos ? p.rotary_pos[b] : p.ctx_len[b]) + tk;
     for (int i = tid; i < hg * half; i += 256) {
       const int g = i / half, j = i % half;
@@ -423,7 +431,7 @@ __global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, 
   const int pmask = p.page - 1;
   const int last = rg.end - 1;
   auto row_off = [&](int key) -> long long {
-    return (((long long)bt[key >> page_shift] * p.page + (key & pmask)) * NKV + kvh) * HD;
+    return (((long long)bt[key >> page_shift] * p.page + (key & pmask)) * NKV + kvh) * HDr;
   };
   constexpr int kStep = kDecChunk * kDecWaves;
   for (int kc0 = rg.start + kDecChunk * wave; kc0 < rg.end; kc0 += kStep) {
@@ -431,11 +439,11 @@ __global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, 
     f32x4 s[2];
 #pragma unroll
     for (int kb = 0; kb < 2; kb++) {
-      const float* kr = Kc + row_off(min(kc0 + 16 * kb + lh, last)) + lg * NQ;
+      const float* kr = Kc + row_off(min(kc0 + 16 * kb + lh, last));
       s[kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int u = 0; u < NQ / 4; u++) {
-        const f32x4 a = *(const f32x4*)(kr + 4 * u);
+        const f32x4 a = *(const f32x4*)(kr + min(lg * NQ + 4 * u, HDr - 4));
 #pragma unroll
         for (int e = 0; e < 4; e++) s[kb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[e], qreg[4 * u + e], s[kb], 0, 0, 0);
       }
@@ -481,10 +489,10 @@ __global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, 
     for (int kb = 0; kb < 2; kb++)
 #pragma unroll
       for (int r = 0; r < 4; r++) {
-        const float* vr = Vc + row_off(min(kc0 + 16 * kb + 4 * lg + r, last)) + lh;
+        const float* vr = Vc + row_off(min(kc0 + 16 * kb + 4 * lg + r, last));
 #pragma unroll
         for (int db = 0; db < NDB; db++)
-          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[16 * db], s[kb][r], oacc[db], 0, 0, 0);
+          oacc[db] = __builtin_amdgcn_mfma_f32_16x16x4f32(vr[min(16 * db + lh, HDr - 1)], s[kb][r], oacc[db], 0, 0, 0);
       }
   }
 
@@ -501,8 +509,8 @@ __global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, 
 #pragma unroll
     for (int r = 0; r < 4; r++) red_o[(wave * 16 + lh) * HD + 16 * db + 4 * lg + r] = oacc[db][r];
   __syncthreads();
-  for (int i = tid; i < hg * HD; i += 256) {
-    const int g = i / HD, d = i % HD;
+  for (int i = tid; i < hg * HDr; i += 256) {
+    const int g = i / HDr, d = i % HDr;
     float gm = -INFINITY;
 #pragma unroll
     for (int w = 0; w < kDecWaves; w++) gm = fmaxf(gm, red_m[w][g]);
@@ -515,7 +523,7 @@ __global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, 
         acc += f * red_o[(w * 16 + g) * HD + d];
       }
     }
-    float* out = p.scratch + (((long long)(b * p.nq + tk) * p.NH + h0 + g) * p.nsplit + sp) * (HD + 2);
+    float* out = p.scratch + (((long long)(b * p.nq + tk) * p.NH + h0 + g) * p.nsplit + sp) * (HDr + 2);
     if (d == 0) {
       out[0] = gm;
       out[1] = l;
@@ -625,16 +633,15 @@ static int launch_dec(const FableDecParams& p, hipStream_t st, const void* nk, c
 // fp16/bf16: every head dim that is a multiple of 8 up to 256 runs in the kernel of the next
 // multiple of 32 (64 at least: the K slice swizzle needs 8 chunks per row) with zero columns
 // past it. The loads skip those columns' bytes, so HBM traffic is that of the real head dim.
-// fp32 has kernels for 64, 128 and 256 exactly.
+// fp32 runs in kernels of width 64, 128 and 256, the same way.
 template <typename T>
 static int dec_dispatch(const FableDecParams& p, hipStream_t st, const void* nk, const void* nv) {
   constexpr bool f32 = std::is_same<T, float>::value;
-  if (p.HD <= 0 || p.HD > 256 || p.HD % 8 || (f32 && p.HD != 64 && p.HD != 128 && p.HD != 256))
-    return fail(FA_ERR_HEADDIM, "fable_attn_dec: head_dim=%d has no kernel (%s)", p.HD,
-                f32 ? "64, 128, 256 for fp32" : "multiples of 8 up to 256");
+  if (p.HD <= 0 || p.HD > 256 || p.HD % 8)
+    return fail(FA_ERR_HEADDIM, "fable_attn_dec: head_dim=%d has no kernel (multiples of 8 up to 256)", p.HD);
   if constexpr (f32) {
-    if (p.HD == 64) return launch_dec<T, 64>(p, st, nk, nv);
-    if (p.HD == 128) return launch_dec<T, 128>(p, st, nk, nv);
+    if (p.HD <= 64) return launch_dec<T, 64>(p, st, nk, nv);
+    if (p.HD <= 128) return launch_dec<T, 128>(p, st, nk, nv);
     return launch_dec<T, 256>(p, st, nk, nv);
   } else {
     switch (p.HD <= 64 ? 2 : (p.HD + 31) / 32) {
@@ -682,10 +689,16 @@ extern "C" int fa_decode_num_splits(int batch, int nq, int NH, int gqa, int64_t 
   return best;
 }
 
+// Whether a call reads or writes p.scratch: with one split the fp16/bf16 partial kernel writes the
+// output and LSE itself and no combine runs; fp32 always combines through the scratch.
+static bool dec_uses_scratch(const FableDecParams& p, int dtype) { return p.nsplit != 1 || dtype == FA_F32; }
+
 extern "C" int fable_attn_dec(FableDecParams p, int dtype, void* stream, const void* new_k, const void* new_v) {
   using namespace fa;
-  if (!p.q || !p.Kc || !p.Vc || !p.block_table || !p.o || !p.scratch || !p.ctx_len)
+  if (!p.q || !p.Kc || !p.Vc || !p.block_table || !p.o || !p.ctx_len)
     return fail(FA_ERR_ARG, "fable_attn_dec: null pointer");
+  if (!p.scratch && dec_uses_scratch(p, dtype))
+    return fail(FA_ERR_ARG, "fable_attn_dec: null scratch (needed unless nsplit == 1 with fp16/bf16)");
   return dec_checked(p, dtype, stream, new_k, new_v);
 }
 
@@ -743,8 +756,12 @@ extern "C" int fable_attn_dec_noalloc(FableDecParams p, int dtype, void* stream,
   if (!p.q || !p.Kc || !p.Vc || !p.block_table || !p.o || !p.ctx_len)
     return fail(FA_ERR_ARG, "fable_attn_dec_noalloc: null pointer");
   if (p.batch <= 0) return FA_OK;
+  if (p.NH <= 0) return fail(FA_ERR_ARG, "fable_attn_dec_noalloc: NH=%d", p.NH);
+  if (p.nsplit < 1 || p.nsplit > 512) return fail(FA_ERR_ARG, "fable_attn_dec_noalloc: nsplit=%d", p.nsplit);
+  if (p.HD <= 0) return fail(FA_ERR_HEADDIM, "fable_attn_dec_noalloc: head_dim=%d", p.HD);
+  // one fp16/bf16 split never touches the array: no size limit then
   const long long need = (long long)p.batch * (p.nq < 1 ? 1 : p.nq) * p.NH * p.nsplit * (p.HD + 2);
-  if (p.NH <= 0 || p.nsplit < 1 || p.HD <= 0 || need > kDecScratchFloats)
+  if (dec_uses_scratch(p, dtype) && need > kDecScratchFloats)
     return fail(FA_ERR_ARG, "fable_attn_dec_noalloc: batch*nq*NH*nsplit*(HD+2) = %lld floats of split "
                             "partials exceed the fixed %lld (lower nsplit, or use fable_attn_dec with a "
                             "caller-allocated scratch)", need, kDecScratchFloats);

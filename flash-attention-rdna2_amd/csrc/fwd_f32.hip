@@ -16,6 +16,10 @@
 //    row sum reduce over the four lane groups. Softcap uses tanhf (fp32 needs its accuracy).
 //  * K and V tiles are double-buffered in LDS with rows padded by 16 bytes; one barrier per
 //    tile; tiles outside the mask are never loaded.
+//  * kernel widths 64, 128 and 256: a head dim p.HD below the width (any multiple of 8) runs
+//    with the columns past it zero. Each 16-byte chunk of a row lies wholly inside or outside
+//    the head dim; outside ones are not loaded (zeros in registers and LDS, so they add nothing
+//    to q.k, and the O columns they produce are not stored).
 #include "attn_device.hpp"
 #include "fwd_common.hpp"
 #include "status.hpp"
@@ -68,7 +72,7 @@ fwd_f32_kernel(FableFwdParams p, int nqt) {
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
   const int kvh = h / p.gqa;
   const SeqView sv = seq_view(p, z, h);
-  const int SQ = sv.SQ, SK = sv.SK;
+  const int SQ = sv.SQ, SK = sv.SK, HDr = p.HD;
   const int qb = qt * C::BR;
   if (qb >= SQ) return;
   const int delta = SK - SQ;
@@ -93,7 +97,7 @@ fwd_f32_kernel(FableFwdParams p, int nqt) {
 #pragma unroll
   for (int u = 0; u < C::NQ / 4; u++) {
     f32x4 v = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    if (qi < SQ) v = *(const f32x4*)(Qg + (long long)qi * p.sQ.s + g * C::NQ + 4 * u);
+    if (qi < SQ && g * C::NQ + 4 * u < HDr) v = *(const f32x4*)(Qg + (long long)qi * p.sQ.s + g * C::NQ + 4 * u);
 #pragma unroll
     for (int e = 0; e < 4; e++) qreg[4 * u + e] = v[e];
   }
@@ -115,7 +119,7 @@ fwd_f32_kernel(FableFwdParams p, int nqt) {
     for (int j = 0; j < C::KJ; j++) {
       const int r = kb + lrow + j * C::RSTEP;
       ldk[j] = ldv[j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      if (r < SK) {
+      if (r < SK && lcol < HDr) {
         ldk[j] = *(const f32x4*)(Kg + (long long)r * p.sK.s + lcol);
         ldv[j] = *(const f32x4*)(Vg + (long long)r * p.sV.s + lcol);
       }
@@ -216,7 +220,8 @@ fwd_f32_kernel(FableFwdParams p, int nqt) {
   if (qi < SQ) {
     float* orow = Og + (long long)qi * p.sO.s + 4 * g;
 #pragma unroll
-    for (int db = 0; db < C::NDB; db++) *(f32x4*)(orow + 16 * db) = oacc[db] * inv;
+    for (int db = 0; db < C::NDB; db++)
+      if (16 * db + 4 * g < HDr) *(f32x4*)(orow + 16 * db) = oacc[db] * inv;
     if (p.LSE && g == 0) p.LSE[sv.lse0 + qi] = l_tot > 0.0f ? m_run * kLn2 + logf(l_tot) : -INFINITY;
   }
 }
@@ -243,13 +248,13 @@ static int launch_f32(const FableFwdParams& p, hipStream_t st) {
   return launch_status("fable_attn_fwd");
 }
 
+// every head dim that is a multiple of 8 up to 256, in the kernel of width 64, 128 or 256
 int launch_fwd_f32(const FableFwdParams& p, hipStream_t st) {
-  switch (p.HD) {
-    case 64: return launch_f32<F32Cfg<64, 64, 8, 2>>(p, st);
-    case 128: return launch_f32<F32Cfg<128, 64, 8, 2>>(p, st);
-    case 256: return launch_f32<F32Cfg<256, 32, 8, 2>>(p, st);
-    default: return fail(FA_ERR_HEADDIM, "fable_attn_fwd: head_dim=%d has no fp32 kernel (64, 128, 256)", p.HD);
-  }
+  if (p.HD <= 0 || p.HD > 256 || p.HD % 8)
+    return fail(FA_ERR_HEADDIM, "fable_attn_fwd: head_dim=%d has no fp32 kernel (multiples of 8 up to 256)", p.HD);
+  if (p.HD <= 64) return launch_f32<F32Cfg<64, 64, 8, 2>>(p, st);
+  if (p.HD <= 128) return launch_f32<F32Cfg<128, 64, 8, 2>>(p, st);
+  return launch_f32<F32Cfg<256, 32, 8, 2>>(p, st);
 }
 
 }  // namespace fa

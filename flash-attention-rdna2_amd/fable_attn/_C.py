@@ -373,12 +373,15 @@ def dec(q, k_cache, v_cache, block_table, cache_seqlens, new_k, new_v, rotary_co
     ctx_bound = block_table.shape[1] * page
     nsplit = int(_L.fa_decode_num_splits(B, NQ, Hq, Hq // Hk, ctx_bound, int(num_splits or 0)))
     out = torch.empty((B, NQ, Hq, D), dtype=q.dtype, device=q.device)
-    scratch = torch.empty((B * NQ * Hq * nsplit * (D + 2),), dtype=torch.float32, device=q.device)
+    # one fp16/bf16 split writes out (and lse) from the partial kernel: no scratch then
+    scratch = (torch.empty((B * NQ * Hq * nsplit * (D + 2),), dtype=torch.float32, device=q.device)
+               if nsplit > 1 or q.dtype == torch.float32 else None)
     lse = (torch.empty((B, NQ, Hq), dtype=torch.float32, device=q.device) if return_lse
            else torch.empty((0,), dtype=torch.float32, device=q.device))
     p = FableDecParams()
     p.q, p.Kc, p.Vc = q.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr()
-    p.block_table, p.o, p.scratch = block_table.data_ptr(), out.data_ptr(), scratch.data_ptr()
+    p.block_table, p.o = block_table.data_ptr(), out.data_ptr()
+    p.scratch = scratch.data_ptr() if scratch is not None else None
     p.ctx_len = cache_seqlens.data_ptr()
     p.cos = rotary_cos.data_ptr() if rotary_cos is not None else None
     p.sin = rotary_sin.data_ptr() if rotary_sin is not None else None

@@ -27,12 +27,11 @@ import torch
 
 from . import _C
 
-# Head dims the kernels take as they are: fp16/bf16 every multiple of 8 up to 256 (rows move in
-# 16-byte accesses; the kernels zero the columns up to their own width), fp32 64, 128 and 256.
-# Any other head dim is zero-padded to the next one it may use: zero columns change neither q.k
-# nor the kept output columns.
+# Head dims the kernels take as they are: every multiple of 8 up to 256, in every dtype (rows
+# move in 16-byte accesses; the kernels zero the columns up to their own width). Any other head
+# dim is zero-padded to the next multiple of 8: zero columns change neither q.k nor the kept
+# output columns.
 MAX_HEAD_DIM = 256
-F32_HEAD_DIMS = (64, 128, 256)
 _DTYPES = (torch.float16, torch.bfloat16, torch.float32)
 
 
@@ -98,10 +97,9 @@ class _Spec:
 
 def _kernel_width(d, dtype):
     """The head dim a call of head dim d runs at (None above MAX_HEAD_DIM)."""
+    del dtype  # (every dtype has kernels for every multiple of 8)
     if d > MAX_HEAD_DIM:
         return None
-    if dtype == torch.float32:
-        return next(w for w in F32_HEAD_DIMS if w >= d)
     return -(-d // 8) * 8
 
 
@@ -345,7 +343,10 @@ def _pages_as_packed(k_cache, v_cache, block_table, cu_seqlens_k, seqused_k):
     """Paged K/V of a varlen prefill as a packed batch without a host round trip: every
     sequence's block-table row is gathered whole (max_blocks * page rows per sequence, one
     device gather), so sequence b starts at row b * max_blocks * page, and its true length
-    becomes seqused_k. Returns (k, v, cu_k, seqused_k, max_seqlen_k)."""
+    becomes seqused_k. Table entries past a sequence's ceil(len / page) pages are not read:
+    serving code leaves -1, stale or out-of-range values there, so they are replaced by page 0
+    on the device before the gather (the rows they bring are past seqused_k and never attended).
+    Returns (k, v, cu_k, seqused_k, max_seqlen_k)."""
     if k_cache.dim() != 4 or v_cache.dim() != 4:
         raise ValueError(
             "fable_attn: with block_table, k and v must be paged "
@@ -355,12 +356,17 @@ def _pages_as_packed(k_cache, v_cache, block_table, cu_seqlens_k, seqused_k):
         raise ValueError(f"fable_attn: block_table must be (batch, max_blocks), got "
                          f"{tuple(block_table.shape)} for batch={nseq}")
     dev = k_cache.device
+    page = k_cache.shape[1]
     bt = block_table.to(device=dev, dtype=torch.long)
-    span = bt.shape[1] * k_cache.shape[1]
+    span = bt.shape[1] * page
+    used = _as_index(seqused_k if seqused_k is not None
+                     else cu_seqlens_k[1:] - cu_seqlens_k[:-1], dev)
+    live = (torch.arange(bt.shape[1], device=dev)[None, :]
+            < ((used.to(torch.long) + page - 1) // page)[:, None])
+    bt = torch.where(live, bt, torch.zeros_like(bt))
     flat = lambda c: c[bt.reshape(-1)].reshape(nseq * span, c.shape[2], c.shape[3])
     cu = torch.arange(nseq + 1, device=dev, dtype=torch.int32) * span
-    used = seqused_k if seqused_k is not None else cu_seqlens_k[1:] - cu_seqlens_k[:-1]
-    return flat(k_cache), flat(v_cache), cu, _as_index(used, dev), span
+    return flat(k_cache), flat(v_cache), cu, used, span
 
 
 def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, max_seqlen_k,
@@ -543,7 +549,7 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None,
         if appending:
             raise NotImplementedError(
                 f"fable_attn: appending k/v needs a head_dim the kernels take as it is (a multiple "
-                f"of 8 for fp16/bf16, 64/128/256 for fp32), got {q.shape[-1]}")
+                f"of 8), got {q.shape[-1]}")
         keep = keep if keep is not None else vc.shape[-1]
         q, kc, vc = _with_width(q, w), _with_width(kc, w), _with_width(vc, w)
     _, wl, _ = _map_window(True, window_size)
@@ -577,10 +583,12 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None,
 def _kvcache_packed_q(q, k_cache, v_cache, k, qv, cu_seqlens_q, max_seqlen_q, return_lse,
                       **kw):
     """flash_attn_with_kvcache with packed queries q (total_q, nheads, d) and cu_seqlens_q
-    (batch+1): the queries are scattered into a (batch, max_seqlen_q, nheads, d) block on the
-    device (no per-sequence loop or host round trip beyond max_seqlen_q when it is not given),
+    (batch+1): the queries are scattered into a (batch, width, nheads, d) block on the device,
     decoded in one call (row t of sequence b at cache_seqlens[b] + t; padding rows are
-    computed and dropped) and gathered back to (total_q, nheads, d)."""
+    computed and dropped) and gathered back to (total_q, nheads, d). width is the longest
+    sequence, read back once from the device (the reference reads cu_seqlens_q on the host and
+    loops over the sequences, :636-660); a max_seqlen_q below it raises ValueError, since rows
+    past it would land in the next sequence's slots."""
     if k is not None:
         raise NotImplementedError(
             "fable_attn: appending k/v with cu_seqlens_q (a ragged append) is not supported; "
@@ -591,7 +599,10 @@ def _kvcache_packed_q(q, k_cache, v_cache, k, qv, cu_seqlens_q, max_seqlen_q, re
     dev = q.device
     cu = _as_index(cu_seqlens_q, dev).long()
     nseq, total = cu.numel() - 1, q.shape[0]
-    width = int(max_seqlen_q) if max_seqlen_q is not None else int((cu[1:] - cu[:-1]).max())
+    width = int((cu[1:] - cu[:-1]).max()) if nseq > 0 else 0
+    if max_seqlen_q is not None and width > int(max_seqlen_q):
+        raise ValueError(f"fable_attn: max_seqlen_q={int(max_seqlen_q)} is below the longest "
+                         f"sequence in cu_seqlens_q ({width})")
     row = torch.arange(total, device=dev)
     seq = torch.searchsorted(cu[1:], row, right=True)           # sequence of each packed row
     slot = seq * width + (row - cu[seq])                         # its row in the padded block

@@ -124,11 +124,10 @@ def test_forward_argument_mapping(fake):
 
 
 def test_head_dim_padding_and_slicing(fake):
-    """fp16/bf16 head dims that are multiples of 8 go to the kernels as they are; others are
-    zero-padded to the next multiple of 8, fp32 ones to 64/128/256; the scale and the output
-    keep the real head dim."""
+    """Head dims that are multiples of 8 go to the kernels as they are (every dtype); others
+    are zero-padded to the next multiple of 8; the scale and the output keep the real head dim."""
     for D, dt, width in ((80, torch.float16, 80), (40, torch.bfloat16, 40), (100, torch.float16, 104),
-                         (80, torch.float32, 128), (24, torch.float32, 64)):
+                         (80, torch.float32, 80), (24, torch.float32, 24), (20, torch.float32, 24)):
         q = rnd(1, 16, 2, D, dt=dt)
         out = fai.flash_attn_func(q, q, q)
         assert fake.calls[-1][1]["shape"][-1] == width, (D, dt)
@@ -309,6 +308,22 @@ def test_paged_varlen_gathers_without_host_lengths(fake):
     assert used.tolist() == [20, 25]
 
 
+def test_paged_varlen_ignores_table_padding():
+    """Block-table entries past a sequence's pages (serving code leaves -1, stale or
+    out-of-range values there) are not gathered: the packed K/V rows of each sequence's real
+    pages are those of the clean table, and no index error arises."""
+    kc = torch.arange(6 * 4 * 1 * 8, dtype=torch.float32).view(6, 4, 1, 8)   # 6 pages of 4 rows
+    cu_k = torch.tensor([0, 5, 8], dtype=torch.int32)                          # 2 and 1 pages used
+    clean = torch.tensor([[3, 1, 0], [5, 0, 0]], dtype=torch.int32)
+    dirty = torch.tensor([[3, 1, -1], [5, 6 + 7, -1]], dtype=torch.int32)
+    k1, _, cu1, used1, span1 = fai._pages_as_packed(kc, kc, clean, cu_k, None)
+    k2, _, cu2, used2, span2 = fai._pages_as_packed(kc, kc, dirty, cu_k, None)
+    assert span1 == span2 == 12 and torch.equal(cu1, cu2) and used2.tolist() == [5, 3]
+    for z, n in enumerate((5, 3)):
+        assert torch.equal(k2[z * 12:z * 12 + n], k1[z * 12:z * 12 + n])
+    assert torch.equal(k2[0:4], kc[3]) and torch.equal(k2[4:5], kc[1, :1])
+
+
 def test_kvcache_packed_queries_one_call(fake):
     """cu_seqlens_q: the packed queries go to the kernel as one (batch, max_seqlen_q) block
     and come back packed, in one decode call."""
@@ -322,6 +337,14 @@ def test_kvcache_packed_queries_one_call(fake):
     decs = [c for c in fake.calls if c[0] == "dec"]
     assert len(decs) == 1 and decs[0][1]["q"] == (2, 3, 4, 64)
     assert out.shape == (5, 4, 64) and lse.shape == (4, 5)
+    # a max_seqlen_q above the longest sequence pads no further; one below it is refused (its
+    # rows would land in the next sequence's slots)
+    fai.flash_attn_with_kvcache(q, kc, kc, cache_seqlens=torch.tensor([10, 30]), block_table=bt,
+                                cu_seqlens_q=cu, max_seqlen_q=8)
+    assert fake.calls[-1][1]["q"] == (2, 3, 4, 64)
+    with pytest.raises(ValueError, match="max_seqlen_q"):
+        fai.flash_attn_with_kvcache(q, kc, kc, cache_seqlens=torch.tensor([10, 30]),
+                                    block_table=bt, cu_seqlens_q=cu, max_seqlen_q=2)
     with pytest.raises(NotImplementedError):
         fai.flash_attn_with_kvcache(q, kc, kc, k=rnd(5, 2, 64), v=rnd(5, 2, 64), block_table=bt,
                                     cu_seqlens_q=cu, max_seqlen_q=3)

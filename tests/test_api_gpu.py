@@ -75,6 +75,13 @@ def test_paged_varlen_equals_packed():
     paged = flash_attn_varlen_func(q, kp, vp, cu_q, cu_k, max(lens_q), max(lens_k), causal=True,
                                    block_table=bt.cuda())
     assert torch.equal(paged, packed)
+    # table entries past a sequence's pages as serving code leaves them: -1 and out of range
+    pad = torch.tensor([-1, total + 7], dtype=torch.int32)
+    for i in range(len(lens_k)):
+        bt[i, npg[i]:] = pad[i % 2]
+    paged = flash_attn_varlen_func(q, kp, vp, cu_q, cu_k, max(lens_q), max(lens_k), causal=True,
+                                   block_table=bt.cuda())
+    assert torch.equal(paged, packed)
     # and the packed result against the oracle, per sequence
     for i in range(len(lens_q)):
         qi = to_np(q[cq[i]:cq[i + 1]]).transpose(1, 0, 2)[None]

@@ -127,8 +127,8 @@ def test_decode_parity(case, dt):
 
 
 # head dims other than 64/128/256: fp16/bf16 kernels of every width that is a multiple of 32
-# from 64 up, zero columns past the head dim (rows in the cache are the real head dim long), with
-# append and rotary; fp32 has 64/128/256
+# from 64 up, fp32 kernels of width 64, 128 and 256, zero columns past the head dim (rows in the
+# cache are the real head dim long), with append and rotary
 DIM_CASES = [
     ("HD32 append+rotary", 32, 8, 4, [70, 200], -1, 1, True, 0, 2, 0.0, False, 16),
     ("HD80 append+rotary interleaved", 80, 16, 4, [300], -1, 2, True, 0, 1, 0.0, False, 16),
@@ -143,7 +143,7 @@ DIM_CASES = [
 ]
 
 
-@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("dt", ["f16", "bf16", "f32"])
 @pytest.mark.parametrize("case", DIM_CASES, ids=[c[0] for c in DIM_CASES])
 def test_decode_head_dims(case, dt):
     test_decode_parity(case, dt)

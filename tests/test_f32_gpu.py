@@ -4,10 +4,12 @@ dtype FA_F32, through fable_attn._C), against the fp64 oracle on the same inputs
 The reference serves fp32 through separate kernels (kernels/fa_forward.hip:317-400, 440-447;
 backward.hip MODE BW_F32) and gates them at rel_rms 1e-5 (forward, fa_forward_gate.inc:169) and
 1e-4 (backward, backward.hip:734); these tests use the same bounds, LSE within 1e-5 absolute.
-Cases: every head dim, causal bottom-right with SQ != SK both ways (empty rows), GQA, windows,
-softcap, alibi, attention_chunk, dropout (mask bit-compatible with the fp16 path), varlen with
-seqused, ragged tails; backward bitwise reproducible; autograd through flash_attn_func with a
-head dim that the API pads.
+Cases: the kernel widths 64, 128, 256 and head dims below them (16, 40, 80, 112, 160, 224:
+the reference's fp32 head dims run in the next kernel width with zero columns inside the kernel),
+causal bottom-right with SQ != SK both ways (empty rows), GQA, windows, softcap, alibi,
+attention_chunk, dropout (mask bit-compatible with the fp16 path), varlen with seqused, ragged
+tails; backward bitwise reproducible; autograd through flash_attn_func at head dim 80; the
+reference-layout launcher fa_forward_launch at head dim 80.
 """
 import math
 
@@ -33,6 +35,17 @@ CASES = [
     ("D256 causal", 1, 2, 2, 140, 140, 256, True, -1, -1, 0.0, False, 0, 0.0),
     ("D256 full gqa", 1, 4, 2, 64, 90, 256, False, -1, -1, 0.0, False, 0, 0.0),
     ("D128 dropout", 1, 4, 4, 128, 128, 128, True, -1, -1, 0.0, False, 0, 0.2),
+    # head dims below the kernel width (reference fp32 head dims, kernels/fa_forward.hip:443-447,
+    # backward.hip:491-497, 508-516)
+    ("D16 causal gqa", 1, 4, 2, 130, 130, 16, True, -1, -1, 0.0, False, 0, 0.0),
+    ("D40 full tail", 2, 2, 2, 77, 93, 40, False, -1, -1, 0.0, False, 0, 0.0),
+    ("D80 causal softcap", 1, 4, 4, 150, 150, 80, True, -1, -1, 20.0, False, 0, 0.0),
+    ("D112 window alibi", 1, 4, 2, 140, 170, 112, False, 30, 10, 0.0, True, 0, 0.0),
+    ("D160 causal SQ<SK", 1, 2, 2, 90, 160, 160, True, -1, -1, 0.0, False, 0, 0.0),
+    ("D224 causal gqa", 1, 4, 2, 100, 100, 224, True, -1, -1, 0.0, False, 0, 0.0),
+    # the 256-wide feature and dropout kernels
+    ("D256 alibi window", 1, 4, 2, 120, 150, 256, False, 50, 20, 0.0, True, 0, 0.0),
+    ("D192 dropout softcap", 1, 2, 2, 96, 96, 192, True, -1, -1, 15.0, False, 0, 0.15),
 ]
 FWD_ONLY = [("D64 chunk 48", 1, 4, 4, 160, 160, 64, True, -1, -1, 0.0, False, 48, 0.0)]
 
@@ -139,9 +152,9 @@ def test_f32_varlen_forward_backward():
         assert torch.count_nonzero(dk[c + nk:ck[i + 1]]) == 0 and torch.count_nonzero(dv[c + nk:ck[i + 1]]) == 0
 
 
-def test_f32_autograd_padded_head_dim():
-    """flash_attn_func in fp32 with head_dim 80 (padded to 128 by the API): output and
-    gradients against the oracle on the unpadded problem."""
+def test_f32_autograd_head_dim_80():
+    """flash_attn_func in fp32 with head_dim 80 (run by the 128-wide kernels with zero columns
+    past 80; the API passes it as it is): output and gradients against the oracle."""
     import torch
 
     from fable_attn import flash_attn_func
@@ -160,3 +173,42 @@ def test_f32_autograd_padded_head_dim():
     for got, r, gname in ((q.grad, ref[0], "dq"), (k.grad, ref[1], "dk"), (v.grad, ref[2], "dv")):
         e = orc.rel_rms(bhsd(got), r)
         assert e <= GTOL, f"{gname} rel_rms {e:.3e}"
+
+
+def test_f32_reference_launcher_head_dim_80():
+    """fa_forward_launch (the reference's own launcher and struct layout, package/csrc/fa_iface.h)
+    in fp32 at head dim 80, which the reference instantiates (kernels/fa_forward.hip:443-447):
+    one call per batch element as the reference's glue makes them (dispatch.cpp:61-78), LSE of
+    batch element 0 only (the reference layout has no batch stride)."""
+    import ctypes
+
+    import torch
+
+    from fable_attn import _lib
+    lib = _lib.load()
+    B, H, Hk, SQ, SK, D = 2, 4, 2, 120, 150, 80
+    q = gen((B, H, SQ, D), 61, "f32")
+    k = gen((B, Hk, SK, D), 62, "f32")
+    v = gen((B, Hk, SK, D), 63, "f32")
+    qd, kd, vd = _view(q), _view(k), _view(v)
+    out = torch.empty((B, SQ, H, D), dtype=torch.float32, device="cuda").transpose(1, 2)
+    lse = torch.empty((H, SQ), dtype=torch.float32, device="cuda")
+    rs = lambda t: _lib.RefStrides(*t.stride()[:3])
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    for b in range(B):
+        p = _lib.RefFwdParams()
+        p.Q = qd.data_ptr() + b * qd.stride(0) * 4
+        p.K = kd.data_ptr() + b * kd.stride(0) * 4
+        p.V = vd.data_ptr() + b * vd.stride(0) * 4
+        p.O = out.data_ptr() + b * out.stride(0) * 4
+        p.LSE = lse.data_ptr() if b == 0 else None
+        p.sQ, p.sK, p.sV, p.sO = rs(qd), rs(kd), rs(vd), rs(out)
+        p.SQ, p.SK, p.HD, p.NH, p.gqa = SQ, SK, D, H, H // Hk
+        p.scale, p.softcap, p.win_left, p.win_right, p.causal = D ** -0.5, 0.0, -1, 0, 1
+        p.batch = 1
+        assert lib.fa_forward_launch(p, 2, st) == 0, lib.fable_attn_last_error()
+    torch.cuda.synchronize()
+    ro, rl = orc.fwd(q, k, v, D ** -0.5, True)
+    assert orc.rel_rms(to_np(out), ro) <= FTOL
+    le, inf_ok = lse_err(to_np(lse)[None], rl[:1])
+    assert inf_ok and le <= LTOL

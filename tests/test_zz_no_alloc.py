@@ -72,10 +72,52 @@ def test_noalloc_decode_rejects_oversized_partials():
     assert cap == 4 << 20
     q, kc, vc, bt, ctx = _case(1, 8, 8, 128, 16, [32], 5)
     out = torch.zeros_like(q)
-    p = _params(_lib, q, kc, vc, bt, ctx, out, None, 1)
-    p.batch = cap // (8 * 130) + 1        # partials one batch element past the array
     st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    # two splits: partials one batch element past the array (the tensors hold one element; the
+    # size check rejects the call before anything is launched)
+    p = _params(_lib, q, kc, vc, bt, ctx, out, None, 2)
+    p.batch = cap // (8 * 2 * 130) + 1
     assert lib.fable_attn_dec_noalloc(p, 0, st, None, None) == 3
     assert b"exceed" in lib.fable_attn_last_error()
+    # fp32 always combines through the array, one split included
+    p = _params(_lib, q, kc, vc, bt, ctx, out, None, 1)
+    p.batch = cap // (8 * 130) + 1
+    assert lib.fable_attn_dec_noalloc(p, 2, st, None, None) == 3
+    assert b"exceed" in lib.fable_attn_last_error()
+    # a bad head count or split count names itself
+    p = _params(_lib, q, kc, vc, bt, ctx, out, None, 1)
+    p.NH = 0
+    assert lib.fable_attn_dec_noalloc(p, 0, st, None, None) == 3
+    assert b"NH=0" in lib.fable_attn_last_error()
+    p = _params(_lib, q, kc, vc, bt, ctx, out, None, 0)
+    assert lib.fable_attn_dec_noalloc(p, 0, st, None, None) == 3
+    assert b"nsplit=0" in lib.fable_attn_last_error()
     torch.cuda.synchronize()
     assert torch.count_nonzero(out) == 0, "nothing may run after a rejected call"
+
+
+def test_noalloc_single_split_has_no_size_limit():
+    """One fp16 split writes the output from the partial kernel and never touches the array,
+    so a call whose partials would exceed it runs, and equals fable_attn_dec (which needs no
+    scratch either at one split)."""
+    import torch
+
+    from fable_attn import _lib
+    lib = _lib.load()
+    cap = lib.fable_attn_dec_noalloc_max_floats()
+    B, H, Hk, D = 1040, 32, 8, 128
+    assert B * H * (D + 2) > cap
+    print(f"[noalloc] single split B={B}", flush=True)
+    q, kc, vc, bt, ctx = _case(B, H, Hk, D, 16, [20] * B, 7)
+    out_a, out_b = torch.empty_like(q), torch.empty_like(q)
+    st = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    pa = _params(_lib, q, kc, vc, bt, ctx, out_a, None, 1)
+    assert lib.fable_attn_dec(pa, 0, st, None, None) == 0, lib.fable_attn_last_error()
+    pb = _params(_lib, q, kc, vc, bt, ctx, out_b, None, 1)
+    assert lib.fable_attn_dec_noalloc(pb, 0, st, None, None) == 0, lib.fable_attn_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(out_a, out_b) and torch.isfinite(out_b).all()
+    # with two splits fable_attn_dec needs its scratch
+    pa = _params(_lib, q, kc, vc, bt, ctx, out_a, None, 2)
+    assert lib.fable_attn_dec(pa, 0, st, None, None) == 3
+    assert b"scratch" in lib.fable_attn_last_error()
