@@ -2,6 +2,8 @@
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extras fwd,bwd,decode,varlen]
 
+(--extras: fwd = C2 at S=4096/8192 and C1; c2sizes and c1 name those parts alone.)
+
 A step is one pass of the hot path over one batch of synthetic input:
   headline (`value`): BASELINE.json configs[1], causal fp16 forward through flash_attn_func,
   B=1, S=16384, H=32, D=128, q/k/v ~ N(0,1) resident in HBM before timing.
@@ -108,11 +110,12 @@ def bench_fwd(S, steps, warmup, causal=True, H=32, D=128, B=1, dtype="fp16", see
     flops = 4.0 * B * H * S * S * D / (2 if causal else 1)
     per = []
     wall, ev = time_steps(lambda: flash_attn_func(q, k, v, causal=causal), steps, warmup, per, warm_ms)
-    return {"S": S, "H": H, "D": D, "B": B, "causal": causal, "dtype": dtype, "flops": flops,
-            "ms": wall, "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
-            "kernel_tflops": flops / (ev * 1e-3) / 1e12, "kernel_ms_median": _median(per),
-            "tflops_median": flops / (_median(per) * 1e-3) / 1e12,
-            "roofline": roofline("mfma", flops, ev, _fwd_traffic(B, S, H, D, causal))}
+    res = {"S": S, "H": H, "D": D, "B": B, "causal": causal, "dtype": dtype, "flops": flops,
+           "ms": wall, "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
+           "kernel_tflops": flops / (ev * 1e-3) / 1e12, "kernel_ms_median": _median(per),
+           "tflops_median": flops / (_median(per) * 1e-3) / 1e12,
+           "roofline": roofline("mfma", flops, ev, _fwd_traffic(B, S, H, D, causal))}
+    return res, (q, k, v)
 
 
 def _fwd_traffic(B, S, H, D, causal):
@@ -125,7 +128,7 @@ def _fwd_traffic(B, S, H, D, causal):
     return None
 
 
-def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0, warm_ms=EXTRA_WARM_MS):
+def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0, warm_ms=EXTRA_WARM_MS, cpu_heads=0):
     """C3: causal bf16 backward, timed without the forward; bitwise-identical check over 3 runs."""
     import torch
     from fable_attn import _C
@@ -144,32 +147,36 @@ def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0, warm_ms=EXTRA_WAR
     per = []
     wall, ev = time_steps(step, steps, warmup, per, warm_ms)
     flops = 2.5 * 4.0 * B * H * S * S * D / 2
-    return {"B": B, "S": S, "H": H, "D": D, "dtype": "bf16", "flops": flops, "ms": wall,
-            "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
-            "kernel_ms_median": _median(per), "tflops_median": flops / (_median(per) * 1e-3) / 1e12,
-            "bitwise_identical_x3": bool(same),
-            "roofline": roofline("mfma", flops, ev, profiled_traffic(BWD_C3_KERNELS))}
+    res = {"B": B, "S": S, "H": H, "D": D, "dtype": "bf16", "flops": flops, "ms": wall,
+           "kernel_ms": ev, "tflops": flops / (wall * 1e-3) / 1e12,
+           "kernel_ms_median": _median(per), "tflops_median": flops / (_median(per) * 1e-3) / 1e12,
+           "bitwise_identical_x3": bool(same),
+           "roofline": roofline("mfma", flops, ev, profiled_traffic(BWD_C3_KERNELS))}
+    if cpu_heads:
+        res["cpu_baseline"] = cpu_bwd(q, k, v, do, cpu_heads)
+    return res
 
 
-def cpu_bwd(heads=32, B=2, S=4096, H=32, D=128, seed=0):
-    """C3 on the CPU: torch autograd through the exact fp32 reference, one (batch, head) at a
-    time, `heads` of the B*H heads; the rate uses C3's numerator (2.5x the causal forward)."""
-    import torch
+def cpu_bwd(q, k, v, do, heads):
+    """C3 on the CPU: torch autograd through the exact fp32 reference on the run's own inputs
+    (copied to the host once, untimed), one (batch, head) at a time, `heads` of the B*H heads;
+    the rate uses C3's numerator (2.5x the causal forward)."""
     from oracle.torch_ref import attention_bhsd
     cores = _cpu_threads()
-    g = torch.Generator().manual_seed(seed)
-    mk = lambda: torch.randn(1, 1, S, D, generator=g).bfloat16().float()
-    q, k, v, do = mk(), mk(), mk(), mk()
+    B, S, H, D = q.shape
+    pairs = [(b, h) for b in range(B) for h in range(H)][:heads]
+    # the sampled heads of the run's tensors, [1, 1, S, D] fp32 each (host copies, untimed)
+    host = [tuple(x[b, :, h].float().cpu()[None, None] for x in (q, k, v, do)) for b, h in pairs]
     t0 = time.perf_counter()
-    for _ in range(heads):
-        qs, ks, vs = (x.clone().requires_grad_() for x in (q, k, v))
-        attention_bhsd(qs, ks, vs, D ** -0.5, causal=True).backward(do)
+    for qh, kh, vh, doh in host:
+        qs, ks, vs = (x.clone().requires_grad_() for x in (qh, kh, vh))
+        attention_bhsd(qs, ks, vs, D ** -0.5, causal=True).backward(doh)
     dt = time.perf_counter() - t0
-    flops = 2.5 * 4.0 * heads * S * S * D / 2
+    flops = 2.5 * 4.0 * len(pairs) * S * S * D / 2
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"{heads} of {B * H} (batch, head) pairs of the causal S={S} D={D} "
-                      f"backward (forward + autograd of the fp32 torch reference on CPU tensors), "
-                      f"{dt:.1f} s; extrapolated linearly to all heads"}
+            "sample": f"{len(pairs)} of {B * H} (batch, head) pairs of the run's own causal S={S} "
+                      f"D={D} inputs (forward + autograd of the fp32 torch reference on CPU "
+                      f"tensors), {dt:.1f} s; extrapolated linearly to all heads"}
 
 
 def bench_decode(steps, warmup, batch=16, Hq=32, Hk=8, D=128, ctx=32768, page=256, seed=0,
@@ -520,25 +527,28 @@ def profiled_traffic(kernel_res):
     return total
 
 
-def cpu_baseline(S=16384, H=32, D=128, heads=32, causal=True, seed=0):
-    """Exact fp32 torch reference on the host cores, `heads` of the H heads of a forward
-    workload (one head at a time to bound memory), scaled to the full workload's FLOP rate
-    (the causal half for causal, as the GPU figure)."""
-    import torch
+def cpu_baseline(inputs, heads=32, causal=True):
+    """Exact fp32 torch reference on the host cores over the run's own inputs (q, k, v of
+    batch element 0, copied to the host once, untimed), `heads` of the H heads of the forward
+    workload, one head at a time to bound memory, scaled to the full workload's FLOP rate (the
+    causal half for causal, as the GPU figure)."""
     from oracle.torch_ref import attention_bhsd
     cores = _cpu_threads()
-    g = torch.Generator().manual_seed(seed)
-    q, k, v = (torch.randn(1, 1, S, D, generator=g).half().float() for _ in range(3))
-    attention_bhsd(q[:, :, :256], k[:, :, :256], v[:, :, :256], D ** -0.5, causal=causal)  # warm
+    q, k, v = inputs
+    B, S, H, D = q.shape
+    heads = min(heads, H)
+    host = [tuple(x[0, :, h].float().cpu()[None, None] for x in (q, k, v)) for h in range(heads)]
+    qh, kh, vh = host[0]
+    attention_bhsd(qh[:, :, :256], kh[:, :, :256], vh[:, :, :256], D ** -0.5, causal=causal)  # warm
     t0 = time.perf_counter()
-    for _ in range(heads):
-        attention_bhsd(q, k, v, D ** -0.5, causal=causal)
+    for qh, kh, vh in host:
+        attention_bhsd(qh, kh, vh, D ** -0.5, causal=causal)
     dt = time.perf_counter() - t0
     flops = 4.0 * heads * S * S * D / (2 if causal else 1)
     return {"value": flops / dt / 1e12, "unit": "TFLOP/s", "cores": cores, "kind": "port",
-            "sample": f"{heads} of {H} heads of the {'causal' if causal else 'non-causal'} S={S} "
-                      f"D={D} forward, fp32 torch reference on CPU tensors, {dt:.1f} s"
-                      + ("; extrapolated linearly to all heads" if heads < H else "")}
+            "sample": f"{heads} of {B * H} heads of the run's own {'causal' if causal else 'non-causal'} "
+                      f"S={S} D={D} forward inputs, fp32 torch reference on CPU tensors, {dt:.1f} s"
+                      + ("; extrapolated linearly to all heads" if heads < B * H else "")}
 
 
 def main():
@@ -592,27 +602,28 @@ def main():
         sys.exit(2)
 
     log("[bench] headline: causal fp16 forward S=16384 H=32 D=128")
-    head = bench_fwd(16384, a.steps, a.warmup)
+    head, head_inputs = bench_fwd(16384, a.steps, a.warmup)
     log(f"[bench] fwd S=16384: {head['ms']:.3f} ms  {head['tflops']:.1f} TFLOP/s")
     cpu_on = not a.no_cpu
     extra = {}
     for name in [x for x in a.extras.split(",") if x]:
         try:
-            if name == "fwd":
+            if name in ("fwd", "c2sizes"):
                 for S in (4096, 8192):
-                    r = bench_fwd(S, max(a.steps, 20), max(3, a.warmup), warm_ms=EXTRA_WARM_MS)
+                    r, ins = bench_fwd(S, max(a.steps, 20), max(3, a.warmup), warm_ms=EXTRA_WARM_MS)
                     if cpu_on:
-                        r["cpu_baseline"] = cpu_baseline(S=S)
+                        r["cpu_baseline"] = cpu_baseline(ins)
                     extra[f"fwd_causal_S{S}"] = r
-                r = bench_fwd(1024, 20, 3, causal=False, H=8, D=64, warm_ms=EXTRA_WARM_MS)
+                    del ins
+            if name in ("fwd", "c1"):
+                r, ins = bench_fwd(1024, 20, 3, causal=False, H=8, D=64, warm_ms=EXTRA_WARM_MS)
                 if cpu_on:
-                    r["cpu_baseline"] = cpu_baseline(S=1024, H=8, D=64, heads=8, causal=False)
+                    r["cpu_baseline"] = cpu_baseline(ins, heads=8, causal=False)
                 extra["fwd_C1_S1024_D64_noncausal"] = r
-            elif name == "bwd":
-                r = bench_bwd(max(20, a.steps), max(3, a.warmup))
-                if cpu_on:
-                    r["cpu_baseline"] = cpu_bwd()
-                extra["bwd_C3"] = r
+                del ins
+            if name == "bwd":
+                extra["bwd_C3"] = bench_bwd(max(20, a.steps), max(3, a.warmup),
+                                            cpu_heads=32 if cpu_on else 0)
             elif name == "decode":
                 extra["decode_C4"] = bench_decode(max(a.steps, 20), max(3, a.warmup),
                                                   cpu_seqs=16 if cpu_on else 0)
@@ -633,7 +644,7 @@ def main():
     cpu = None
     if not a.no_cpu:
         log("[bench] cpu baseline")
-        cpu = cpu_baseline(heads=a.cpu_heads)
+        cpu = cpu_baseline(head_inputs, heads=a.cpu_heads)
         log(f"[bench] cpu: {cpu['value']:.4f} TFLOP/s on {cpu['cores']} cores")
     ach = head["kernel_tflops"]
     line = {

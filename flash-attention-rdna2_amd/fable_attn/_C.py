@@ -343,6 +343,8 @@ def dec(q, k_cache, v_cache, block_table, cache_seqlens, new_k, new_v, rotary_co
     for n, t in (("q", q), ("k_cache", k_cache), ("v_cache", v_cache)):
         _req(t.is_contiguous() and t.dtype == q.dtype and t.device == dev,
              f"{n}: contiguous, dtype and device of q")
+        _req(t.data_ptr() % 16 == 0 and (D * t.element_size()) % 16 == 0,
+             f"{n}: rows must be 16-byte aligned (base pointer and head_dim)")
     _req(v_cache.shape == k_cache.shape and k_cache.shape[3] == D,
          "k_cache/v_cache must both be [num_blocks, page, nheads_k, D] with q's D")
     _req(block_table.dim() == 2 and block_table.shape[0] == B, "block_table must be [B, max_blocks]")
@@ -367,7 +369,8 @@ def dec(q, k_cache, v_cache, block_table, cache_seqlens, new_k, new_v, rotary_co
         _req(new_v is not None, "new_k and new_v go together")
         for n, t in (("k", new_k), ("v", new_v)):
             _req(tuple(t.shape) == (B, NQ, Hk, D) and t.dtype == q.dtype and t.device == dev and
-                 t.is_contiguous(), f"{n}: contiguous [B, seqlen_q, nheads_k, D] of q's dtype")
+                 t.is_contiguous() and t.data_ptr() % 16 == 0,
+                 f"{n}: contiguous, 16-byte aligned [B, seqlen_q, nheads_k, D] of q's dtype")
     else:
         _req(new_v is None, "new_k and new_v go together")
     ctx_bound = block_table.shape[1] * page

@@ -18,14 +18,16 @@ Inputs are (batch, seqlen, nheads, headdim); the kernels take [B, H, S, D] strid
 nothing is copied unless a row is misaligned. An unsupported configuration raises; a missing
 library raises ImportError at import time. Nothing falls back to another implementation.
 """
+import ctypes
 import dataclasses
 import math
 import random
+import threading
 from typing import Optional
 
 import torch
 
-from . import _C
+from . import _C, _lib
 
 # Head dims the kernels take as they are: every multiple of 8 up to 256, in every dtype (rows
 # move in 16-byte accesses; the kernels zero the columns up to their own width). Any other head
@@ -167,12 +169,23 @@ def _normalize(q, k, v, *, qv=None, softmax_scale=None, causal=False, window_siz
 
 def _bhsd(t):
     """(B,S,H,D) -> the [B,H,S,D] view the kernels take; a copy only when a row is not 16-byte
-    aligned (the kernels move rows in 16-byte accesses)."""
+    aligned (the kernels move rows in 16-byte accesses). The copy is a fresh allocation: a
+    contiguous tensor at a misaligned offset would stay where it is under .contiguous()."""
     v = t.transpose(1, 2)
     st, el = v.stride(), v.element_size()
     aligned = (st[-1] == 1 and v.data_ptr() % 16 == 0
                and (st[0] * el | st[1] * el | st[2] * el) % 16 == 0)
-    return v if aligned else t.contiguous().transpose(1, 2)
+    return v if aligned else t.clone(memory_format=torch.contiguous_format).transpose(1, 2)
+
+
+def _aligned(t, dense=False):
+    """t itself when the kernels can read it in place (contiguous head dim, 16-byte aligned
+    base and strides; with dense, also contiguous), else a fresh contiguous copy."""
+    st, el = t.stride(), t.element_size()
+    ok = st[-1] == 1 and t.data_ptr() % 16 == 0 and all((x * el) % 16 == 0 for x in st[:-1])
+    if ok and (not dense or t.is_contiguous()):
+        return t
+    return t.clone(memory_format=torch.contiguous_format)
 
 
 
@@ -233,7 +246,7 @@ class _Attention(torch.autograd.Function):
             dq, dk, dv = _C.bwd(_bhsd(dout.transpose(1, 2)), q, k, v, out, lse, *args)
         else:
             cu_q, cu_k, mq, mk, su_q, su_k = pack
-            dq, dk, dv = _C.bwd_varlen(dout.contiguous(), q, k, v, out, lse, cu_q, cu_k, mq, mk,
+            dq, dk, dv = _C.bwd_varlen(_aligned(dout), q, k, v, out, lse, cu_q, cu_k, mq, mk,
                                        *args, su_q, su_k)
         return None, None, dq, dk, dv
 
@@ -296,6 +309,77 @@ def _dense(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap, alib
     return res, lse, probs
 
 
+# ----------------------------------------------------------------------------- inference fast path
+_tls = threading.local()
+_MAX_PLANS = 256
+
+
+def _infer_plan(q, k, v, softmax_scale, causal, window_size, softcap):
+    """The launch parameters of one inference call signature, validated once: the general
+    path's normalisation (which raises exactly as it does there) followed by the binding's
+    layout checks. None when the signature needs the general path (a padded or widened head
+    dim, rows the kernels cannot read in place). The result holds no data pointer."""
+    spec = _normalize(q, k, v, softmax_scale=softmax_scale, causal=causal,
+                      window_size=window_size, softcap=softcap)
+    if spec.keep is not None or spec.q is not q or spec.k is not k or spec.v is not v:
+        return None
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4 or k.dtype != q.dtype or v.dtype != q.dtype:
+        return None
+    if k.device != q.device or v.device != q.device or q.device.index is None:
+        return None
+    B, SQ, Hq, D = q.shape
+    SK, Hk = k.shape[1], k.shape[2]
+    if k.shape[0] != B or k.shape[3] != D or tuple(v.shape) != tuple(k.shape) or Hq % Hk:
+        return None
+    el = q.element_size()
+    for t in (q, k, v):
+        st = t.stride()
+        if st[3] != 1 or (st[0] * el | st[1] * el | st[2] * el) % 16:
+            return None
+    bhs = lambda t: _lib.Strides(t.stride(0), t.stride(2), t.stride(1))   # [B,H,S,D] view
+    o = _lib.Strides(SQ * Hq * D, D, Hq * D)      # the (B,S,H,D)-dense output seen as [B,H,S,D]
+    p = _lib.FableFwdParams(0, 0, 0, 0, None, bhs(q), bhs(k), bhs(v), o, SQ, SK, D, Hq, Hq // Hk,
+                            spec.scale, spec.softcap, spec.wl, spec.wr, None, spec.causal, 0.0, 0,
+                            None, None, B, 0, None, None, 0, 0)
+    return p, _C._dt(q), (B, SQ, Hq, D)
+
+
+def _infer_fast(q, k, v, softmax_scale, causal, window_size, softcap):
+    """flash_attn_func's plain inference call (no gradient, dropout, alibi, qv, chunk or
+    probabilities) with the per-call host work cut to what changes between calls of one
+    signature: a per-thread cache maps (shapes, strides, dtype, device, mask, scale, softcap)
+    to validated launch parameters, so a call allocates the output, fills four pointers and
+    launches (no LSE: the caller does not get it). None sends the call to the general path,
+    which gives the same result."""
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        return None
+    plans = getattr(_tls, "plans", None)
+    if plans is None:
+        plans = _tls.plans = {}
+    try:
+        key = (q.shape, k.shape, v.shape, q.stride(), k.stride(), v.stride(), q.dtype, q.device,
+               causal, window_size, softcap, softmax_scale)
+        plan = plans.get(key, False)
+    except (AttributeError, TypeError):   # not tensors, or an unhashable argument
+        return None
+    if plan is False:
+        if len(plans) >= _MAX_PLANS:
+            plans.clear()
+        plan = plans[key] = _infer_plan(q, k, v, softmax_scale, causal, window_size, softcap)
+    if plan is None:
+        return None
+    qp, kp, vp = q.data_ptr(), k.data_ptr(), v.data_ptr()
+    dev = q.device.index
+    if (qp | kp | vp) & 15 or dev != torch._C._cuda_getDevice():
+        return None
+    p, dt, shape = plan
+    out = torch.empty(shape, dtype=q.dtype, device=q.device)
+    p.Q, p.K, p.V, p.O = qp, kp, vp, out.data_ptr()
+    _lib.check(_C._L.fable_attn_fwd(p, dt, ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(dev))),
+               "fable_attn_fwd")
+    return out
+
+
 def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
                     window_size=(-1, -1), softcap=0.0, alibi_slopes=None,
                     deterministic=False, return_attn_probs=False, *,
@@ -304,6 +388,14 @@ def flash_attn_func(q, k, v, dropout_p=0.0, softmax_scale=None, causal=False,
                     num_splits=1, pack_gqa=None, sm_margin=0):
     """q, k, v: (batch, seqlen, nheads, headdim). Returns out in the same layout (dense), or
     (out, softmax_lse, S_dmask) when return_attn_probs=True."""
+    if (not dropout_p and alibi_slopes is None and qv is None and not attention_chunk
+            and not return_attn_probs and q_descale is None and k_descale is None
+            and v_descale is None and (num_splits is None or type(num_splits) is int)
+            and (pack_gqa is None or type(pack_gqa) is bool)
+            and (sm_margin is None or type(sm_margin) is int)):
+        out = _infer_fast(q, k, v, softmax_scale, causal, window_size, softcap)
+        if out is not None:
+            return out
     return _dense(q, k, v, dropout_p, softmax_scale, causal, window_size, softcap, alibi_slopes,
                   deterministic, return_attn_probs, qv, attention_chunk, q_descale, k_descale,
                   v_descale, num_splits, pack_gqa, sm_margin)
@@ -397,7 +489,7 @@ def flash_attn_varlen_func(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlen_q, ma
     pack = (_as_index(cu_seqlens_q, dev), _as_index(cu_seqlens_k, dev), int(max_seqlen_q),
             int(max_seqlen_k), _as_index(seqused_q, dev) if seqused_q is not None else None,
             _as_index(seqused_k, dev) if seqused_k is not None else None)
-    out, lse = _run(spec, pack, spec.q.contiguous(), spec.k.contiguous(), spec.v.contiguous())
+    out, lse = _run(spec, pack, _aligned(spec.q), _aligned(spec.k), _aligned(spec.v))
     out = spec.cut(out)
     if not return_attn_probs:
         return out
@@ -569,8 +661,9 @@ def flash_attn_with_kvcache(q, k_cache, v_cache, k=None, v=None, qv=None,
     sin = rotary_sin.to(torch.float32).contiguous() if rotary_sin is not None else None
     alibi = alibi_slopes.to(torch.float32).contiguous() if alibi_slopes is not None else None
     rpos = _as_index(rotary_seqlens, dev) if rotary_seqlens is not None else None
-    out, lse = _C.dec(q.contiguous(), kc.contiguous(), vc.contiguous(), table, lens,
-                      k.contiguous() if appending else None, v.contiguous() if appending else None,
+    out, lse = _C.dec(_aligned(q, dense=True), kc.contiguous(), vc.contiguous(), table, lens,
+                      _aligned(k, dense=True) if appending else None,
+                      _aligned(v, dense=True) if appending else None,
                       cos, sin, bool(rotary_interleaved), float(softmax_scale), int(keys_back),
                       int(num_splits or 0), leftpad, bool(return_softmax_lse),
                       float(softcap or 0.0), alibi, int(cos.shape[-1] * 2) if cos is not None else 0,

@@ -235,7 +235,8 @@ typedef struct FableBwdParams {
  * q [batch, nq, NH, HD] contiguous; Kc/Vc [num_blocks, page, NH/gqa, HD] contiguous;
  * block_table [batch, max_blocks] int32; ctx_len [batch] int32 = cache length BEFORE the
  * append (flash_attn cache_seqlens); o [batch, nq, NH, HD]; scratch fp32
- * [batch*nq*NH*nsplit*(HD+2)] (caller-allocated); lse_out [batch*nq*NH] or NULL.
+ * [batch*nq*NH*nsplit*(HD+2)] (caller-allocated; may be NULL when nsplit == 1 with fp16/bf16,
+ * where the partial kernel writes o and lse_out itself); lse_out [batch*nq*NH] or NULL.
  * New token tk of sequence b sits at position ctx_len[b]+tk and sees keys
  * [max(leftpad[b], pos-window+1 if window>=0), ctx_len[b] + (append ? tk+1 : 0)).
  * page must be a power of two. rotary: 0 none, 1 neox (half split), 2 interleaved (pairs);
@@ -302,7 +303,8 @@ int fable_attn_dec(FableDecParams p, int dtype, void* stream, const void* new_k,
  * forbid hipMalloc). p.scratch is ignored: the split partials go to a fixed device array owned
  * by the library, one per GPU, kept until the process ends, of
  * fable_attn_dec_noalloc_max_floats() floats (16 MiB); a call needing more
- * (batch*nq*NH*nsplit*(HD+2) floats) fails with FA_ERR_ARG. Nothing is allocated or freed.
+ * (batch*nq*NH*nsplit*(HD+2) floats) fails with FA_ERR_ARG, except with nsplit == 1 in
+ * fp16/bf16, which never touches the array and has no size limit. Nothing is allocated or freed.
  * The stream's device must be the current device. Calls that overlap on one GPU share the
  * array and race: the caller serialises them. Otherwise exactly fable_attn_dec (same kernels,
  * same results). */

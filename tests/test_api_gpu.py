@@ -131,3 +131,49 @@ def test_host_checks_reject_before_launch():
         _C.dec(qd, kc, kc, bt, cs[:1], None, None, None, None, False, 0.1, -1)
     with pytest.raises(RuntimeError, match="block_table"):
         _C.dec(qd, kc, kc, bt[:1], cs, None, None, None, None, False, 0.1, -1)
+
+
+def test_inference_fast_path_matches_general_path():
+    """flash_attn_func's inference calls go through a per-thread cache of validated launch
+    parameters; the output must be bit for bit the general path's (the same kernel, launched
+    with the same parameters), for dense and strided inputs, GQA, masks, softcap and every
+    dtype; calls with gradients, unaligned rows or a padded head dim take the general path."""
+    import torch
+
+    from fable_attn import flash_attn_interface as fai
+    print("[fast-path]", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(11)
+    cases = [((2, 300, 8, 64), 8, torch.float16, dict(causal=True)),
+             ((1, 257, 8, 128), 2, torch.bfloat16, dict(window_size=(40, 7), softcap=20.0)),
+             ((1, 100, 4, 80), 4, torch.float32, dict(causal=True, softmax_scale=0.3)),
+             ((2, 64, 4, 96), 1, torch.float16, dict())]
+    for shape, hk, dt, kw in cases:
+        B, S, H, D = shape
+        q = torch.randn(shape, device="cuda", dtype=dt, generator=g)
+        kv = torch.randn(B, S, 2, hk, D, device="cuda", dtype=dt, generator=g)
+        k, v = kv.unbind(2)                      # strided views, as flash_attn_kvpacked_func makes
+        fai._tls.plans = {}
+        fast = fai.flash_attn_func(q, k, v, **kw)
+        assert len(fai._tls.plans) == 1 and next(iter(fai._tls.plans.values())) is not None
+        gen = fai._dense(q, k, v, 0.0, kw.get("softmax_scale"), kw.get("causal", False),
+                         kw.get("window_size", (-1, -1)), kw.get("softcap", 0.0), None, False,
+                         False, None, 0, None, None, None, 1, None, 0)
+        torch.cuda.synchronize()
+        assert fast.shape == shape and fast.is_contiguous()
+        assert torch.equal(fast, gen), (shape, dt, kw)
+        again = fai.flash_attn_func(q, k, v, **kw)      # the cached plan, new output buffer
+        assert torch.equal(again, gen) and again.data_ptr() != fast.data_ptr()
+    # the general path: gradients, an unaligned base pointer, a padded head dim
+    q = torch.randn(1, 64, 2, 64, device="cuda", dtype=torch.float16, generator=g)
+    fai._tls.plans = {}
+    qg = q.clone().requires_grad_()
+    fai.flash_attn_func(qg, q, q).sum().backward()
+    assert qg.grad is not None and not fai._tls.plans
+    buf = torch.randn(1 + 64 * 2 * 64, device="cuda", dtype=torch.float16, generator=g)
+    qu = buf[1:].view(1, 64, 2, 64)                     # rows 2 bytes off 16-byte alignment
+    ref = fai.flash_attn_func(qu.clone(), q, q)
+    assert torch.equal(fai.flash_attn_func(qu, q, q), ref)      # copied to an aligned buffer
+    q40 = torch.randn(1, 64, 2, 36, device="cuda", dtype=torch.float16, generator=g)
+    fai._tls.plans = {}
+    o40 = fai.flash_attn_func(q40, q40, q40)
+    assert o40.shape == (1, 64, 2, 36) and list(fai._tls.plans.values()) == [None]

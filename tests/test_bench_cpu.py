@@ -13,7 +13,8 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 def test_profiles_cover_the_benched_kernels():
     # every workload whose roofline carries `traffic` finds its kernels in the committed tables
-    for res in (bench.FWD_C2_KERNEL, bench.BWD_C3_KERNELS, bench.DEC_C4_KERNELS, bench.VARLEN_C5_KERNEL):
+    for res in (bench.FWD_C2_KERNEL, bench.FWD_C1_KERNEL, bench.BWD_C3_KERNELS, bench.DEC_C4_KERNELS,
+                bench.VARLEN_C5_KERNEL):
         t = bench.profiled_traffic(res)
         assert t is not None and t > 0, res
     # the forward's bytes cover at least Q, K, V read and O written once
@@ -23,6 +24,7 @@ def test_profiles_cover_the_benched_kernels():
 
 def test_forward_traffic_only_for_profiled_shapes():
     assert bench._fwd_traffic(1, 16384, 32, 128, True) is not None
+    assert bench._fwd_traffic(1, 1024, 8, 64, False) >= 4 * 1024 * 8 * 64 * 2   # C1
     assert bench._fwd_traffic(1, 8192, 32, 128, True) is None
     assert bench._fwd_traffic(1, 4096, 32, 128, True) is None
 
@@ -46,6 +48,9 @@ def test_parity_summary(tmp_path):
     # dk's floor 3e-3 > 2/3 of 4e-3, so its bound is 1.5 x 3e-3 = 4.5e-3: 1e-3 is 22% of it
     assert "1.00e-03 (worst 22% of its bound)" in t
     assert "3.00e-03 (worst 75% of its bound)" in t
+    # the raised bound is listed case by case, with whether the error exceeds the flat bound
+    assert "Gradients held to 1.5x their floor instead of the flat bound: 1 (of 3" in t
+    assert "| bwd | b | bf16 | dk | 1.00e-03 | 3.00e-03 | 4.50e-03 | no (4e-03) |" in t
 
 
 def test_more_than_one_gpu_is_refused():
