@@ -893,12 +893,16 @@ struct BwdDsQCfg {
 };
 
 // Element offset of (key row r, query slot n) in a wave's dS block: 64-byte rows of four 16-byte
-// chunks, chunk n/8 stored at position (n/8) ^ (2*r.bit2 + r.bit3). The transposing reads
-// (rows R..R+3 and R+4..R+7 of the two half-waves, R a multiple of 8) then use disjoint chunk
-// pairs, and the 16-byte writes of 16 consecutive rows land in 16 distinct 16-byte slots of a
-// 256-byte bank cycle.
+// chunks, chunk n/8 stored at position (n/8) ^ (2*(r.bit1 ^ r.bit3) + r.bit2). The 16-byte
+// writes (one row per lane) then reach distinct 16-byte bank slots within every 8 consecutive
+// rows of one parity (bits 1, 2 map one to one) and within every 16 consecutive rows (bits 2, 3
+// map one to one for each r mod 4), and the transposing reads of rows R..R+3 find rows R and
+// R+2 (and R+1, R+3) on disjoint chunk pairs. SQ_LDS_BANK_CONFLICT of the dQ kernel on C3: 8.9e6
+// cycles per dispatch with the earlier 2*r.bit2 + r.bit3 (its 16-byte writes conflicted two
+// ways), 0 with this one; the time did not change (the writes cost ~3% of the backward by
+// their LDS latency, not by conflicts: a timing copy without them ran 1.03x faster).
 __device__ __forceinline__ int dsl_ofs(int r, int n) {
-  return r * 32 + 8 * ((n >> 3) ^ (2 * ((r >> 2) & 1) + ((r >> 3) & 1))) + (n & 7);
+  return r * 32 + 8 * ((n >> 3) ^ (2 * (((r >> 1) ^ (r >> 3)) & 1) + ((r >> 2) & 1))) + (n & 7);
 }
 
 // dQ^T = K^T . dS^T over the dS tiles the pair kernel wrote for this wave's 32 queries. K tiles
