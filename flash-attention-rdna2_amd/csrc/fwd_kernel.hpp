@@ -314,6 +314,16 @@ fwd_kernel(FableFwdParams p, int nqt) {
   // 1 - 2 / (exp(2y) + 1); exp(2y) = exp2(q.k * kcap), so no division per score
   const float kcap = p.softcap > 0.0f ? 2.0f * kLog2e * p.scale / p.softcap : 0.0f;
   const float lcap = p.softcap * kLog2e;
+  // Polynomial softcap (transform bit 3; the one-wave loop of 32-key tiles below): tanh(y) =
+  // y P(y^2) on |y| <= kPolyY, y = scale*s/c, odd degree 7, minimax coefficients from Lawson's
+  // iteratively reweighted least squares: |error| <= 1.9e-8 exactly, 5e-8 evaluated in fp32,
+  // against 1.8e-7 for the exp/rcp form above, with no transcendental; the logit (log2 units)
+  // is u (a1 + u^2 (a3 + u^2 (a5 + u^2 a7))), u = s * kpoly, a_i = c_i * c * log2(e)
+  constexpr float kPolyY = 0.4f;
+  const float kpoly = p.softcap > 0.0f ? p.scale / p.softcap : 0.0f;
+  const float prange = p.softcap > 0.0f ? kPolyY * p.softcap / p.scale : 0.0f;  // largest |s|
+  const float pa1 = 0.9999995735192077f * lcap, pa3 = -0.3332972661781136f * lcap;
+  const float pa5 = 0.1325057420337534f * lcap, pa7 = -0.046826030150687044f * lcap;
   const float aslope2 = aslope * kLog2e;
   // dropout: probabilities are scaled after the row sum, O = sum z p V / sum p
   const float keep_scale = DROP ? 1.0f / (1.0f - p.dropout_p) : 1.0f;
@@ -330,7 +340,10 @@ fwd_kernel(FableFwdParams p, int nqt) {
   // (bit 0 softcap, bit 1 alibi), then the interval mask
   auto logit = [&](auto masked, auto cap, int i, float sv, int kb, int jb, int r, unsigned vis) -> float {
     float x;
-    if constexpr ((decltype(cap)::value & 1) != 0) {
+    if constexpr ((decltype(cap)::value & 8) != 0) {
+      const float u = sv * kpoly, u2 = u * u;
+      x = u * fmaf(u2, fmaf(u2, fmaf(u2, pa7, pa5), pa3), pa1);
+    } else if constexpr ((decltype(cap)::value & 1) != 0) {
       const float e = exp2_fast(sv * kcap);
       x = fmaf(-2.0f * lcap, __builtin_amdgcn_rcpf(e + 1.0f), lcap);
     } else {
@@ -569,6 +582,14 @@ fwd_kernel(FableFwdParams p, int nqt) {
           unsigned vis[C::NB];
 #pragma unroll
           for (int jb = 0; jb < C::NB; jb++) vis[jb] = vis_word(0, kb1, jb);
+          // Softcap by the polynomial on 32-key tiles (C5: 0.58 instead of 1.53 transcendentals
+          // per MFMA, the same time); the 64-key softcap shape keeps the exp/rcp form (with the
+          // polynomial it held 40 more registers, 491 of 512, and ran 0.96-0.97x). The raw
+          // scores stay in registers for the rare tile outside the polynomial's range.
+          constexpr bool kPoly = (decltype(cap)::value & 1) != 0 && C::NB == 1;
+          using CapP = std::integral_constant<int, decltype(cap)::value | (kPoly ? 8 : 0)>;
+          float raw[kPoly ? 16 * C::NB : 1];
+          float amax = 0.0f;  // largest |raw score| of the lane's tile
           V4 rd[2][SPS][2];
           auto vread = [&](int k, V4 (&r)[2]) {
             const int db = k / C::NG, g = k % C::NG;
@@ -598,11 +619,35 @@ fwd_kernel(FableFwdParams p, int nqt) {
               const int kk = k + u;
               float sk = s[0][kk / 16][kk % 16];
               asm volatile("" : "+v"(sk));
-              s[0][kk / 16][kk % 16] = logit(Masked{}, cap, 0, sk, kb1, kk / 16, kk % 16, vis[kk / 16]);
+              if constexpr (kPoly) {
+                raw[kk] = sk;
+                amax = fmaxf(amax, fabsf(sk));
+              }
+              s[0][kk / 16][kk % 16] = logit(Masked{}, CapP{}, 0, sk, kb1, kk / 16, kk % 16, vis[kk / 16]);
             }
             __builtin_amdgcn_sched_barrier(0);
           }
+          const float m_keep = m_run[0], l_keep = l_run[0];
           corr[0] = softmax(Masked{}, std::integral_constant<int, 4>{}, 0, s[0], kb1, pb[0], resc[0]);
+          if constexpr (kPoly) {
+            // A score outside the polynomial's range anywhere in the wave: the row state goes
+            // back to before this tile, and the tile is redone with the exp/rcp form. The test
+            // comes after the softmax, so the common path keeps the products and the whole
+            // softmax in one basic block (tested before it, the softmax moved to a block of its
+            // own and C5 ran 0.98-0.99x)
+            if (__builtin_amdgcn_readfirstlane((int)(__builtin_amdgcn_ballot_w64(!(amax <= prange)) != 0))) {
+              m_run[0] = m_keep;
+              l_run[0] = l_keep;
+#pragma unroll
+              for (int kk = 0; kk < 16 * C::NB; kk++) {
+                // (the exact form stays inside the branch: not hoisted ahead of the test)
+                float rv = raw[kk];
+                asm volatile("" : "+v"(rv));
+                s[0][kk / 16][kk % 16] = logit(Masked{}, cap, 0, rv, kb1, kk / 16, kk % 16, vis[kk / 16]);
+              }
+              corr[0] = softmax(Masked{}, std::integral_constant<int, 4>{}, 0, s[0], kb1, pb[0], resc[0]);
+            }
+          }
         } else {
           pv(t & (NST - 1), pb);
 #pragma unroll

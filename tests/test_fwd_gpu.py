@@ -268,3 +268,44 @@ def test_varlen_full_config_c5_sampled():
         got_l = to_np(lse[hd, a:a + L])[None, None]
         _check_rows("fwd_full_c5", f"C5 seq {z} (L={L}) head {hd}", "bf16", seq(out), got_l,
                     o_ref, l_ref, rows)
+
+
+# The D=256 softcap loop computes tanh by a polynomial on |scale*s/softcap| <= 0.4 and switches
+# a whole 32-key block of one wave to the exact form when any of its scores is outside that
+# range. name, B, S, H, gqa, window left, softcap, alibi, key rows scaled by 8 (None: none)
+SOFTCAP_RANGE = [
+    ("narrow: some blocks outside the range", 1, 300, 8, 2, 64, 30.0, False, (96, 128)),
+    ("64-key tiles: some blocks outside the range", 1, 330, 8, 2, -1, 30.0, False, (160, 224)),
+    ("64-key tiles + alibi: every block outside", 1, 230, 8, 2, -1, 2.0, True, None),
+    ("narrow: every block outside", 1, 260, 4, 1, 100, 1.5, False, None),
+]
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("case", SOFTCAP_RANGE, ids=[c[0] for c in SOFTCAP_RANGE])
+def test_softcap_polynomial_range(case, dt):
+    import torch
+
+    from fable_attn import _C
+    name, B, S, H, gqa, wl, sc, alibi, big = case
+    print(f"[fwd-softcap-range] {name} {dt}", flush=True)
+    D, Hk = 256, H // gqa
+    q = gen((B, H, S, D), 41, dt)
+    k = gen((B, Hk, S, D), 42, dt)
+    v = gen((B, Hk, S, D), 43, dt)
+    if big is not None:
+        k[:, :, big[0]:big[1]] *= 8.0          # exact in fp16/bf16: a power of two
+    al = _alibi(H) if alibi else None
+    scale = 1.0 / math.sqrt(D)
+    o_ref, l_ref = orc.fwd(q, k, v, scale, True, wl, 0, sc, al, 0)
+    dev = lambda a: to_dev(a, dt).transpose(1, 2).contiguous().transpose(1, 2)
+    ald = torch.from_numpy(al).cuda() if al is not None else None
+    out, lse = _C.fwd(dev(q), dev(k), dev(v), scale, True, wl, 0, sc, ald, 0.0, 0)
+    torch.cuda.synchronize()
+    o, l = to_np(out), to_np(lse)
+    rel = orc.rel_rms(o, o_ref)
+    lerr, inf_ok = lse_err(l, l_ref)
+    log_errors("fwd_softcap_range", name, dt, o=rel, lse=lerr)
+    assert np.isfinite(o).all()
+    assert rel <= TOL[dt], f"rel_rms {rel:.3e} > {TOL[dt]}"
+    assert inf_ok and lerr <= LSE_ABS, f"LSE abs err {lerr:.3e}"
