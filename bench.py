@@ -326,7 +326,7 @@ def summarize_pmc(fetch_dir, write_dir, kernel_re=None):
             continue
         f, w = c["FETCH_SIZE"][1], c["WRITE_SIZE"][1]
         hbm = f * 1024 * factor["FETCH_SIZE"] + w * 1024 * factor["WRITE_SIZE"]
-        out.append(f"| `{k[:100]}` | {c['FETCH_SIZE'][0]} | {f:.1f} | {w:.1f} | {hbm:.0f} |")
+        out.append(f"| `{k}` | {c['FETCH_SIZE'][0]} | {f:.1f} | {w:.1f} | {hbm:.0f} |")
     out.append("")
     out.append(f"Calibration (1 GiB `{COPY_KERNEL}`): FETCH_SIZE x{factor['FETCH_SIZE']:.4f}, "
                f"WRITE_SIZE x{factor['WRITE_SIZE']:.4f} (bytes per KiB-count / 1024).")
@@ -360,7 +360,7 @@ def summarize_mfma(d, kernel_re=None):
         busy = sum(e["SQ_VALU_MFMA_BUSY_CYCLES"] for e in es)
         cyc = sum(e["GRBM_GUI_ACTIVE"] for e in es) / nxcc
         ns = sum(e["ns"] for e in es)
-        out.append(f"| `{k[:100]}` | {len(es)} | {ns / len(es) / 1e3:.1f} | {cyc / ns:.2f} | "
+        out.append(f"| `{k}` | {len(es)} | {ns / len(es) / 1e3:.1f} | {cyc / ns:.2f} | "
                    f"{busy / (simds * cyc):.1%} | {busy / (simds * ns * fmax_ghz):.1%} |")
     out.append("")
     out.append(f"Agent: {simds} SIMDs, {nxcc} XCDs, peak engine clock {fmax_ghz:.1f} GHz.")
@@ -429,7 +429,7 @@ def summarize_stats(d, kernel_re=None, skip=0, last=0):
         ds = [t for _, t in sorted(trace.get(r["Name"], []))]
         ds = ds[-last:] if last else ds[skip:]
         after = f"{sum(ds) / len(ds) / 1e3:.1f}" if ds else "-"
-        out.append(f"| `{r['Name'][:100]}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
+        out.append(f"| `{r['Name']}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.1f} | "
                    f"{float(r['MinNs']) / 1e3:.1f} | {float(r['MaxNs']) / 1e3:.1f} | "
                    f"{float(r['Percentage']):.2f} | {after} |")
     return "\n".join(out)
@@ -437,13 +437,15 @@ def summarize_stats(d, kernel_re=None, skip=0, last=0):
 
 # kernel symbols of the measured workloads, as regexes over the mangled names in the PMC
 # tables (the headline's kernel; the kernels of one C3, C4 or C5 step)
-FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128ELi64ELi8ELi2ELi1EEELb1ELb0ELb0EEEv14FableFwdParamsi"
-FWD_C1_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi64E.*ELb0ELb0ELb0EEEv14FableFwdParamsi"
+FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128ELi64ELi8ELi2ELi1EEELb1ELb0ELb0EEEv14FableFwdParamsiNS_8FwdSplitE"
+# C1 takes the key split: the split kernel, then the merge of its partials
+FWD_C1_KERNEL = (r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi64E.*ELb0ELb0ELb0EEEv14FableFwdParamsiNS_8FwdSplitE",
+                 r"_ZN2fa24fwd_split_combine_kernelIDF16_EEv14FableFwdParamsNS_8FwdSplitE")
 BWD_C3_KERNELS = (r"_ZN2fa15bwd_dsum_kernelIDF16b.*", r"_ZN2fa20bwd_dkdv_pair_kernelIDF16b.*",
                   r"_ZN2fa16bwd_dq_ds_kernelIDF16b.*")
 DEC_C4_KERNELS = (r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0ELb1EEEv14FableDecParamsiii",
                   r"_ZN2fa18dec_combine_kernelIDF16_Li128EEEv14FableDecParams")
-VARLEN_C5_KERNEL = r"_ZN2fa10fwd_kernelIDF16bNS_6FwdCfgILi256E.*ELb1ELb1ELb0EEEv14FableFwdParamsi"
+VARLEN_C5_KERNEL = r"_ZN2fa10fwd_kernelIDF16bNS_6FwdCfgILi256E.*ELb1ELb1ELb0EEEv14FableFwdParamsiNS_8FwdSplitE"
 
 
 def summarize_parity(path):

@@ -114,6 +114,21 @@ __device__ __forceinline__ void store_cblock(T* dst, const f32x16& acc, float sc
   }
 }
 
+// The same C block in fp32, without the exchange: the lane's 16 values are head dims
+// 16j + 8u + 4hh + 0..3 (j, u in {0, 1}) of its query, four 16-byte stores.
+__device__ __forceinline__ void store_cblock_f32(float* dst, const f32x16& acc, float scale, int hh, bool ok,
+                                                 int ncols = 32) {
+#pragma unroll
+  for (int j = 0; j < 2; j++)
+#pragma unroll
+    for (int u = 0; u < 2; u++) {
+      const int d = 16 * j + 8 * u + 4 * hh;
+      const f32x4 v = {acc[8 * j + 4 * u] * scale, acc[8 * j + 4 * u + 1] * scale,
+                       acc[8 * j + 4 * u + 2] * scale, acc[8 * j + 4 * u + 3] * scale};
+      if (ok && d < ncols) *(f32x4*)(dst + d) = v;
+    }
+}
+
 // 2^x on the transcendental unit (v_exp_f32): exp2(-inf) = 0.
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 

@@ -1,6 +1,7 @@
-// fwd.hip — fable_attn_fwd, the forward's C-ABI entry point: argument checks and dispatch to
-// the per-width fp16/bf16 kernels (fwd_d32.hip .. fwd_d256.hip, kernel in fwd_kernel.hpp) and the
-// fp32 kernels (fwd_f32.hip). Reference launcher: kernels/fa_forward.hip:424-451.
+// fwd.hip — the forward's C-ABI entry points (fable_attn_fwd, fable_attn_fwd_ws and the
+// workspace query): argument checks and dispatch to the per-width fp16/bf16 kernels
+// (fwd_d32.hip .. fwd_d256.hip, kernel in fwd_kernel.hpp) and the fp32 kernels (fwd_f32.hip);
+// the merge of a key-split forward's partials. Reference launcher: kernels/fa_forward.hip:424-451.
 #include "attn_device.hpp"
 #include "fwd_common.hpp"
 #include "status.hpp"
@@ -10,41 +11,107 @@ namespace fa {
 // fp16/bf16: every head dim that is a multiple of 8 up to 256 runs in the kernel of the next
 // multiple of 32 (the columns between are zero: at most 24 of them, <= 1.75x the MFMA work at
 // head dim 8, <= 1.1x from 80 up)
-static int dispatch_hd(const FableFwdParams& p, int dtype, hipStream_t st) {
+static int dispatch_hd(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws) {
   if (p.HD <= 0 || p.HD > 256 || p.HD % 8)
     return fail(FA_ERR_HEADDIM, "fable_attn_fwd: head_dim=%d has no kernel (multiples of 8 up to 256)", p.HD);
   switch ((p.HD + 31) / 32) {
-    case 1: return launch_fwd_d32(p, dtype, st);
-    case 2: return launch_fwd_d64(p, dtype, st);
-    case 3: return launch_fwd_d96(p, dtype, st);
-    case 4: return launch_fwd_d128(p, dtype, st);
-    case 5: return launch_fwd_d160(p, dtype, st);
-    case 6: return launch_fwd_d192(p, dtype, st);
-    case 7: return launch_fwd_d224(p, dtype, st);
-    default: return launch_fwd_d256(p, dtype, st);
+    case 1: return launch_fwd_d32(p, dtype, st, ws);
+    case 2: return launch_fwd_d64(p, dtype, st, ws);
+    case 3: return launch_fwd_d96(p, dtype, st, ws);
+    case 4: return launch_fwd_d128(p, dtype, st, ws);
+    case 5: return launch_fwd_d160(p, dtype, st, ws);
+    case 6: return launch_fwd_d192(p, dtype, st, ws);
+    case 7: return launch_fwd_d224(p, dtype, st, ws);
+    default: return launch_fwd_d256(p, dtype, st, ws);
   }
 }
 
-}  // namespace fa
+// Merge of the key-split partials: one thread per (row, 4 head dims), rows r = (b*NH + h)*SQ + q.
+// LSE = m + log(sum_s exp(lse_s - m)), O = sum_s exp(lse_s - LSE) O_s; a row no split saw gets
+// O = 0 and LSE = -inf, as in the unsplit kernel.
+template <typename T>
+__global__ __launch_bounds__(256) void fwd_split_combine_kernel(FableFwdParams p, FwdSplit sp) {
+  const int ch = p.HD / 4;
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= sp.rows * ch) return;
+  const long long r = gid / ch;
+  const int c = (int)(gid - r * ch);
+  const int q = (int)(r % p.SQ);
+  const long long bh = r / p.SQ;
+  const int h = (int)(bh % p.NH), b = (int)(bh / p.NH);
+  float m = -INFINITY;
+  for (int k = 0; k < sp.n; k++) m = fmaxf(m, sp.lse[k * sp.rows + r]);
+  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+  float wsum = 0.0f;
+  if (m != -INFINITY) {
+    for (int k = 0; k < sp.n; k++) {
+      const float w = __expf(sp.lse[k * sp.rows + r] - m);
+      wsum += w;
+      acc += w * *(const f32x4*)(sp.o + (k * sp.rows + r) * p.HD + 4 * c);
+    }
+  }
+  const float inv = m != -INFINITY ? 1.0f / wsum : 0.0f;
+  typename Dt<T>::V4 o;
+#pragma unroll
+  for (int e = 0; e < 4; e++) o[e] = (T)(acc[e] * inv);
+  T* dst = (T*)p.O + (long long)b * p.sO.b + (long long)h * p.sO.h + (long long)q * p.sO.s + 4 * c;
+  *(u32x2*)dst = __builtin_bit_cast(u32x2, o);
+  if (c == 0 && p.LSE)
+    p.LSE[(long long)b * p.lse_sb + (long long)h * p.lse_sh + q] = m != -INFINITY ? m + __logf(wsum) : -INFINITY;
+}
 
-extern "C" int fable_attn_fwd(FableFwdParams p, int dtype, void* stream) {
-  using namespace fa;
-  if (!p.Q || !p.K || !p.V || !p.O) return fail(FA_ERR_ARG, "fable_attn_fwd: null tensor pointer");
-  if (p.NH <= 0 || p.gqa <= 0 || p.NH % p.gqa) return fail(FA_ERR_ARG, "fable_attn_fwd: NH=%d gqa=%d", p.NH, p.gqa);
-  if (!(p.dropout_p >= 0.0f && p.dropout_p < 1.0f)) return fail(FA_ERR_ARG, "fable_attn_fwd: dropout_p=%g", p.dropout_p);
-  if ((p.cu_q == nullptr) != (p.cu_k == nullptr)) return fail(FA_ERR_ARG, "fable_attn_fwd: cu_q and cu_k go together");
-  if (!p.cu_q && p.batch <= 0) return FA_OK;
-  if (p.SQ < 0 || p.SK < 0) return fail(FA_ERR_ARG, "fable_attn_fwd: SQ=%d SK=%d", p.SQ, p.SK);
+int launch_fwd_split_combine(const FableFwdParams& p, int dtype, const FwdSplit& sp, hipStream_t st) {
+  const long long items = sp.rows * (p.HD / 4);
+  const dim3 grid((unsigned)((items + 255) / 256)), block(256);
+  if (dtype == FA_F16)
+    hipLaunchKernelGGL(fwd_split_combine_kernel<_Float16>, grid, block, 0, st, p, sp);
+  else
+    hipLaunchKernelGGL(fwd_split_combine_kernel<__bf16>, grid, block, 0, st, p, sp);
+  return launch_status("fable_attn_fwd (split merge)");
+}
+
+// checks shared by the entry points (a workspace query needs no tensor pointers); 1 when the
+// call has nothing to do
+static int fwd_check(FableFwdParams& p, int dtype, bool query, int& rc) {
+  rc = FA_OK;
+  if (!query && (!p.Q || !p.K || !p.V || !p.O))
+    return rc = fail(FA_ERR_ARG, "fable_attn_fwd: null tensor pointer"), 1;
+  if (p.NH <= 0 || p.gqa <= 0 || p.NH % p.gqa) return rc = fail(FA_ERR_ARG, "fable_attn_fwd: NH=%d gqa=%d", p.NH, p.gqa), 1;
+  if (!(p.dropout_p >= 0.0f && p.dropout_p < 1.0f)) return rc = fail(FA_ERR_ARG, "fable_attn_fwd: dropout_p=%g", p.dropout_p), 1;
+  if ((p.cu_q == nullptr) != (p.cu_k == nullptr)) return rc = fail(FA_ERR_ARG, "fable_attn_fwd: cu_q and cu_k go together"), 1;
+  if (!p.cu_q && p.batch <= 0) return 1;
+  if (p.SQ < 0 || p.SK < 0) return rc = fail(FA_ERR_ARG, "fable_attn_fwd: SQ=%d SK=%d", p.SQ, p.SK), 1;
   // A window or chunk at least as long as the sequences bounds nothing; dropping it keeps every
   // mask bound the kernels form (row + delta + window) inside 32-bit range.
   if (p.win_left >= p.SK) p.win_left = -1;
   if (p.win_right >= p.SQ) p.win_right = -1;
   if (p.attn_chunk >= p.SK) p.attn_chunk = 0;
-  hipStream_t st = (hipStream_t)stream;
-  switch (dtype) {
-    case FA_F16:
-    case FA_BF16: return dispatch_hd(p, dtype, st);
-    case FA_F32: return launch_fwd_f32(p, st);
-    default: return fail(FA_ERR_DTYPE, "fable_attn_fwd: dtype %d not implemented (fp16/bf16/fp32)", dtype);
-  }
+  if (dtype != FA_F16 && dtype != FA_BF16 && dtype != FA_F32)
+    return rc = fail(FA_ERR_DTYPE, "fable_attn_fwd: dtype %d not implemented (fp16/bf16/fp32)", dtype), 1;
+  return 0;
+}
+
+static int fwd_run(FableFwdParams p, int dtype, FwdWs& ws, hipStream_t st) {
+  int rc;
+  if (fwd_check(p, dtype, ws.query, rc)) return rc;
+  if (dtype == FA_F32) return ws.query ? FA_OK : launch_fwd_f32(p, st);
+  return dispatch_hd(p, dtype, st, ws);
+}
+
+}  // namespace fa
+
+extern "C" int fable_attn_fwd(FableFwdParams p, int dtype, void* stream) {
+  fa::FwdWs ws{nullptr, 0, false, 0};
+  return fa::fwd_run(p, dtype, ws, (hipStream_t)stream);
+}
+
+extern "C" int64_t fable_attn_fwd_ws_bytes(FableFwdParams p, int dtype) {
+  fa::FwdWs ws{nullptr, 0, true, 0};
+  if (fa::fwd_run(p, dtype, ws, nullptr) != FA_OK) return -1;
+  return ws.need;
+}
+
+extern "C" int fable_attn_fwd_ws(FableFwdParams p, int dtype, void* ws_ptr, int64_t ws_bytes, void* stream) {
+  fa::FwdWs ws{ws_ptr, ws_bytes, false, 0};
+  return fa::fwd_run(p, dtype, ws, (hipStream_t)stream);
 }

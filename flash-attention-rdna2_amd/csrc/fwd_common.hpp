@@ -76,16 +76,39 @@ __device__ __forceinline__ bool fwd_visible(const FableFwdParams& p, int i, int 
   return ok;
 }
 
+// Key split of a small forward grid (fp16/bf16, dense batches, no left window, chunk or
+// dropout): when the query tiles of a call fill few of the CUs, `n` workgroups per query tile
+// each take a contiguous share of its key tiles and write an fp32 partial O (row-major,
+// head dim p.HD) and its LSE for every row r = (b*NH + h)*SQ + q, split after split; a second
+// kernel (fwd_split_combine_kernel, fwd.hip) merges the partials into O and LSE.
+struct FwdSplit {
+  int n;           // workgroups per query tile; 1: no split, the kernel writes O and LSE itself
+  long long rows;  // B * NH * SQ
+  float* o;        // [n][rows][p.HD]
+  float* lse;      // [n][rows], natural log; -inf where a split saw no key of the row
+};
+
+// A launch request: the caller's workspace for a key split (null / too small: no split), or a
+// query for the bytes a split of this call would use (nothing is launched).
+struct FwdWs {
+  void* ptr;
+  long long bytes;
+  bool query;
+  long long need;  // out: workspace bytes of the split this call takes (0: none)
+};
+
 // the fp16/bf16 forward per kernel width (fwd_d32 ... fwd_d256.hip: head dims up to the width,
 // in steps of 8) and the fp32 forward (fwd_f32.hip), dispatched from fable_attn_fwd
-int launch_fwd_d32(const FableFwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_d64(const FableFwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_d96(const FableFwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_d128(const FableFwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_d160(const FableFwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_d192(const FableFwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_d224(const FableFwdParams& p, int dtype, hipStream_t st);
-int launch_fwd_d256(const FableFwdParams& p, int dtype, hipStream_t st);
+int launch_fwd_d32(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws);
+int launch_fwd_d64(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws);
+int launch_fwd_d96(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws);
+int launch_fwd_d128(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws);
+int launch_fwd_d160(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws);
+int launch_fwd_d192(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws);
+int launch_fwd_d224(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws);
+int launch_fwd_d256(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws);
 int launch_fwd_f32(const FableFwdParams& p, hipStream_t st);
+// merge of the key-split partials (fwd.hip)
+int launch_fwd_split_combine(const FableFwdParams& p, int dtype, const FwdSplit& sp, hipStream_t st);
 
 }  // namespace fa

@@ -4,9 +4,9 @@
 
 namespace fa {
 
-int launch_fwd_d160(const FableFwdParams& p, int dtype, hipStream_t st) {
-  if (dtype == FA_F16) return launch_fwd<_Float16, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 2, 1>>(p, st);
-  return launch_fwd<__bf16, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 2, 1>>(p, st);
+int launch_fwd_d160(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws) {
+  if (dtype == FA_F16) return launch_fwd<_Float16, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 2, 1>>(p, st, ws);
+  return launch_fwd<__bf16, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 4, 1>, FwdCfg<160, 32, 2, 1>>(p, st, ws);
 }
 
 }  // namespace fa

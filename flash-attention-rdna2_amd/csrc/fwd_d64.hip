@@ -4,9 +4,9 @@
 
 namespace fa {
 
-int launch_fwd_d64(const FableFwdParams& p, int dtype, hipStream_t st) {
-  if (dtype == FA_F16) return launch_fwd<_Float16, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 4, 2>, FwdCfg<64, 64, 4, 2>>(p, st);
-  return launch_fwd<__bf16, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 4, 2>, FwdCfg<64, 64, 4, 2>>(p, st);
+int launch_fwd_d64(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs& ws) {
+  if (dtype == FA_F16) return launch_fwd<_Float16, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 4, 2>, FwdCfg<64, 64, 4, 2>>(p, st, ws);
+  return launch_fwd<__bf16, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 8, 2>, FwdCfg<64, 64, 4, 2>, FwdCfg<64, 64, 4, 2>>(p, st, ws);
 }
 
 }  // namespace fa

@@ -64,7 +64,7 @@ struct FwdCfg {
 template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-fwd_kernel(FableFwdParams p, int nqt) {
+fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
   // K/V rings of NST stages, a barrier every BP tiles. Iteration t reads K tile t+1 and V tile t
@@ -83,8 +83,10 @@ fwd_kernel(FableFwdParams p, int nqt) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
 
-  // ---- work item -> (sequence z, head h, q tile)
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nqt, p.gqa, kFwdUMajor);
+  // ---- work item -> (sequence z, head h, q tile), and the key split (grid split-major)
+  const int nitems = gridDim.x / sp.n;
+  const int split = blockIdx.x / nitems;
+  const int w = xcd_group_remap(blockIdx.x - split * nitems, nitems, nqt, p.gqa, kFwdUMajor);
   const int qti = w % nqt, zh = w / nqt;
   const int h = zh % p.NH, z = zh / p.NH;
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
@@ -109,8 +111,14 @@ fwd_kernel(FableFwdParams p, int nqt) {
   const bool wave_rows = qw < SQ;
   int wk0 = 0, wk1 = 0;
   if (wave_rows) key_range<CAUSAL, FEAT>(p, qw, min(qw + 32 * QB, SQ) - 1, delta, SK, wk0, wk1);
-  const int kstart = (bk0 / C::BC) * C::BC;
-  const int ntiles = bk1 > bk0 ? (bk1 - kstart + C::BC - 1) / C::BC : 0;
+  int kstart = (bk0 / C::BC) * C::BC;
+  int ntiles = bk1 > bk0 ? (bk1 - kstart + C::BC - 1) / C::BC : 0;
+  if (sp.n > 1) {  // this workgroup's share of the key tiles: a contiguous run of them
+    const int per = (ntiles + sp.n - 1) / sp.n;
+    const int t0 = min(split * per, ntiles), t1 = min(t0 + per, ntiles);
+    kstart += t0 * C::BC;
+    ntiles = t1 - t0;
+  }
 
   // ---- Q (B operands) in registers: lane holds query qw + 32i + l32, head-dim 16ds + 8hh..+7.
   // A head dim p.HD below the kernel's C::HD (a multiple of 8) runs with zero columns
@@ -692,12 +700,20 @@ fwd_kernel(FableFwdParams p, int nqt) {
     if (BP == 1 || t % BP == BP - 1) __syncthreads();
   }
 
-  // ---- epilogue: O = acc / l, LSE
+  // ---- epilogue: O = acc / l, LSE (a key split: the fp32 partial O and LSE of its keys)
 #pragma unroll
   for (int i = 0; i < QB; i++) {
     const int qi = qw + 32 * i + l32;
     const float l_tot = half_sum(l_run[i]);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
+    if (sp.n > 1) {
+      const long long r = (long long)split * sp.rows + ((long long)z * p.NH + h) * SQ + qi;
+#pragma unroll
+      for (int db = 0; db < C::NDB; db++)
+        store_cblock_f32(sp.o + r * HDr + db * 32, oacc[i][db], inv, hh, qi < SQ, HDr - db * 32);
+      if (qi < SQ && hh == 0) sp.lse[r] = l_tot > 0.0f ? m_run[i] * kLn2 + __logf(l_tot) : -INFINITY;
+      continue;
+    }
     T* orow = Og + (long long)qi * p.sO.s;
 #pragma unroll
     for (int db = 0; db < C::NDB; db++)
@@ -722,8 +738,24 @@ struct CfgTag {
   using type = K;
 };
 
+// Key split of a small grid: splits per query tile when the tiles fill at most half the CUs,
+// up to one workgroup per CU, at least kSplitMinTiles key tiles per split, at most 16.
+constexpr long long kSplitSlots = 256;
+constexpr int kSplitMinTiles = 4;
+
+template <class K>
+static int fwd_split_count(const FableFwdParams& p, long long nblk) {
+  if (p.cu_q || p.dropout_p > 0.0f || p.win_left >= 0 || p.attn_chunk > 0) return 1;
+  if (nblk <= 0 || 2 * nblk > kSplitSlots) return 1;
+  const int tiles = (p.SK + K::BC - 1) / K::BC;  // the most any query tile reads
+  long long n = (kSplitSlots + nblk - 1) / nblk;
+  n = n < tiles / kSplitMinTiles ? n : tiles / kSplitMinTiles;
+  n = n < 16 ? n : 16;
+  return n >= 2 ? (int)n : 1;
+}
+
 template <typename T, class C, class CF, class CN, class CS = C>
-static int launch_fwd(const FableFwdParams& p, hipStream_t st) {
+static int launch_fwd(const FableFwdParams& p, hipStream_t st, FwdWs& ws) {
   const bool drop = p.dropout_p > 0.0f;
   const bool feat = drop || p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
                     p.win_left >= 0 || (p.win_right >= 0 && !(p.win_right == 0 && p.causal));
@@ -735,11 +767,30 @@ static int launch_fwd(const FableFwdParams& p, hipStream_t st) {
     using K = typename decltype(cfg)::type;
     const int nqt = (p.SQ + K::BR - 1) / K::BR;
     const long long nblk = (long long)nqt * p.NH * p.batch;
+    FwdSplit sp{1, 0, nullptr, nullptr};
+    const int n = fwd_split_count<K>(p, nblk);
+    if (n > 1) {
+      const long long rows = (long long)p.batch * p.NH * p.SQ;
+      const long long obytes = ((long long)n * rows * p.HD * 4 + 255) / 256 * 256;
+      const long long need = obytes + (long long)n * rows * 4;
+      if (ws.query) {
+        ws.need = need;
+        return FA_OK;
+      }
+      if (ws.ptr && ws.bytes >= need && ((uintptr_t)ws.ptr & 255) == 0)
+        sp = FwdSplit{n, rows, (float*)ws.ptr, (float*)((char*)ws.ptr + obytes)};
+    }
+    if (ws.query) {
+      ws.need = 0;
+      return FA_OK;
+    }
     if (nblk <= 0) return FA_OK;
-    if (nblk > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_fwd: grid too large");
+    if (nblk * sp.n > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_fwd: grid too large");
     hipLaunchKernelGGL((fwd_kernel<T, K, decltype(causal)::value, decltype(ft)::value, decltype(dr)::value>),
-                       dim3((unsigned)nblk), dim3(K::NT), 0, st, p, nqt);
-    return launch_status("fable_attn_fwd");
+                       dim3((unsigned)(nblk * sp.n)), dim3(K::NT), 0, st, p, nqt, sp);
+    const int rc = launch_status("fable_attn_fwd");
+    if (rc != FA_OK || sp.n == 1) return rc;
+    return launch_fwd_split_combine(p, std::is_same<T, _Float16>::value ? FA_F16 : FA_BF16, sp, st);
   };
   auto pick = [&](auto causal) -> int {
     using Y = std::integral_constant<bool, true>;

@@ -193,8 +193,20 @@ def fwd(q, k, v, scale, causal, win_left, win_right, softcap, alibi, dropout_p, 
                        float(dropout_p), int(seed) & ((1 << 64) - 1), None, None, B, int(attn_chunk),
                        None, None, Hq * SQ, SQ)
     with _on(q.device):
-        _lib.check(_L.fable_attn_fwd(p, _dt(q), _stream(q)), "fable_attn_fwd")
+        _launch_fwd(p, _dt(q), q.device, _stream(q))
     return out, lse
+
+
+def _launch_fwd(p, dt, device, stream, ws_bytes=None):
+    """fable_attn_fwd, or fable_attn_fwd_ws with a fresh workspace when the library splits this
+    call's keys (a small grid); ws_bytes: the library's answer, when the caller has it cached."""
+    if ws_bytes is None:
+        ws_bytes = _L.fable_attn_fwd_ws_bytes(p, dt)
+    if ws_bytes > 0:
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        _lib.check(_L.fable_attn_fwd_ws(p, dt, ws.data_ptr(), ws_bytes, stream), "fable_attn_fwd")
+    else:
+        _lib.check(_L.fable_attn_fwd(p, dt, stream), "fable_attn_fwd")
 
 
 def fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win_right, softcap,

@@ -16,7 +16,7 @@ LIB_PATH = os.path.join(_HERE, "libfable_attn_hip.so")
 FA_F16, FA_BF16, FA_F32 = 0, 1, 2
 FA_OK = 0
 
-ABI_VERSION = 4  # FABLE_ATTN_ABI_VERSION of include/fable_attn_abi.h
+ABI_VERSION = 5  # FABLE_ATTN_ABI_VERSION of include/fable_attn_abi.h
 
 c_i32, c_i64, c_u64, c_f32, c_ptr = (ctypes.c_int32, ctypes.c_int64, ctypes.c_uint64,
                                      ctypes.c_float, ctypes.c_void_p)
@@ -118,7 +118,7 @@ STRUCTS = {0: FableFwdParams, 1: FableBwdParams, 2: FableDecParams, 3: CombinePa
 
 # exported symbols of libfable_attn_hip.so (the C-ABI surface)
 EXPORTS = ("fa_forward_launch", "fable_attn_backward_launch", "fa_decode_launch",
-           "fable_attn_fwd", "fable_attn_bwd", "fable_attn_dec", "fable_attn_dec_noalloc",
+           "fable_attn_fwd", "fable_attn_fwd_ws", "fable_attn_fwd_ws_bytes", "fable_attn_bwd", "fable_attn_dec", "fable_attn_dec_noalloc",
            "fable_attn_dec_noalloc_max_floats",
            "fa_decode_num_splits", "fa_combine_launch", "fable_attn_bwd_ds_bytes",
            "fable_attn_abi_version", "fable_attn_struct_size", "fable_attn_last_error")
@@ -137,6 +137,9 @@ def load():
             "`python flash-attention-rdna2_amd/build.py` (no CPU fallback exists)")
     lib = ctypes.CDLL(LIB_PATH)
     lib.fable_attn_fwd.argtypes = [FableFwdParams, c_i32, c_ptr]
+    lib.fable_attn_fwd_ws.argtypes = [FableFwdParams, c_i32, c_ptr, c_i64, c_ptr]
+    lib.fable_attn_fwd_ws_bytes.argtypes = [FableFwdParams, c_i32]
+    lib.fable_attn_fwd_ws_bytes.restype = c_i64
     lib.fable_attn_bwd.argtypes = [FableBwdParams, c_i32, c_ptr]
     lib.fable_attn_dec.argtypes = [FableDecParams, c_i32, c_ptr, c_ptr, c_ptr]
     lib.fa_decode_num_splits.argtypes = [c_i32, c_i32, c_i32, c_i32, c_i64, c_i32]
@@ -146,7 +149,7 @@ def load():
     lib.fa_decode_launch.argtypes = [RefDecParams, c_i32, c_ptr, c_ptr, c_ptr]
     lib.fable_attn_dec_noalloc.argtypes = [FableDecParams, c_i32, c_ptr, c_ptr, c_ptr]
     lib.fable_attn_dec_noalloc_max_floats.restype = c_i64
-    for f in ("fable_attn_fwd", "fable_attn_bwd", "fable_attn_dec", "fable_attn_dec_noalloc",
+    for f in ("fable_attn_fwd", "fable_attn_fwd_ws", "fable_attn_bwd", "fable_attn_dec", "fable_attn_dec_noalloc",
               "fa_forward_launch",
               "fable_attn_backward_launch", "fa_decode_launch",
               "fa_decode_num_splits", "fa_combine_launch", "fable_attn_abi_version"):

@@ -341,7 +341,8 @@ def _infer_plan(q, k, v, softmax_scale, causal, window_size, softcap):
     p = _lib.FableFwdParams(0, 0, 0, 0, None, bhs(q), bhs(k), bhs(v), o, SQ, SK, D, Hq, Hq // Hk,
                             spec.scale, spec.softcap, spec.wl, spec.wr, None, spec.causal, 0.0, 0,
                             None, None, B, 0, None, None, 0, 0)
-    return p, _C._dt(q), (B, SQ, Hq, D)
+    dt = _C._dt(q)
+    return p, dt, (B, SQ, Hq, D), int(_C._L.fable_attn_fwd_ws_bytes(p, dt))
 
 
 def _infer_fast(q, k, v, softmax_scale, causal, window_size, softcap):
@@ -372,11 +373,10 @@ def _infer_fast(q, k, v, softmax_scale, causal, window_size, softcap):
     dev = q.device.index
     if (qp | kp | vp) & 15 or dev != torch._C._cuda_getDevice():
         return None
-    p, dt, shape = plan
+    p, dt, shape, ws_bytes = plan
     out = torch.empty(shape, dtype=q.dtype, device=q.device)
     p.Q, p.K, p.V, p.O = qp, kp, vp, out.data_ptr()
-    _lib.check(_C._L.fable_attn_fwd(p, dt, ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(dev))),
-               "fable_attn_fwd")
+    _C._launch_fwd(p, dt, q.device, ctypes.c_void_p(torch._C._cuda_getCurrentRawStream(dev)), ws_bytes)
     return out
 
 

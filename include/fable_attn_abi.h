@@ -43,7 +43,7 @@
 extern "C" {
 #endif
 
-#define FABLE_ATTN_ABI_VERSION 4
+#define FABLE_ATTN_ABI_VERSION 5
 
 /* dtype codes, same values as the reference (fa_forward.hip:403, backward.hip:25) */
 enum { FA_F16 = 0, FA_BF16 = 1, FA_F32 = 2 };
@@ -284,6 +284,17 @@ typedef struct CombineParams {
 
 /* the forward (reference launcher kernels/fa_forward.hip:424-451); dense or packed varlen */
 int fable_attn_fwd(FableFwdParams p, int dtype, void* stream);
+
+/* The forward with a caller-owned workspace for a key split: when the query tiles of a call fill
+ * few of the CUs (fp16/bf16, dense batches, no left window, chunk or dropout), several workgroups
+ * per query tile each take a share of its keys, write fp32 partials to `ws`, and a second kernel
+ * merges them into O and LSE. fable_attn_fwd_ws_bytes gives the bytes this call would use (0: no
+ * split for this call; -1: the call is invalid, see fable_attn_last_error); a `ws` that is NULL,
+ * smaller, or not 256-byte aligned runs the call unsplit. Same results as fable_attn_fwd up to
+ * fp32 summation order. No reference counterpart (the reference launches one workgroup per query
+ * tile, kernels/fa_forward.hip:424-451); added for short sequences with few heads. */
+int64_t fable_attn_fwd_ws_bytes(FableFwdParams p, int dtype);
+int fable_attn_fwd_ws(FableFwdParams p, int dtype, void* ws, int64_t ws_bytes, void* stream);
 
 /* the backward (reference launcher kernels/backward.hip:508-521); dense or packed varlen */
 int fable_attn_bwd(FableBwdParams p, int dtype, void* stream);

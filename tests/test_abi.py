@@ -90,7 +90,7 @@ def test_library_exports_every_declared_function():
     assert set(declared) == set(_lib.EXPORTS), declared
     for f in declared:
         assert hasattr(lib, f), f
-    assert lib.fable_attn_abi_version() == _lib.ABI_VERSION == 4
+    assert lib.fable_attn_abi_version() == _lib.ABI_VERSION == 5
     for k, st in _lib.STRUCTS.items():
         assert lib.fable_attn_struct_size(k) == ctypes.sizeof(st)
 
@@ -196,3 +196,39 @@ def test_bwd_ds_workspace_size():
         p.B, p.Hq, p.SQ, p.SK, p.causal, p.win_left, p.win_right = 1, 3, SQ, SK, causal, wl, wr
         got = lib.fable_attn_bwd_ds_bytes(p, 0)
         assert got == hdr(SK) + 3 * _visible_tiles(SQ, SK, causal, wl, wr) * 2048, (SQ, SK, causal, wl, wr)
+
+
+def _fwd_params(B, H, SQ, SK, D, gqa=1, causal=False, wl=-1, wr=-1, softcap=0.0, chunk=0,
+                dropout=0.0, varlen=False):
+    """FableFwdParams of a dense [B,H,S,D] call, tensor pointers left null (a workspace query
+    reads none)."""
+    from fable_attn import _lib
+    s = lambda S, Hh: _lib.Strides(S * Hh * D, D, Hh * D)
+    cu = ctypes.c_void_p(16) if varlen else None
+    return _lib.FableFwdParams(None, None, None, None, None, s(SQ, H), s(SK, H // gqa), s(SK, H // gqa),
+                               s(SQ, H), SQ, SK, D, H, gqa, D ** -0.5, softcap, wl, wr, None,
+                               1 if causal else 0, dropout, 0, cu, cu, B, chunk, None, None, H * SQ, SQ)
+
+
+def test_forward_key_split_workspace_query():
+    """fable_attn_fwd_ws_bytes: the key split of small grids (host logic only, no launch). C1
+    (64 query tiles of 128 rows on 256 CUs) splits in 4: fp32 partial O and LSE of every row per
+    split; the large grids, left windows, chunks, dropout, varlen and fp32 never split; an
+    invalid call answers -1."""
+    from fable_attn import _lib
+    lib = _lib.load()
+    q = lambda dt=0, **kw: lib.fable_attn_fwd_ws_bytes(_fwd_params(**kw), dt)
+    rows = 1 * 8 * 1024
+    assert q(B=1, H=8, SQ=1024, SK=1024, D=64) == (4 * rows * 64 * 4 + 255) // 256 * 256 + 4 * rows * 4
+    assert q(1, B=1, H=8, SQ=1024, SK=1024, D=64) > 0                      # bf16 alike
+    assert q(B=1, H=32, SQ=16384, SK=16384, D=128, causal=True) == 0       # C2: a full grid
+    assert q(B=2, H=32, SQ=4096, SK=4096, D=128, causal=True) == 0
+    assert q(B=1, H=2, SQ=1500, SK=1500, D=128, causal=True) > 0
+    assert q(B=1, H=8, SQ=1024, SK=1024, D=64, wl=100) == 0                # left window
+    assert q(B=1, H=8, SQ=1024, SK=1024, D=64, chunk=256) == 0
+    assert q(B=1, H=8, SQ=1024, SK=1024, D=64, dropout=0.1) == 0
+    assert q(B=1, H=8, SQ=1024, SK=1024, D=64, varlen=True) == 0
+    assert q(2, B=1, H=8, SQ=1024, SK=1024, D=64) == 0                     # fp32
+    assert q(B=1, H=8, SQ=256, SK=256, D=64) == 0                          # too few key tiles
+    assert q(B=1, H=8, SQ=1024, SK=1024, D=60) == -1                       # no kernel for D=60
+    assert b"head_dim=60" in lib.fable_attn_last_error()

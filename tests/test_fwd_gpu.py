@@ -309,3 +309,74 @@ def test_softcap_polynomial_range(case, dt):
     assert np.isfinite(o).all()
     assert rel <= TOL[dt], f"rel_rms {rel:.3e} > {TOL[dt]}"
     assert inf_ok and lerr <= LSE_ABS, f"LSE abs err {lerr:.3e}"
+
+
+# Small grids whose keys the library splits over several workgroups per query tile (fp32
+# partials merged by a second kernel): causal with splits that see no key, SQ < SK and SQ > SK
+# (empty rows), GQA, alibi, softcap on the one-wave D=256 loop, a right-only window, head dims
+# that leave zero columns. Same case layout as CASES.
+SPLIT_CASES = [
+    ("split d128 causal", 1, 1500, 1500, 128, 2, 1, True, -1, -1, 0.0, False, 0),
+    ("split d64 full SQ<SK GQA", 1, 100, 3000, 64, 4, 2, False, -1, -1, 0.0, False, 0),
+    ("split d256 causal softcap", 1, 700, 700, 256, 2, 1, True, -1, -1, 30.0, False, 0),
+    ("split d96 causal SQ<SK alibi", 1, 200, 900, 96, 2, 2, True, -1, -1, 0.0, True, 0),
+    ("split d128 window (-1,40)", 1, 1200, 1200, 128, 1, 1, False, -1, 40, 0.0, False, 0),
+    ("split d64 causal SQ>SK empty rows B2", 2, 600, 520, 64, 2, 1, True, -1, -1, 0.0, False, 0),
+    ("split d80 full", 1, 300, 2100, 80, 3, 1, False, -1, -1, 0.0, False, 0),
+]
+
+
+def _split_bytes(case, dt):
+    from fable_attn import _C, _lib
+    name, B, SQ, SK, D, H, gqa, causal, wl, wr, sc, alibi, chunk = case
+    s = lambda S, Hh: _lib.Strides(S * Hh * D, D, Hh * D)
+    p = _lib.FableFwdParams(None, None, None, None, None, s(SQ, H), s(SK, H // gqa), s(SK, H // gqa),
+                            s(SQ, H), SQ, SK, D, H, gqa, D ** -0.5, sc, wl, wr, None, 1 if causal else 0,
+                            0.0, 0, None, None, B, chunk, None, None, H * SQ, SQ)
+    return _C._L.fable_attn_fwd_ws_bytes(p, 0 if dt == "f16" else 1)
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
+def test_forward_key_split_parity(case, dt):
+    print(f"[fwd-split] {case[0]} {dt}", flush=True)
+    assert _split_bytes(case, dt) > 0, "the case must take the key split"
+    o, l, o_ref, l_ref = run_case(case, dt)
+    rel = orc.rel_rms(o, o_ref)
+    lerr, inf_ok = lse_err(l, l_ref)
+    log_errors("fwd_split", case[0], dt, o=rel, lse=lerr)
+    assert np.isfinite(o).all(), "non-finite output"
+    assert rel <= TOL[dt], f"rel_rms {rel:.3e} > {TOL[dt]}"
+    assert inf_ok, "empty-row LSE (-inf) pattern differs"
+    assert lerr <= LSE_ABS, f"LSE abs err {lerr:.3e}"
+    empty = np.isneginf(l_ref)
+    if empty.any():
+        rows = np.broadcast_to(empty[..., None], o.shape)
+        assert (o[rows] == 0).all(), "empty rows must be exactly zero"
+
+
+def test_forward_key_split_matches_unsplit():
+    """The split and the unsplit kernels on the same inputs (a workspace that is too small
+    runs the call unsplit): equal to fp32 summation order."""
+    import torch
+
+    from fable_attn import _C, _lib
+    case = SPLIT_CASES[0]
+    name, B, SQ, SK, D, H, gqa, causal, wl, wr, sc, alibi, chunk = case
+    q, k, v = (to_dev(gen((B, H, n, D), 7 + i, "f16"), "f16") for i, n in enumerate((SQ, SK, SK)))
+    outs = []
+    for split in (True, False):
+        out = torch.empty_like(q)
+        lse = torch.empty((B, H, SQ), dtype=torch.float32, device="cuda")
+        s = lambda t: _lib.Strides(t.stride(0), t.stride(1), t.stride(2))
+        p = _lib.FableFwdParams(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), lse.data_ptr(),
+                                s(q), s(k), s(v), s(out), SQ, SK, D, H, gqa, D ** -0.5, 0.0, -1, -1, None,
+                                1, 0.0, 0, None, None, B, 0, None, None, H * SQ, SQ)
+        need = _C._L.fable_attn_fwd_ws_bytes(p, 0)
+        assert need > 0
+        ws = torch.empty(need if split else need - 256, dtype=torch.uint8, device="cuda")
+        _lib.check(_C._L.fable_attn_fwd_ws(p, 0, ws.data_ptr(), ws.numel(), None), "fable_attn_fwd_ws")
+        torch.cuda.synchronize()
+        outs.append((to_np(out), to_np(lse)))
+    assert np.abs(outs[0][0] - outs[1][0]).max() <= 2e-3
+    assert np.abs(outs[0][1] - outs[1][1]).max() <= 1e-5
