@@ -739,15 +739,20 @@ struct CfgTag {
 };
 
 // Key split of a small grid: splits per query tile when the tiles fill at most half the CUs,
-// up to one workgroup per CU, at least kSplitMinTiles key tiles per split, at most 16.
+// up to one workgroup per CU, at least kSplitMinTiles key tiles per split, at most 16. A causal
+// grid of one round (at most one workgroup per CU) with rows of kSplitLongRow key tiles or more
+// splits in two: its longest rows set the time (B1 H8 S8192 D128 1.27-1.30x, H6 1.17x, H4
+// S16384 1.12x); with shorter rows the halves of a grid over 128 workgroups take a second round
+// (H12 S4096, 64 tiles: 0.87x).
 constexpr long long kSplitSlots = 256;
-constexpr int kSplitMinTiles = 4;
+constexpr int kSplitMinTiles = 4, kSplitLongRow = 128;
 
 template <class K>
 static int fwd_split_count(const FableFwdParams& p, long long nblk) {
   if (p.cu_q || p.dropout_p > 0.0f || p.win_left >= 0 || p.attn_chunk > 0) return 1;
-  if (nblk <= 0 || 2 * nblk > kSplitSlots) return 1;
+  if (nblk <= 0) return 1;
   const int tiles = (p.SK + K::BC - 1) / K::BC;  // the most any query tile reads
+  if (2 * nblk > kSplitSlots) return (p.causal && nblk <= kSplitSlots && tiles >= kSplitLongRow) ? 2 : 1;
   long long n = (kSplitSlots + nblk - 1) / nblk;
   n = n < tiles / kSplitMinTiles ? n : tiles / kSplitMinTiles;
   n = n < 16 ? n : 16;

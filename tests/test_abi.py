@@ -224,6 +224,13 @@ def test_forward_key_split_workspace_query():
     assert q(B=1, H=32, SQ=16384, SK=16384, D=128, causal=True) == 0       # C2: a full grid
     assert q(B=2, H=32, SQ=4096, SK=4096, D=128, causal=True) == 0
     assert q(B=1, H=2, SQ=1500, SK=1500, D=128, causal=True) > 0
+    # one round of causal workgroups: split in two only with rows of 128 key tiles or more
+    two = lambda S, H: (2 * H * S * 128 * 4 + 255) // 256 * 256 + 2 * H * S * 4
+    assert q(B=1, H=6, SQ=8192, SK=8192, D=128, causal=True) == two(8192, 6)
+    assert q(B=1, H=8, SQ=8192, SK=8192, D=128, causal=True) == two(8192, 8)
+    assert q(B=1, H=12, SQ=4096, SK=4096, D=128, causal=True) == 0            # 64-tile rows
+    assert q(B=1, H=16, SQ=8192, SK=8192, D=128, causal=False) == 0           # not causal
+    assert q(B=1, H=16, SQ=8192, SK=8192, D=128, causal=True) == 0            # two rounds
     assert q(B=1, H=8, SQ=1024, SK=1024, D=64, wl=100) == 0                # left window
     assert q(B=1, H=8, SQ=1024, SK=1024, D=64, chunk=256) == 0
     assert q(B=1, H=8, SQ=1024, SK=1024, D=64, dropout=0.1) == 0

@@ -211,6 +211,9 @@ def _check_rows(test, case, dt, got_o, got_lse, o_ref, l_ref, rows):
     ("C2 causal fp16 B1 S8192 H32", 1, 8192, 32, True, "f16"),
     ("C2 causal fp16 B1 S4096 H32", 1, 4096, 32, True, "f16"),
     ("full bf16 B2 S8192 H32", 2, 8192, 32, False, "bf16"),
+    # one round of causal workgroups with long rows: keys split in two
+    ("key split causal fp16 B1 S8192 H6", 1, 8192, 6, True, "f16"),
+    ("key split causal bf16 B1 S16384 H4", 1, 16384, 4, True, "bf16"),
 ], ids=lambda c: c[0])
 def test_forward_full_size_sampled_rows(cfg):
     """BASELINE.json configs[1] at its full size and its S=8192 / S=4096 variants (and a
