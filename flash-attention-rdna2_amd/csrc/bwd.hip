@@ -35,7 +35,7 @@ static void normalize_windows(FableBwdParams& p) {
 }  // namespace fa
 
 extern "C" int64_t fable_attn_bwd_ds_bytes(FableBwdParams p, int dtype) {
-  if ((dtype != FA_F16 && dtype != FA_BF16) || p.D <= 0 || p.D % 8 || fa::bwd_width(p.D) > 128 || p.B <= 0 ||
+  if ((dtype != FA_F16 && dtype != FA_BF16) || p.D <= 0 || p.D % 8 || fa::bwd_width(p.D) > 256 || p.B <= 0 ||
       p.Hq <= 0)
     return 0;
   fa::normalize_windows(p);

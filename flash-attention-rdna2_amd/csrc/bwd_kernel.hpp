@@ -16,7 +16,7 @@
 //     S = Q.K^T and dP = dO.V^T; P and dS stay in registers as B operands of
 //     dV^T += dO^T.P and dK^T += Q^T.dS (dO^T/Q^T by transposing LDS reads).
 // On that recomputing path S and dP are computed in both kernels (the price of no atomics, as in
-// the reference). With a dS workspace (FableBwdParams.ds_ws, fp16/bf16 at kernel widths up to 128) the order
+// the reference). With a dS workspace (FableBwdParams.ds_ws, fp16/bf16, every kernel width) the order
 // is instead: a rowsum kernel for D, the dK/dV kernel, which also stores each dS tile once, and
 // a dQ kernel that forms dQ = dS.K from the stored tiles; every product is computed once, still
 // without atomics and in a fixed order.
@@ -267,7 +267,7 @@ struct BwdKVCfg {
   static constexpr int PER = (CH + NT - 1) / NT;
 };
 
-template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false>
+template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false, bool DSW = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
 bwd_dkdv_kernel(FableBwdParams p, int nkt) {
@@ -320,6 +320,18 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
   const int ntq = bq1 > bq0 ? (bq1 - qstart + C::BQ - 1) / C::BQ : 0;
   const int total = ntq * p.gqa;
   const float c_log2 = p.scale * kLog2e;
+  // dS workspace (the head-dim pass 0 of each key block stores it): this wave's 32-key block
+  // in the compacted layout, a cursor over the tiles in the loop's order (q tiles of a head,
+  // then the next head), as in the pair kernel
+  T* ds_cur = nullptr;
+  long long ds_wrap = 0;
+  if constexpr (DSW) {
+    const int nkb = (p.SK + 31) >> 5;
+    const int* tbl = (const int*)p.ds_ws;
+    const int ds_T = tbl[nkb];
+    ds_cur = ds_head_tiles<T>(p, b, kvh * p.gqa, ds_T) + (long long)(tbl[min(kw >> 5, nkb - 1)] + (qstart >> 5)) * 1024;
+    ds_wrap = ((long long)ds_T - (ntq - 1)) * 1024;
+  }
 
   // Q/dO tiles through buffer descriptors over rows qt0..SQ-1 (rows past SQ read as zeros);
   // each thread's first QJ chunk slots are Q, the rest dO. The LSE/D row values are loaded
@@ -410,6 +422,13 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
           pS[r >> 3][r & 7] = (T)dsv;
         }
       }
+      if constexpr (DSW) {  // the dS tile (32 queries x this wave's 32 keys), streaming stores
+        if (dpass == 0) {
+          T* dst = ds_cur + 16 * l32 + 8 * hh;
+          __builtin_nontemporal_store(pS[0], (V8*)dst);
+          __builtin_nontemporal_store(pS[1], (V8*)(dst + 512));
+        }
+      }
       // dV^T += dO^T . P, dK^T += Q^T . dS (A operands by transposing reads of the tiles)
 #pragma unroll
       for (int db = 0; db < C::NDB; db++) {
@@ -437,6 +456,7 @@ bwd_dkdv_kernel(FableBwdParams p, int nkt) {
         }
       }
     }
+    if constexpr (DSW) ds_cur += (it % ntq) + 1 == ntq ? ds_wrap : 1024;
     lstore(stage ^ 1);
     __syncthreads();
   }
@@ -1121,8 +1141,11 @@ inline long long ds_bytes(const FableBwdParams& p) {
 // backward through the dS workspace: D rows, then dK/dV (writing dS), then dQ = dS.K
 template <typename T, class CKV, bool CAUSAL, bool FEAT, bool DROP>
 static int launch_bwd_ds(const FableBwdParams& p, hipStream_t st, int nkt) {
-  // 8 waves where a K tile's chunks split evenly over them (widths that are multiples of 64)
-  using CD = BwdDsQCfg<CKV::HD, (CKV::HD / 8) % 8 == 0 ? 8 : 4, 2, kDsqSets>;
+  // up to 128 wide: 8 waves where a K tile's chunks split evenly over them (widths that are
+  // multiples of 64); wider: 4 waves. Two waves per SIMD up to 192 wide; at 256 one (the dQ
+  // accumulators of a 256-wide row take 128 registers, the kernel 268)
+  constexpr bool kWide = CKV::HD > 128;
+  using CD = BwdDsQCfg<CKV::HD, (!kWide && (CKV::HD / 8) % 8 == 0) ? 8 : 4, (CKV::HD > 192) ? 1 : 2, kDsqSets>;
   // the D-row kernel reduces over a power-of-two count of lanes per row (chunks past the head
   // dim add zero)
   constexpr int DW = CKV::HD <= 32 ? 32 : (CKV::HD <= 64 ? 64 : (CKV::HD <= 128 ? 128 : 256));
@@ -1130,11 +1153,14 @@ static int launch_bwd_ds(const FableBwdParams& p, hipStream_t st, int nkt) {
   const long long gd = (long long)((p.SQ + RPB - 1) / RPB) * p.Hq * p.B;
   const int nqt = (p.SQ + CD::BQ - 1) / CD::BQ;
   const long long gq = (long long)nqt * p.Hq * p.B;
-  const long long gkv = (long long)nkt * p.Hk * p.B;
-  if (gd > 0x7FFFFFFF || gq > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_bwd: grid too large");
+  const long long gkv = (long long)nkt * p.Hk * p.B * CKV::DSPLIT;
+  if (gd > 0x7FFFFFFF || gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_bwd: grid too large");
   hipLaunchKernelGGL((bwd_dsum_kernel<T, DW>), dim3((unsigned)gd), dim3(256), 0, st, p, (p.SQ + RPB - 1) / RPB);
   if (int rc = launch_status("fable_attn_bwd (dsum)")) return rc;
-  hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
+  if constexpr (CKV::PAIR)
+    hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
+  else
+    hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
   if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;
   hipLaunchKernelGGL((bwd_dq_ds_kernel<T, CD, CAUSAL, FEAT>), dim3((unsigned)gq), dim3(CD::NT), 0, st, p, nqt);
   return launch_status("fable_attn_bwd (dq)");
@@ -1147,7 +1173,7 @@ static int launch_bwd2(const FableBwdParams& p, hipStream_t st) {
   const long long gq = (long long)nqt * p.Hq * p.B * CQ::DSPLIT;
   const long long gkv = (long long)nkt * p.Hk * p.B * CKV::DSPLIT;
   if (gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_bwd: grid too large");
-  if constexpr (CKV::PAIR) {
+  {
     const long long need = ds_bytes(p);
     // (the tiles are moved with 16-byte accesses: an unaligned workspace is not used)
     if (p.ds_ws && ((uintptr_t)p.ds_ws & 15) == 0 && need > 0 && p.ds_ws_bytes >= need)

@@ -21,7 +21,7 @@ Tensor checks raise RuntimeError as TORCH_CHECK does there. torch only allocates
 workspaces and supplies the current stream; all compute is in libfable_attn_hip.so. There is
 no fallback: if the library is missing, importing this module raises ImportError.
 
-Backward dS workspace: for fp16/bf16 at head dims up to 128 the backward can store dS once and
+Backward dS workspace: for fp16/bf16 at every head dim the backward can store dS once and
 form dQ = dS.K from it (FableBwdParams.ds_ws) instead of recomputing S and dP in its dQ kernel. The
 workspace holds 2 bytes per visible (query, key) pair of every q head, in 32x32 tiles (about half
 of B*Hq*SQ*SK*2 bytes under a causal mask; packed varlen batches keep the rectangle of the longest

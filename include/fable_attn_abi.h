@@ -299,9 +299,10 @@ int fable_attn_fwd_ws(FableFwdParams p, int dtype, void* ws, int64_t ws_bytes, v
 /* the backward (reference launcher kernels/backward.hip:508-521); dense or packed varlen */
 int fable_attn_bwd(FableBwdParams p, int dtype, void* stream);
 
-/* Bytes of FableBwdParams.ds_ws the backward can use for these shapes (0: this head dim / dtype has
- * no dS-workspace path). No reference counterpart: the reference backward recomputes dS in its
- * dQ kernel (backward.hip:298-387). Size B*Hq*ceil(SQ/32)*ceil(SK/32)*2 KiB for fp16/bf16. */
+/* Bytes of FableBwdParams.ds_ws the backward can use for these shapes (fp16/bf16 at every head
+ * dim; 0 for fp32, which recomputes, or when no query sees a key). No reference counterpart: the
+ * reference backward recomputes dS in its dQ kernel (backward.hip:298-387). A 256-byte table,
+ * then 2 KiB per 32x32 (query, key) tile holding a visible pair, for every (batch, q head). */
 int64_t fable_attn_bwd_ds_bytes(FableBwdParams p, int dtype);
 
 /* paged-KV decode (reference launcher kernels/fa_decode.hip:343-362).

@@ -166,7 +166,7 @@ def _visible_tiles(SQ, SK, causal, wl=-1, wr=-1):
 def test_bwd_ds_workspace_size():
     """fable_attn_bwd_ds_bytes: a 256-byte-padded table of ceil(SK/32)+1 ints, then 2 KiB per
     (32-query, 32-key) tile that holds a visible pair, for every (batch, q head), for the
-    fp16/bf16 head dims with a dS-workspace path (up to 128); 0 elsewhere (host-only call).
+    fp16/bf16 head dims (every multiple of 8 up to 256); 0 elsewhere (host-only call).
     The tile count is checked against a brute-force count over the pair mask."""
     from fable_attn import _lib
     lib = _lib.load()
@@ -184,9 +184,11 @@ def test_bwd_ds_workspace_size():
     for d in (8, 16, 32, 96, 120):                         # widths 32 and 96 have the path too
         p.D = d
         assert lib.fable_attn_bwd_ds_bytes(p, 1) == want, d
-    for d in (136, 160, 192, 224, 256):                    # one-wave-per-SIMD widths recompute
+    for d in (136, 160, 192, 224, 256):                    # the one-wave-per-SIMD widths too
         p.D = d
-        assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0, d
+        assert lib.fable_attn_bwd_ds_bytes(p, 0) == want, d
+    p.D = 264                                               # past 256: no kernel at all
+    assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0
     p.D, p.SQ = 128, 0
     assert lib.fable_attn_bwd_ds_bytes(p, 0) == 0
     # causal and windowed: only the tiles with a visible pair
