@@ -301,8 +301,9 @@ int fable_attn_bwd(FableBwdParams p, int dtype, void* stream);
 
 /* Bytes of FableBwdParams.ds_ws the backward can use for these shapes (fp16/bf16 at every head
  * dim; 0 for fp32, which recomputes, or when no query sees a key). No reference counterpart: the
- * reference backward recomputes dS in its dQ kernel (backward.hip:298-387). A 256-byte table,
- * then 2 KiB per 32x32 (query, key) tile holding a visible pair, for every (batch, q head). */
+ * reference backward recomputes dS in its dQ kernel (backward.hip:298-387). A table of
+ * ceil(SK/32)+1 ints padded to a multiple of 256 bytes, then 2 KiB per 32x32 (query, key) tile
+ * holding a visible pair, for every (batch, q head). */
 int64_t fable_attn_bwd_ds_bytes(FableBwdParams p, int dtype);
 
 /* paged-KV decode (reference launcher kernels/fa_decode.hip:343-362).
