@@ -1151,8 +1151,12 @@ static int launch_bwd_ds(const FableBwdParams& p, hipStream_t st, int nkt) {
   constexpr int DW = CKV::HD <= 32 ? 32 : (CKV::HD <= 64 ? 64 : (CKV::HD <= 128 ? 128 : 256));
   constexpr int RPB = 256 / (DW / 8) * DSUM_RPT;  // rows per dsum workgroup
   const long long gd = (long long)((p.SQ + RPB - 1) / RPB) * p.Hq * p.B;
+  // grids of fewer 8-wave workgroups than CUs run 4-wave ones (twice as many, half the rows)
+  using CDS = BwdDsQCfg<CKV::HD, 4, CD::WPE, kDsqSets>;
   const int nqt = (p.SQ + CD::BQ - 1) / CD::BQ;
-  const long long gq = (long long)nqt * p.Hq * p.B;
+  const bool small = CD::NW == 8 && (long long)nqt * p.Hq * p.B < 256;
+  const int nqts = (p.SQ + CDS::BQ - 1) / CDS::BQ;
+  const long long gq = (long long)(small ? nqts : nqt) * p.Hq * p.B;
   const long long gkv = (long long)nkt * p.Hk * p.B * CKV::DSPLIT;
   if (gd > 0x7FFFFFFF || gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_bwd: grid too large");
   hipLaunchKernelGGL((bwd_dsum_kernel<T, DW>), dim3((unsigned)gd), dim3(256), 0, st, p, (p.SQ + RPB - 1) / RPB);
@@ -1162,6 +1166,12 @@ static int launch_bwd_ds(const FableBwdParams& p, hipStream_t st, int nkt) {
   else
     hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
   if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;
+  if constexpr (CD::NW == 8) {
+    if (small) {
+      hipLaunchKernelGGL((bwd_dq_ds_kernel<T, CDS, CAUSAL, FEAT>), dim3((unsigned)gq), dim3(CDS::NT), 0, st, p, nqts);
+      return launch_status("fable_attn_bwd (dq)");
+    }
+  }
   hipLaunchKernelGGL((bwd_dq_ds_kernel<T, CD, CAUSAL, FEAT>), dim3((unsigned)gq), dim3(CD::NT), 0, st, p, nqt);
   return launch_status("fable_attn_bwd (dq)");
 }
