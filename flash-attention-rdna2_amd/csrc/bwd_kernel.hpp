@@ -486,6 +486,15 @@ __device__ __forceinline__ void for_sets(std::integer_sequence<int, I...>, F&& f
 // one's VALU work overlaps the other's MFMAs. The Q/dO tiles sit in a 4-stage LDS ring (the
 // S-wave reads tile t, the dP-wave tile t-1, tile t+1 is stored) and tiles t+2 .. t+NSET are in
 // flight in the S-waves' registers; one barrier per tile.
+// Query split of the pair dK/dV kernel on a grid of one round (dS-workspace path, dense
+// batches): `n` workgroups per key block each take a contiguous run of its query tiles and
+// write fp32 partial dK and dV rows; bwd_split_merge_kernel sums them in share order.
+struct BwdSplit {
+  int n;           // shares per key block; 1: no split, the kernel writes dK and dV itself
+  long long rows;  // B * Hk * SK
+  float* part;     // [n][dK | dV][rows][p.D]
+};
+
 template <int HD_, int NP_, int NSET_>
 struct BwdKVPCfg {
   static constexpr bool PAIR = true;
@@ -513,7 +522,7 @@ struct BwdKVPCfg {
 template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false, bool DSW = false>
 __global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
                           amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
+bwd_dkdv_pair_kernel(FableBwdParams p, int nkt, BwdSplit sp) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
   __shared__ __attribute__((aligned(16))) T lds[4 * C::STAGE];
@@ -525,7 +534,10 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   const bool dpw = wave >= C::NP;  // dP-wave (holds V, accumulates dK)
   const int pair = dpw ? wave - C::NP : wave;
 
-  const int w = xcd_group_remap(blockIdx.x, gridDim.x, nkt, 1, kBwdUMajor);
+  // work item (grid share-major: every key block's first share, then the second, ...)
+  const int nitems = gridDim.x / sp.n;
+  const int share = blockIdx.x / nitems;
+  const int w = xcd_group_remap(blockIdx.x - share * nitems, nitems, nkt, 1, kBwdUMajor);
   const int kt = w % nkt, zh = w / nkt;
   const int kvh = zh % p.Hk, b = zh / p.Hk;
   const BwdSeq sq = bwd_seq(p, b);
@@ -564,7 +576,15 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   if (pair_keys) query_range_b<CAUSAL, FEAT>(p, kw, min(kw + 32, SK) - 1, delta, SQ, wq0, wq1);
   const int qstart = (max(bq0, 0) / C::BQ) * C::BQ;
   const int ntq = bq1 > bq0 ? (bq1 - qstart + C::BQ - 1) / C::BQ : 0;
-  const int total = ntq * p.gqa;
+  // this workgroup's steps: `total` tiles of the block's ntq*gqa, from tile it0 on (a query
+  // split gives each share a contiguous run of them)
+  int it0 = 0, total = ntq * p.gqa;
+  if (sp.n > 1) {
+    const int per = (total + sp.n - 1) / sp.n;
+    it0 = min(share * per, total);
+    total = min(it0 + per, total) - it0;
+  }
+  const int qi0 = ntq > 0 ? it0 % ntq : 0, hg0 = ntq > 0 ? it0 / ntq : 0;  // its first tile
   const float c_log2 = p.scale * kLog2e;
 
   // Q/dO tiles through buffer descriptors over rows qt0..SQ-1 (rows past SQ read as zeros);
@@ -592,11 +612,13 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   const long long q_wrap = p.qs.h - ntq * q_step, do_wrap = p.dos.h - ntq * do_step;
   const long long l_wrap = p.lse_sh - (long long)ntq * C::BQ;
   const long long q_left0 = (long long)(SQ - qstart) * p.qs.s * 2, do_left0 = (long long)(SQ - qstart) * p.dos.s * 2;
-  const T* g_q = (const T*)p.Q + (long long)b * p.qs.b + (long long)(kvh * p.gqa) * p.qs.h + (sq.qo + qstart) * p.qs.s;
-  const T* g_do = (const T*)p.dO + (long long)b * p.dos.b + (long long)(kvh * p.gqa) * p.dos.h + (sq.qo + qstart) * p.dos.s;
-  long long g_l = (long long)b * p.lse_sb + (long long)(kvh * p.gqa) * p.lse_sh + sq.qo + qstart;
-  long long g_qleft = q_left0, g_doleft = do_left0;
-  int g_qi = 0, g_t = 0;  // q tile index within the head, tile number
+  const int hfirst = kvh * p.gqa + hg0;
+  const T* g_q = (const T*)p.Q + (long long)b * p.qs.b + (long long)hfirst * p.qs.h + (sq.qo + qstart) * p.qs.s + qi0 * q_step;
+  const T* g_do = (const T*)p.dO + (long long)b * p.dos.b + (long long)hfirst * p.dos.h + (sq.qo + qstart) * p.dos.s +
+                  qi0 * do_step;
+  long long g_l = (long long)b * p.lse_sb + (long long)hfirst * p.lse_sh + sq.qo + qstart + qi0 * C::BQ;
+  long long g_qleft = q_left0 - 2 * qi0 * q_step, g_doleft = do_left0 - 2 * qi0 * do_step;
+  int g_qi = qi0, g_t = 0;  // q tile index within the head, tile number (from it0)
   auto gload = [&](auto set) {
     constexpr int S = decltype(set)::value;
     const bool in = g_t < total;
@@ -718,7 +740,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   }
   __syncthreads();
   // the tile a role works on: head hg of the group, q tile qi (advanced once per tile)
-  int w_qi = 0, w_hg = 0;
+  int w_qi = qi0, w_hg = hg0;
   auto w_next = [&]() {
     if (++w_qi == ntq) {
       w_qi = 0;
@@ -788,7 +810,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
   T* ds_cur = nullptr;
   long long ds_wrap = 0;
   if constexpr (DSW) {
-    ds_cur = ds_head_tiles<T>(p, b, kvh * p.gqa, ds_T) + (long long)(ds_row + (qstart >> 5)) * 1024;
+    ds_cur = ds_head_tiles<T>(p, b, hfirst, ds_T) + (long long)(ds_row + (qstart >> 5) + qi0) * 1024;
     ds_wrap = ((long long)ds_T - (ntq - 1)) * 1024;
   }
   auto d_step = [&](auto set, int it) {
@@ -845,13 +867,44 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt) {
         for_sets(std::make_integer_sequence<int, NSET>{}, [&](auto set) { s_step(set, it + decltype(set)::value); });
     }
   }
+  const float sc = dpw ? p.scale : 1.0f;
+  if (sp.n > 1) {  // a query split: this share's fp32 partial dK (or dV) rows
+    const long long r = ((long long)(2 * share + (dpw ? 0 : 1)) * sp.rows + ((long long)b * p.Hk + kvh) * SK + key) * HDr;
+#pragma unroll
+    for (int db = 0; db < C::NDB; db++) store_cblock_f32(sp.part + r + 32 * db, acc[db], sc, hh, key < SK, HDr - 32 * db);
+    return;
+  }
   {
     T* row = dpw ? (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (sq.ko + key) * p.dks.s
                  : (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (sq.ko + key) * p.dvs.s;
-    const float sc = dpw ? p.scale : 1.0f;
 #pragma unroll
     for (int db = 0; db < C::NDB; db++) store_cblock<T>(row + 32 * db, acc[db], sc, hh, key < SK, HDr - 32 * db);
   }
+}
+
+// Sum of the query-split partials of the pair dK/dV kernel, shares in order (bitwise
+// reproducible): one thread per (row, 4 head dims), rows (dK | dV, b, kv head, key).
+template <typename T>
+__global__ __launch_bounds__(256) void bwd_split_merge_kernel(FableBwdParams p, BwdSplit sp) {
+  const int ch = p.D / 4;
+  const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
+  if (gid >= 2 * sp.rows * ch) return;
+  const long long r = gid / ch;
+  const int c = (int)(gid - r * ch);
+  const int which = (int)(r / sp.rows);  // 0 dK, 1 dV
+  const long long rr = r - which * sp.rows;
+  const int key = (int)(rr % p.SK);
+  const long long bk = rr / p.SK;
+  const int kvh = (int)(bk % p.Hk), b = (int)(bk / p.Hk);
+  f32x4 acc = *(const f32x4*)(sp.part + ((long long)which * sp.rows + rr) * p.D + 4 * c);
+  for (int k = 1; k < sp.n; k++)
+    acc += *(const f32x4*)(sp.part + ((long long)(2 * k + which) * sp.rows + rr) * p.D + 4 * c);
+  typename Dt<T>::V4 o;
+#pragma unroll
+  for (int e = 0; e < 4; e++) o[e] = (T)acc[e];
+  T* dst = which == 0 ? (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (long long)key * p.dks.s
+                      : (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (long long)key * p.dvs.s;
+  *(u32x2*)(dst + 4 * c) = __builtin_bit_cast(u32x2, o);
 }
 
 // ------------------------------------------------------------ dQ from a dS workspace
@@ -1132,10 +1185,40 @@ bwd_dq_ds_kernel(FableBwdParams p, int nqt) {
 #endif
 constexpr int kDsqSets = DSQ_SETS;
 // bytes of the compacted dS workspace (bwd_common.hpp): the table, then every (b, h)'s tiles
+// keys per workgroup of the pair dK/dV kernel at each width (the BwdKVPCfg of bwd_d32.hip ..
+// bwd_d128.hip; 0: the width has no pair kernel); the launcher checks it against the config
+inline int bwd_pair_bk(int D) {
+  const int w = bwd_width(D);
+  return w > 128 ? 0 : (w == 128 ? 128 : 64);
+}
+// Shares per key block of the pair kernel's query split. A causal grid of at most one
+// workgroup per CU runs as long as its longest key block (the first sees every query): halving
+// the blocks of at least 32 query-tile steps pays for the fp32 partials and their merge. A
+// grid filling at most half the CUs splits up to one workgroup per CU, at least 16 steps each.
+inline int bwd_split_count(const FableBwdParams& p) {
+  const int bk = bwd_pair_bk(p.D);
+  if (bk == 0 || p.cu_q || p.B <= 0 || p.Hk <= 0 || p.SQ <= 0 || p.SK <= 0) return 1;
+  const long long gkv = (long long)((p.SK + bk - 1) / bk) * p.Hk * p.B;
+  const long long steps = (long long)((p.SQ + 31) / 32) * p.gqa;  // the most a key block takes
+  if (gkv > 256) return 1;
+  if (2 * gkv > 256) return (p.causal && steps >= 32) ? 2 : 1;
+  long long n = 256 / gkv;
+  n = n < steps / 16 ? n : steps / 16;
+  n = n < 8 ? n : 8;
+  return n >= 2 ? (int)n : 1;
+}
+inline long long ds_split_offset(const FableBwdParams& p, long long tiles) {
+  return (ds_header_bytes((p.SK + 31) >> 5) + (long long)p.B * p.Hq * tiles * 2048 + 255) / 256 * 256;
+}
+// bytes of the compacted dS workspace: the table, every (b, h)'s tiles, and the pair kernel's
+// split partials when it splits
 inline long long ds_bytes(const FableBwdParams& p) {
   if (p.SQ <= 0 || p.SK <= 0) return 0;
   const long long t = ds_tiles_per_head(p);  // 0: no query sees any key, the recomputing path serves
-  return t > 0 ? ds_header_bytes((p.SK + 31) >> 5) + (long long)p.B * p.Hq * t * 2048 : 0;
+  if (t <= 0) return 0;
+  const int n = bwd_split_count(p);
+  const long long part = n > 1 ? (long long)n * 2 * p.B * p.Hk * p.SK * p.D * 4 : 0;
+  return n > 1 ? ds_split_offset(p, t) + part : ds_header_bytes((p.SK + 31) >> 5) + (long long)p.B * p.Hq * t * 2048;
 }
 
 // backward through the dS workspace: D rows, then dK/dV (writing dS), then dQ = dS.K
@@ -1161,11 +1244,27 @@ static int launch_bwd_ds(const FableBwdParams& p, hipStream_t st, int nkt) {
   if (gd > 0x7FFFFFFF || gq > 0x7FFFFFFF || gkv > 0x7FFFFFFF) return fail(FA_ERR_ARG, "fable_attn_bwd: grid too large");
   hipLaunchKernelGGL((bwd_dsum_kernel<T, DW>), dim3((unsigned)gd), dim3(256), 0, st, p, (p.SQ + RPB - 1) / RPB);
   if (int rc = launch_status("fable_attn_bwd (dsum)")) return rc;
-  if constexpr (CKV::PAIR)
-    hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
-  else
+  if constexpr (CKV::PAIR) {
+    BwdSplit sp{1, 0, nullptr};
+    const int n = CKV::BK == bwd_pair_bk(p.D) ? bwd_split_count(p) : 1;
+    if (n > 1 && (long long)p.D % 4 == 0) {
+      const long long t = ds_tiles_per_head(p);
+      const long long off = ds_split_offset(p, t);
+      if (p.ds_ws_bytes >= off + (long long)n * 2 * p.B * p.Hk * p.SK * p.D * 4)
+        sp = BwdSplit{n, (long long)p.B * p.Hk * p.SK, (float*)((char*)p.ds_ws + off)};
+    }
+    hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)(gkv * sp.n)),
+                       dim3(CKV::NT), 0, st, p, nkt, sp);
+    if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;
+    if (sp.n > 1) {
+      const long long items = 2 * sp.rows * (p.D / 4);
+      hipLaunchKernelGGL((bwd_split_merge_kernel<T>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, p, sp);
+      if (int rc = launch_status("fable_attn_bwd (dkdv merge)")) return rc;
+    }
+  } else {
     hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
-  if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;
+    if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;
+  }
   if constexpr (CD::NW == 8) {
     if (small) {
       hipLaunchKernelGGL((bwd_dq_ds_kernel<T, CDS, CAUSAL, FEAT>), dim3((unsigned)gq), dim3(CDS::NT), 0, st, p, nqts);
@@ -1195,7 +1294,8 @@ static int launch_bwd2(const FableBwdParams& p, hipStream_t st) {
   }
   if (gkv > 0) {
     if constexpr (CKV::PAIR)
-      hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
+      hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt,
+                         BwdSplit{1, 0, nullptr});
     else
       hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
     if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;

@@ -195,9 +195,35 @@ def test_bwd_ds_workspace_size():
     for SQ, SK, causal, wl, wr in ((4096, 4096, 1, -1, 0), (150, 150, 1, -1, -1), (96, 300, 1, -1, -1),
                                    (300, 96, 1, -1, -1), (1000, 1000, 0, 100, 0), (500, 700, 0, 64, 64),
                                    (700, 500, 1, 37, -1), (64, 64, 0, 5000, -1)):
-        p.B, p.Hq, p.SQ, p.SK, p.causal, p.win_left, p.win_right = 1, 3, SQ, SK, causal, wl, wr
+        # (64 batches: grids of more than one round, so the dK/dV kernel does not split)
+        p.B, p.Hq, p.Hk, p.gqa = 64, 3, 3, 1
+        p.SQ, p.SK, p.causal, p.win_left, p.win_right = SQ, SK, causal, wl, wr
         got = lib.fable_attn_bwd_ds_bytes(p, 0)
-        assert got == hdr(SK) + 3 * _visible_tiles(SQ, SK, causal, wl, wr) * 2048, (SQ, SK, causal, wl, wr)
+        assert got == hdr(SK) + 64 * 3 * _visible_tiles(SQ, SK, causal, wl, wr) * 2048, (SQ, SK, causal, wl, wr)
+
+
+def test_bwd_query_split_workspace():
+    """A dK/dV grid of one round splits the query tiles of each key block; the workspace then
+    ends, after the 256-byte-aligned tiles, with the fp32 partial dK and dV rows of every share."""
+    from fable_attn import _lib
+    lib = _lib.load()
+    hdr = lambda SK: -(-((SK + 31) // 32 + 1) * 4 // 256) * 256
+    tiles = lambda S: _visible_tiles(S, S, 1)
+    p = _lib.FableBwdParams()
+    p.win_left, p.win_right, p.causal, p.D = -1, -1, 1, 128
+    # B1 H8 S4096 causal: 256 dK/dV workgroups (one round), key block 0 takes 128 steps -> 2 shares
+    p.B, p.Hq, p.Hk, p.gqa, p.SQ, p.SK = 1, 8, 8, 1, 4096, 4096
+    tiles_end = -(-(hdr(4096) + 8 * tiles(4096) * 2048) // 256) * 256
+    assert lib.fable_attn_bwd_ds_bytes(p, 1) == tiles_end + 2 * 2 * 8 * 4096 * 128 * 4
+    # a quarter of the CUs (64 workgroups at D=64, 64-key blocks): up to 4 shares of >= 16 steps
+    p.D, p.Hq, p.Hk, p.SQ, p.SK = 64, 2, 2, 2048, 2048
+    tiles_end = -(-(hdr(2048) + 2 * tiles(2048) * 2048) // 256) * 256
+    assert lib.fable_attn_bwd_ds_bytes(p, 0) == tiles_end + 4 * 2 * 2 * 2048 * 64 * 4
+    # C3 (2048 workgroups) and the one-wave widths never split
+    p.D, p.B, p.Hq, p.Hk, p.SQ, p.SK = 128, 2, 32, 32, 4096, 4096
+    assert lib.fable_attn_bwd_ds_bytes(p, 0) == hdr(4096) + 2 * 32 * tiles(4096) * 2048
+    p.D, p.B, p.Hq, p.Hk = 256, 1, 8, 8
+    assert lib.fable_attn_bwd_ds_bytes(p, 0) == hdr(4096) + 8 * tiles(4096) * 2048
 
 
 def _fwd_params(B, H, SQ, SK, D, gqa=1, causal=False, wl=-1, wr=-1, softcap=0.0, chunk=0,

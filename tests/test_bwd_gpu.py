@@ -14,9 +14,9 @@ where that floor exceeds 2/3 of the bound the bound becomes 1.5x the floor (test
 check_grads). Every case logs its errors, its distance from the model and the floor.
 At the full BASELINE.json configs[2] size sampled heads are checked against the fp64 oracle.
 
-Every case runs both backward paths at head dims up to 128: "ds" (the dK/dV kernel stores dS in
-a workspace and dQ = dS.K is formed from it, the default) and "recompute" (no workspace: the dQ
-kernel recomputes S and dP); head dims above 128 have the recomputing path only.
+Every case runs both backward paths: "ds" (the dK/dV kernel stores dS in a workspace and
+dQ = dS.K is formed from it, the default; small grids also split the pair dK/dV kernel's query
+tiles) and "recompute" (no workspace: the dQ kernel recomputes S and dP).
 """
 import math
 
@@ -58,6 +58,12 @@ CASES = [
     ("D160 causal", 1, 2, 2, 96, 96, 160, True, -1, -1, 0.0, False),
     ("D192 full softcap", 1, 2, 1, 80, 100, 192, False, -1, -1, 20.0, False),
     ("D224 causal", 1, 2, 2, 70, 70, 224, True, -1, -1, 0.0, False),
+    # small dK/dV grids whose key blocks split their query tiles over several workgroups
+    # (fp32 partials summed by a merge kernel; "ds" path only)
+    ("split D128 causal gqa4 S640", 1, 8, 2, 640, 640, 128, True, -1, -1, 0.0, False),
+    ("split D64 full S1100x900", 1, 2, 2, 1100, 900, 64, False, -1, -1, 0.0, False),
+    ("split D96 window (300,0) softcap", 1, 4, 2, 700, 700, 96, True, 300, 0, 20.0, False),
+    ("split D32 causal alibi", 1, 4, 4, 1200, 1200, 32, True, -1, -1, 0.0, True),
 ]
 
 
@@ -237,3 +243,21 @@ def test_backward_long_causal_takes_the_ds_path():
     for i, name in ((0, "dQ"), (1, "dK")):
         e = ((ds[0][i].float() - rc[i].float()).norm() / rc[i].float().norm()).item()
         assert torch.isfinite(ds[0][i]).all() and e <= 1e-3, f"{name} of the two paths: rel_rms {e:.3e}"
+
+
+def test_backward_query_split_taken():
+    """The "split" cases above take the pair kernel's query split: after their 256-byte-aligned
+    dS tiles, the workspace they get holds n >= 2 shares of fp32 partial dK and dV rows."""
+    from fable_attn import _C, _lib
+    for case in [c for c in CASES if c[0].startswith("split")]:
+        name, B, Hq, Hk, SQ, SK, D, causal, wl, wr, sc, alibi = case
+        p = _lib.FableBwdParams()
+        p.B, p.Hq, p.Hk, p.gqa, p.SQ, p.SK, p.D = B, Hq, Hk, Hq // Hk, SQ, SK, D
+        p.causal, p.win_left, p.win_right = int(causal), wl, wr
+        got = _C._L.fable_attn_bwd_ds_bytes(p, 0)
+        p.B = 64                                   # many rounds of workgroups: no split
+        hdr = -(-((SK + 31) // 32 + 1) * 4 // 256) * 256
+        tiles = (_C._L.fable_attn_bwd_ds_bytes(p, 0) - hdr) // 64
+        extra = got - -(-(hdr + B * tiles) // 256) * 256
+        share = 2 * B * Hk * SK * D * 4
+        assert extra > 0 and extra % share == 0 and extra // share >= 2, (name, got, extra)
