@@ -26,7 +26,9 @@ static int dispatch_hd(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs
   }
 }
 
-// Merge of the key-split partials: one thread per (row, 4 head dims), rows r = (b*NH + h)*SQ + q.
+// Merge of the key-split partials: one thread per (row, 4 head dims). Row r belongs to work
+// item w = r / br (query tile, head, sequence, decoded as the forward does) and is query
+// qt*br + r % br of that sequence; rows past the sequence's end are left alone.
 // LSE = m + log(sum_s exp(lse_s - m)), O = sum_s exp(lse_s - LSE) O_s; a row no split saw gets
 // O = 0 and LSE = -inf, as in the unsplit kernel.
 template <typename T>
@@ -36,9 +38,12 @@ __global__ __launch_bounds__(256) void fwd_split_combine_kernel(FableFwdParams p
   if (gid >= sp.rows * ch) return;
   const long long r = gid / ch;
   const int c = (int)(gid - r * ch);
-  const int q = (int)(r % p.SQ);
-  const long long bh = r / p.SQ;
-  const int h = (int)(bh % p.NH), b = (int)(bh / p.NH);
+  const int w = (int)(r / sp.br), qti = w % sp.nqt, zh = w / sp.nqt;
+  const int h = zh % p.NH, z = zh / p.NH;
+  const int qt = p.causal ? sp.nqt - 1 - qti : qti;
+  const SeqView sv = seq_view(p, z, h);
+  const int q = qt * sp.br + (int)(r - (long long)w * sp.br);
+  if (q >= sv.SQ) return;
   float m = -INFINITY;
   for (int k = 0; k < sp.n; k++) m = fmaxf(m, sp.lse[k * sp.rows + r]);
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
@@ -54,10 +59,9 @@ __global__ __launch_bounds__(256) void fwd_split_combine_kernel(FableFwdParams p
   typename Dt<T>::V4 o;
 #pragma unroll
   for (int e = 0; e < 4; e++) o[e] = (T)(acc[e] * inv);
-  T* dst = (T*)p.O + (long long)b * p.sO.b + (long long)h * p.sO.h + (long long)q * p.sO.s + 4 * c;
+  T* dst = (T*)p.O + sv.o0 + (long long)h * p.sO.h + (long long)q * p.sO.s + 4 * c;
   *(u32x2*)dst = __builtin_bit_cast(u32x2, o);
-  if (c == 0 && p.LSE)
-    p.LSE[(long long)b * p.lse_sb + (long long)h * p.lse_sh + q] = m != -INFINITY ? m + __logf(wsum) : -INFINITY;
+  if (c == 0 && p.LSE) p.LSE[sv.lse0 + q] = m != -INFINITY ? m + __logf(wsum) : -INFINITY;
 }
 
 int launch_fwd_split_combine(const FableFwdParams& p, int dtype, const FwdSplit& sp, hipStream_t st) {

@@ -76,14 +76,17 @@ __device__ __forceinline__ bool fwd_visible(const FableFwdParams& p, int i, int 
   return ok;
 }
 
-// Key split of a small forward grid (fp16/bf16, dense batches, no left window, chunk or
-// dropout): when the query tiles of a call fill few of the CUs, `n` workgroups per query tile
-// each take a contiguous share of its key tiles and write an fp32 partial O (row-major,
-// head dim p.HD) and its LSE for every row r = (b*NH + h)*SQ + q, split after split; a second
-// kernel (fwd_split_combine_kernel, fwd.hip) merges the partials into O and LSE.
+// Key split of a small forward grid (fp16/bf16, dense or packed varlen batches, no left
+// window, chunk or dropout): when the query tiles of a call fill few of the CUs, `n`
+// workgroups per query tile each take a contiguous share of its key tiles and write an fp32
+// partial O (row-major, head dim p.HD) and its LSE for every row of the tile, at row
+// r = item * br + (row within the tile), split after split (item: the query tile's work item,
+// sequence-head-major as the grid); a second kernel (fwd_split_combine_kernel, fwd.hip) merges
+// them into O and LSE, through the same sequence view as the forward.
 struct FwdSplit {
   int n;           // workgroups per query tile; 1: no split, the kernel writes O and LSE itself
-  long long rows;  // B * NH * SQ
+  int nqt, br;     // query tiles per (sequence, head) and rows per tile of the launch
+  long long rows;  // work items * br
   float* o;        // [n][rows][p.HD]
   float* lse;      // [n][rows], natural log; -inf where a split saw no key of the row
 };

@@ -707,7 +707,7 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
     const float l_tot = half_sum(l_run[i]);
     const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
     if (sp.n > 1) {
-      const long long r = (long long)split * sp.rows + ((long long)z * p.NH + h) * SQ + qi;
+      const long long r = (long long)split * sp.rows + (long long)w * C::BR + (qi - qb);
 #pragma unroll
       for (int db = 0; db < C::NDB; db++)
         store_cblock_f32(sp.o + r * HDr + db * 32, oacc[i][db], inv, hh, qi < SQ, HDr - db * 32);
@@ -749,7 +749,7 @@ constexpr int kSplitMinTiles = 4, kSplitLongRow = 128;
 
 template <class K>
 static int fwd_split_count(const FableFwdParams& p, long long nblk) {
-  if (p.cu_q || p.dropout_p > 0.0f || p.win_left >= 0 || p.attn_chunk > 0) return 1;
+  if (p.dropout_p > 0.0f || p.win_left >= 0 || p.attn_chunk > 0) return 1;
   if (nblk <= 0) return 1;
   const int tiles = (p.SK + K::BC - 1) / K::BC;  // the most any query tile reads
   if (2 * nblk > kSplitSlots) return (p.causal && nblk <= kSplitSlots && tiles >= kSplitLongRow) ? 2 : 1;
@@ -772,10 +772,10 @@ static int launch_fwd(const FableFwdParams& p, hipStream_t st, FwdWs& ws) {
     using K = typename decltype(cfg)::type;
     const int nqt = (p.SQ + K::BR - 1) / K::BR;
     const long long nblk = (long long)nqt * p.NH * p.batch;
-    FwdSplit sp{1, 0, nullptr, nullptr};
+    FwdSplit sp{1, nqt, K::BR, 0, nullptr, nullptr};
     const int n = fwd_split_count<K>(p, nblk);
     if (n > 1) {
-      const long long rows = (long long)p.batch * p.NH * p.SQ;
+      const long long rows = nblk * K::BR;
       const long long obytes = ((long long)n * rows * p.HD * 4 + 255) / 256 * 256;
       const long long need = obytes + (long long)n * rows * 4;
       if (ws.query) {
@@ -783,7 +783,7 @@ static int launch_fwd(const FableFwdParams& p, hipStream_t st, FwdWs& ws) {
         return FA_OK;
       }
       if (ws.ptr && ws.bytes >= need && ((uintptr_t)ws.ptr & 255) == 0)
-        sp = FwdSplit{n, rows, (float*)ws.ptr, (float*)((char*)ws.ptr + obytes)};
+        sp = FwdSplit{n, nqt, K::BR, rows, (float*)ws.ptr, (float*)((char*)ws.ptr + obytes)};
     }
     if (ws.query) {
       ws.need = 0;

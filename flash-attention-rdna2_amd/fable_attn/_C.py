@@ -248,7 +248,7 @@ def fwd_varlen(q, k, v, cu_q, cu_k, max_sq, max_sk, scale, causal, win_left, win
     p.seqused_k = seqused_k.data_ptr() if seqused_k is not None else None
     p.lse_sb, p.lse_sh = 0, q.shape[0]
     with _on(q.device):
-        _lib.check(_L.fable_attn_fwd(p, _dt(q), _stream(q)), "fable_attn_fwd (varlen)")
+        _launch_fwd(p, _dt(q), q.device, _stream(q))
     return (out, lse) if return_lse else out
 
 

@@ -286,9 +286,9 @@ typedef struct CombineParams {
 int fable_attn_fwd(FableFwdParams p, int dtype, void* stream);
 
 /* The forward with a caller-owned workspace for a key split: when the query tiles of a call fill
- * few of the CUs (fp16/bf16, dense batches, no left window, chunk or dropout), several workgroups
- * per query tile each take a share of its keys, write fp32 partials to `ws`, and a second kernel
- * merges them into O and LSE. fable_attn_fwd_ws_bytes gives the bytes this call would use (0: no
+ * few of the CUs (fp16/bf16, dense or packed varlen batches, no left window, chunk or dropout),
+ * several workgroups per query tile each take a share of its keys, write fp32 partials to `ws`,
+ * and a second kernel merges them into O and LSE. fable_attn_fwd_ws_bytes gives the bytes this call would use (0: no
  * split for this call; -1: the call is invalid, see fable_attn_last_error); a `ws` that is NULL,
  * smaller, or not 256-byte aligned runs the call unsplit. Same results as fable_attn_fwd up to
  * fp32 summation order. No reference counterpart (the reference launches one workgroup per query

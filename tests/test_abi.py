@@ -241,7 +241,7 @@ def _fwd_params(B, H, SQ, SK, D, gqa=1, causal=False, wl=-1, wr=-1, softcap=0.0,
 def test_forward_key_split_workspace_query():
     """fable_attn_fwd_ws_bytes: the key split of small grids (host logic only, no launch). C1
     (64 query tiles of 128 rows on 256 CUs) splits in 4: fp32 partial O and LSE of every row per
-    split; the large grids, left windows, chunks, dropout, varlen and fp32 never split; an
+    split; the large grids, left windows, chunks, dropout and fp32 never split; an
     invalid call answers -1."""
     from fable_attn import _lib
     lib = _lib.load()
@@ -262,7 +262,7 @@ def test_forward_key_split_workspace_query():
     assert q(B=1, H=8, SQ=1024, SK=1024, D=64, wl=100) == 0                # left window
     assert q(B=1, H=8, SQ=1024, SK=1024, D=64, chunk=256) == 0
     assert q(B=1, H=8, SQ=1024, SK=1024, D=64, dropout=0.1) == 0
-    assert q(B=1, H=8, SQ=1024, SK=1024, D=64, varlen=True) == 0
+    assert q(B=1, H=8, SQ=1024, SK=1024, D=64, varlen=True) == q(B=1, H=8, SQ=1024, SK=1024, D=64)  # packed alike
     assert q(2, B=1, H=8, SQ=1024, SK=1024, D=64) == 0                     # fp32
     assert q(B=1, H=8, SQ=256, SK=256, D=64) == 0                          # too few key tiles
     assert q(B=1, H=8, SQ=1024, SK=1024, D=60) == -1                       # no kernel for D=60

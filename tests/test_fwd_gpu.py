@@ -166,16 +166,42 @@ def _varlen(dt, lens, used_q=None, used_k=None, D=128, H=8, gqa=4, causal=True, 
     return o, l, o_ref, l_ref
 
 
+def _varlen_split_bytes(lens, H, gqa, D, causal, dt):
+    """fable_attn_fwd_ws_bytes of a packed varlen call (a query: the sequence table is not read)."""
+    import ctypes
+
+    from fable_attn import _C, _lib
+    tot = sum(lens)
+    p = _lib.FableFwdParams()
+    p.sQ = _lib.Strides(0, D, H * D)
+    p.sK = p.sV = _lib.Strides(0, D, H // gqa * D)
+    p.sO = p.sQ
+    p.SQ, p.SK, p.HD, p.NH, p.gqa = max(lens), max(lens), D, H, gqa
+    p.scale, p.causal, p.win_left, p.win_right = D ** -0.5, int(causal), -1, -1
+    p.cu_q = p.cu_k = ctypes.c_void_p(16)
+    p.batch, p.lse_sb, p.lse_sh = len(lens), 0, tot
+    return _C._L.fable_attn_fwd_ws_bytes(p, 0 if dt == "f16" else 1)
+
+
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
-@pytest.mark.parametrize("kind", ["plain", "seqused", "window_softcap_d256"])
+@pytest.mark.parametrize("kind", ["plain", "seqused", "window_softcap_d256", "split", "split_seqused",
+                                  "split_full_d128"])
 def test_varlen_parity(kind, dt):
     print(f"[varlen] {kind} {dt}", flush=True)
     if kind == "plain":
         r = _varlen(dt, [100, 64, 200])
     elif kind == "seqused":
         r = _varlen(dt, [100, 64, 200], used_q=[70, 64, 150], used_k=[90, 30, 180])
-    else:
+    elif kind == "window_softcap_d256":
         r = _varlen(dt, [300, 77, 512, 129], D=256, H=16, gqa=1, wl=64, wr=0, sc=30.0)
+    elif kind == "split":              # few heads: the keys of each query tile are split
+        assert _varlen_split_bytes([700, 1300, 900], 2, 1, 64, True, dt) > 0
+        r = _varlen(dt, [700, 1300, 900], D=64, H=2, gqa=1)
+    elif kind == "split_seqused":
+        r = _varlen(dt, [700, 1300, 900], used_q=[650, 1300, 700], used_k=[700, 1250, 880], D=64, H=2, gqa=1)
+    else:
+        assert _varlen_split_bytes([900, 1500], 2, 2, 128, False, dt) > 0
+        r = _varlen(dt, [900, 1500], D=128, H=2, gqa=2, causal=False)
     o, l, o_ref, l_ref = r
     rel = orc.rel_rms(o, o_ref)
     lerr, inf_ok = lse_err(l, l_ref)
