@@ -486,12 +486,15 @@ __device__ __forceinline__ void for_sets(std::integer_sequence<int, I...>, F&& f
 // one's VALU work overlaps the other's MFMAs. The Q/dO tiles sit in a 4-stage LDS ring (the
 // S-wave reads tile t, the dP-wave tile t-1, tile t+1 is stored) and tiles t+2 .. t+NSET are in
 // flight in the S-waves' registers; one barrier per tile.
-// Query split of the pair dK/dV kernel on a grid of one round (dS-workspace path, dense
-// batches): `n` workgroups per key block each take a contiguous run of its query tiles and
-// write fp32 partial dK and dV rows; bwd_split_merge_kernel sums them in share order.
+// Query split of the pair dK/dV kernel on a grid of one round (dS-workspace path, dense or
+// packed varlen batches): `n` workgroups per key block each take a contiguous run of its query
+// tiles and write fp32 partial dK and dV rows, at row r = item * bk + (key within the block)
+// (item: the key block's work item, sequence-head-major as the grid); bwd_split_merge_kernel
+// sums them in share order and writes each row through the sequence's key offset.
 struct BwdSplit {
   int n;           // shares per key block; 1: no split, the kernel writes dK and dV itself
-  long long rows;  // B * Hk * SK
+  int nkt, bk;     // key blocks per (sequence, kv head) and keys per block of the launch
+  long long rows;  // work items * bk
   float* part;     // [n][dK | dV][rows][p.D]
 };
 
@@ -869,7 +872,7 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt, BwdSplit sp) {
   }
   const float sc = dpw ? p.scale : 1.0f;
   if (sp.n > 1) {  // a query split: this share's fp32 partial dK (or dV) rows
-    const long long r = ((long long)(2 * share + (dpw ? 0 : 1)) * sp.rows + ((long long)b * p.Hk + kvh) * SK + key) * HDr;
+    const long long r = ((long long)(2 * share + (dpw ? 0 : 1)) * sp.rows + (long long)w * C::BK + (key - kb0)) * HDr;
 #pragma unroll
     for (int db = 0; db < C::NDB; db++) store_cblock_f32(sp.part + r + 32 * db, acc[db], sc, hh, key < SK, HDr - 32 * db);
     return;
@@ -883,7 +886,8 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt, BwdSplit sp) {
 }
 
 // Sum of the query-split partials of the pair dK/dV kernel, shares in order (bitwise
-// reproducible): one thread per (row, 4 head dims), rows (dK | dV, b, kv head, key).
+// reproducible): one thread per (row, 4 head dims), rows (dK | dV, work item, key in block);
+// keys past the sequence's end are left alone.
 template <typename T>
 __global__ __launch_bounds__(256) void bwd_split_merge_kernel(FableBwdParams p, BwdSplit sp) {
   const int ch = p.D / 4;
@@ -893,17 +897,19 @@ __global__ __launch_bounds__(256) void bwd_split_merge_kernel(FableBwdParams p, 
   const int c = (int)(gid - r * ch);
   const int which = (int)(r / sp.rows);  // 0 dK, 1 dV
   const long long rr = r - which * sp.rows;
-  const int key = (int)(rr % p.SK);
-  const long long bk = rr / p.SK;
-  const int kvh = (int)(bk % p.Hk), b = (int)(bk / p.Hk);
+  const int w = (int)(rr / sp.bk), kt = w % sp.nkt, zh = w / sp.nkt;
+  const int kvh = zh % p.Hk, b = zh / p.Hk;
+  const BwdSeq sq = bwd_seq(p, b);
+  const int key = kt * sp.bk + (int)(rr - (long long)w * sp.bk);
+  if (key >= sq.SK) return;
   f32x4 acc = *(const f32x4*)(sp.part + ((long long)which * sp.rows + rr) * p.D + 4 * c);
   for (int k = 1; k < sp.n; k++)
     acc += *(const f32x4*)(sp.part + ((long long)(2 * k + which) * sp.rows + rr) * p.D + 4 * c);
   typename Dt<T>::V4 o;
 #pragma unroll
   for (int e = 0; e < 4; e++) o[e] = (T)acc[e];
-  T* dst = which == 0 ? (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (long long)key * p.dks.s
-                      : (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (long long)key * p.dvs.s;
+  T* dst = which == 0 ? (T*)p.dK + (long long)b * p.dks.b + (long long)kvh * p.dks.h + (sq.ko + key) * p.dks.s
+                      : (T*)p.dV + (long long)b * p.dvs.b + (long long)kvh * p.dvs.h + (sq.ko + key) * p.dvs.s;
   *(u32x2*)(dst + 4 * c) = __builtin_bit_cast(u32x2, o);
 }
 
@@ -1197,7 +1203,7 @@ inline int bwd_pair_bk(int D) {
 // grid filling at most half the CUs splits up to one workgroup per CU, at least 16 steps each.
 inline int bwd_split_count(const FableBwdParams& p) {
   const int bk = bwd_pair_bk(p.D);
-  if (bk == 0 || p.cu_q || p.B <= 0 || p.Hk <= 0 || p.SQ <= 0 || p.SK <= 0) return 1;
+  if (bk == 0 || p.B <= 0 || p.Hk <= 0 || p.SQ <= 0 || p.SK <= 0) return 1;
   const long long gkv = (long long)((p.SK + bk - 1) / bk) * p.Hk * p.B;
   const long long steps = (long long)((p.SQ + 31) / 32) * p.gqa;  // the most a key block takes
   if (gkv > 256) return 1;
@@ -1206,6 +1212,11 @@ inline int bwd_split_count(const FableBwdParams& p) {
   n = n < steps / 16 ? n : steps / 16;
   n = n < 8 ? n : 8;
   return n >= 2 ? (int)n : 1;
+}
+// partial rows of the split: every key block's work item times its keys
+inline long long bwd_split_rows(const FableBwdParams& p) {
+  const int bk = bwd_pair_bk(p.D);
+  return bk > 0 ? (long long)((p.SK + bk - 1) / bk) * p.Hk * p.B * bk : 0;
 }
 inline long long ds_split_offset(const FableBwdParams& p, long long tiles) {
   return (ds_header_bytes((p.SK + 31) >> 5) + (long long)p.B * p.Hq * tiles * 2048 + 255) / 256 * 256;
@@ -1217,7 +1228,7 @@ inline long long ds_bytes(const FableBwdParams& p) {
   const long long t = ds_tiles_per_head(p);  // 0: no query sees any key, the recomputing path serves
   if (t <= 0) return 0;
   const int n = bwd_split_count(p);
-  const long long part = n > 1 ? (long long)n * 2 * p.B * p.Hk * p.SK * p.D * 4 : 0;
+  const long long part = n > 1 ? (long long)n * 2 * bwd_split_rows(p) * p.D * 4 : 0;
   return n > 1 ? ds_split_offset(p, t) + part : ds_header_bytes((p.SK + 31) >> 5) + (long long)p.B * p.Hq * t * 2048;
 }
 
@@ -1245,13 +1256,13 @@ static int launch_bwd_ds(const FableBwdParams& p, hipStream_t st, int nkt) {
   hipLaunchKernelGGL((bwd_dsum_kernel<T, DW>), dim3((unsigned)gd), dim3(256), 0, st, p, (p.SQ + RPB - 1) / RPB);
   if (int rc = launch_status("fable_attn_bwd (dsum)")) return rc;
   if constexpr (CKV::PAIR) {
-    BwdSplit sp{1, 0, nullptr};
+    BwdSplit sp{1, nkt, CKV::BK, 0, nullptr};
     const int n = CKV::BK == bwd_pair_bk(p.D) ? bwd_split_count(p) : 1;
     if (n > 1 && (long long)p.D % 4 == 0) {
       const long long t = ds_tiles_per_head(p);
       const long long off = ds_split_offset(p, t);
-      if (p.ds_ws_bytes >= off + (long long)n * 2 * p.B * p.Hk * p.SK * p.D * 4)
-        sp = BwdSplit{n, (long long)p.B * p.Hk * p.SK, (float*)((char*)p.ds_ws + off)};
+      if (p.ds_ws_bytes >= off + (long long)n * 2 * bwd_split_rows(p) * p.D * 4)
+        sp = BwdSplit{n, nkt, CKV::BK, bwd_split_rows(p), (float*)((char*)p.ds_ws + off)};
     }
     hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)(gkv * sp.n)),
                        dim3(CKV::NT), 0, st, p, nkt, sp);
@@ -1295,7 +1306,7 @@ static int launch_bwd2(const FableBwdParams& p, hipStream_t st) {
   if (gkv > 0) {
     if constexpr (CKV::PAIR)
       hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt,
-                         BwdSplit{1, 0, nullptr});
+                         BwdSplit{1, nkt, CKV::BK, 0, nullptr});
     else
       hipLaunchKernelGGL((bwd_dkdv_kernel<T, CKV, CAUSAL, FEAT, DROP>), dim3((unsigned)gkv), dim3(CKV::NT), 0, st, p, nkt);
     if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;

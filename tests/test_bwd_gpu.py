@@ -259,5 +259,6 @@ def test_backward_query_split_taken():
         hdr = -(-((SK + 31) // 32 + 1) * 4 // 256) * 256
         tiles = (_C._L.fable_attn_bwd_ds_bytes(p, 0) - hdr) // 64
         extra = got - -(-(hdr + B * tiles) // 256) * 256
-        share = 2 * B * Hk * SK * D * 4
+        bk = 128 if (D + 31) // 32 * 32 == 128 else 64      # keys per pair-kernel workgroup
+        share = 2 * B * Hk * -(-SK // bk) * bk * D * 4       # dK and dV rows of every work item
         assert extra > 0 and extra % share == 0 and extra // share >= 2, (name, got, extra)

@@ -163,3 +163,51 @@ def test_varlen_autograd_matches_dense_autograd():
         o.backward(dout[a:b][None])
         for name, got, ref in (("dq", gq, qs.grad), ("dk", gk, ks.grad), ("dv", gv, vs.grad)):
             assert torch.equal(got[a:b], ref[0]), f"seq {i} {name} differs from the dense path"
+
+
+# longer packed sequences, few heads: the pair dK/dV grid is one round and splits the query
+# tiles of its key blocks (fp32 partials merged per key row through the sequence's offset)
+SPLIT_CASES = [
+    ("split causal gqa D64", [900, 1400, 600], None, 4, 2, 64, True, -1, -1, 0.0),
+    ("split full seqused D128", [700, 1100], [900, 1000], 2, 2, 128, False, -1, -1, 0.0),
+]
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("case", SPLIT_CASES, ids=[c[0] for c in SPLIT_CASES])
+def test_varlen_backward_query_split(case, dt):
+    """Against the fp64 oracle per sequence (the dense per-sequence kernels split differently, so
+    they agree with it to rounding, not bitwise); bitwise reproducible over two runs."""
+    import torch
+
+    from fable_attn import _C, _lib
+    print(f"[varlen-bwd-split] {case[0]} {dt}", flush=True)
+    _, _, _, Hq, Hk, D, causal, wl, wr, sc = case
+    lq, lk, q, k, v, do = _make(case, dt)
+    p = _lib.FableBwdParams()
+    p.B, p.Hq, p.Hk, p.gqa, p.SQ, p.SK, p.D = len(lq), Hq, Hk, Hq // Hk, max(lq), max(lk), D
+    p.causal, p.win_left, p.win_right = int(causal), wl, wr
+    unsplit = _C._L.fable_attn_bwd_ds_bytes(p, 0)
+    p.B = 64 * len(lq)                                  # many rounds: no split
+    assert _C._L.fable_attn_bwd_ds_bytes(p, 0) // 64 < unsplit, "the case must split"
+    su_q = [min(L, 600) for L in lq] if "seqused" in case[0] else None
+    su_k = [min(L, 800) for L in lk] if "seqused" in case[0] else None
+    dq, dk, dv = _varlen_kernel(case, dt, lq, lk, q, k, v, do, su_q=su_q, su_k=su_k)
+    out = to_np(_varlen_kernel.last_out)
+    again = _varlen_kernel(case, dt, lq, lk, q, k, v, do, su_q=su_q, su_k=su_k)
+    for a, b in zip((dq, dk, dv), again):
+        assert torch.equal(a, b), "varlen backward differs between runs"
+    cq, ck = _cu(lq), _cu(lk)
+    scale = 1.0 / math.sqrt(D)
+    for i in range(len(lq)):
+        a, c = cq[i], ck[i]
+        b = a + (su_q[i] if su_q else lq[i])
+        d = c + (su_k[i] if su_k else lk[i])
+        bhsd = lambda x: np.ascontiguousarray(x.transpose(1, 0, 2)[None])
+        args = (bhsd(q[a:b]), bhsd(k[c:d]), bhsd(v[c:d]), bhsd(do[a:b]), scale, causal, wl, wr, sc, None)
+        ref = orc.bwd(*args)
+        model = orc.bwd(*args, model=dt, stored_o=bhsd(out[a:b]))
+        got = [to_np(x).transpose(1, 0, 2)[None] for x in (dq[a:b], dk[c:d], dv[c:d])]
+        check_grads("varlen_bwd_split", f"{case[0]} seq {i}", dt, got, ref, model, vanish_ok=True)
+        if su_q:   # rows past the used lengths get zero gradient
+            assert not to_np(dq[b:cq[i + 1]]).any() and not to_np(dk[d:ck[i + 1]]).any()
