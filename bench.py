@@ -553,6 +553,74 @@ def cpu_baseline(inputs, heads=32, causal=True):
                       + ("; extrapolated linearly to all heads" if heads < B * H else "")}
 
 
+# shapes of the rate sweep: (B, S, Hq, Hk, D, causal); the forward in fp16, the backward in bf16
+SWEEP_FWD = [(1, 1024, 8, 8, 64, False), (1, 2048, 8, 8, 128, True), (1, 4096, 8, 8, 128, True),
+             (1, 8192, 4, 4, 128, True), (1, 4096, 32, 32, 128, True), (1, 8192, 32, 32, 128, True),
+             (1, 16384, 32, 32, 128, True), (4, 2048, 16, 16, 128, False), (1, 16384, 8, 8, 128, False),
+             (2, 2048, 16, 16, 64, True), (1, 4096, 16, 16, 256, True), (1, 8192, 32, 8, 128, True)]
+SWEEP_BWD = [(2, 4096, 32, 32, 128, True), (1, 4096, 8, 8, 128, True), (1, 4096, 32, 8, 128, True),
+             (1, 8192, 8, 8, 128, True), (2, 2048, 16, 16, 128, False), (1, 2048, 16, 16, 64, True),
+             (1, 4096, 16, 16, 256, True), (2, 2048, 16, 16, 192, False)]
+
+
+def sweep(reps=5, inner=10):
+    """Markdown table of forward (fp16) and backward (bf16, dS workspace) rates through the
+    binding the public API uses (fable_attn._C.fwd / bwd), per shape: the median of `reps`
+    HIP-event timings of `inner` back-to-back calls, and whether the small-grid split applies
+    (forward: key split; backward: query split of the dK/dV kernel)."""
+    import torch
+    from fable_attn import _C, _lib
+
+    def timed(fn):
+        for _ in range(3):
+            fn()
+        ts = []
+        for _ in range(reps):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(inner):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            ts.append(e0.elapsed_time(e1) / inner)
+        return _median(ts)
+
+    g = torch.Generator(device="cuda").manual_seed(0)
+    out = ["| pass | B | S | Hq / Hk | D | causal | dtype | ms per call | TFLOP/s | split |",
+           "|---|---|---|---|---|---|---|---|---|---|"]
+    for pas, shapes, dt in (("forward", SWEEP_FWD, torch.float16), ("backward", SWEEP_BWD, torch.bfloat16)):
+        for B, S, Hq, Hk, D, causal in shapes:
+            mk = lambda H: torch.randn(B, S, H, D, device="cuda", dtype=dt, generator=g).transpose(1, 2)
+            q, k, v = mk(Hq), mk(Hk), mk(Hk)
+            sc = D ** -0.5
+            fl = 4.0 * B * Hq * S * S * D * (0.5 if causal else 1.0)
+            st = lambda t: _lib.Strides(t.stride(0), t.stride(1), t.stride(2))
+            if pas == "forward":
+                p = _lib.FableFwdParams(None, None, None, None, None, st(q), st(k), st(v), st(q), S, S, D, Hq,
+                                        Hq // Hk, sc, 0.0, -1, -1, None, int(causal), 0.0, 0, None, None, B,
+                                        0, None, None, Hq * S, S)
+                split = _C._L.fable_attn_fwd_ws_bytes(p, 0) > 0
+                ms = timed(lambda: _C.fwd(q, k, v, sc, causal, -1, -1, 0.0, None, 0.0, 0))
+            else:
+                fl *= 2.5
+                do = mk(Hq)
+                o, lse = _C.fwd(q, k, v, sc, causal, -1, -1, 0.0, None, 0.0, 0)
+                p = _lib.FableBwdParams()
+                p.B, p.Hq, p.Hk, p.gqa, p.SQ, p.SK, p.D = B, Hq, Hk, Hq // Hk, S, S, D
+                p.causal, p.win_left, p.win_right = int(causal), -1, -1
+                need = _C._L.fable_attn_bwd_ds_bytes(p, 1)
+                hdr = ((S + 31) // 32 + 1) * 4 + 255 >> 8 << 8
+                p.B = 64 * B                            # many rounds of workgroups: the tiles alone
+                tiles = (_C._L.fable_attn_bwd_ds_bytes(p, 1) - hdr) // 64
+                split = need > hdr + tiles + 255        # the split's partials follow the tiles
+                ms = timed(lambda: _C.bwd(do, q, k, v, o, lse, sc, causal, -1, -1, 0.0, None, 0.0, 0))
+                del do, o, lse
+            out.append(f"| {pas} | {B} | {S} | {Hq} / {Hk} | {D} | {'yes' if causal else 'no'} | "
+                       f"{str(dt)[6:]} | {ms:.4f} | {fl / (ms * 1e-3) / 1e12:.0f} | {'yes' if split else 'no'} |")
+            del q, k, v
+    return "\n".join(out)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -575,6 +643,8 @@ def main():
                     help="print every counter of rocprofv3 --pmc runs for --kernel-filter and exit")
     ap.add_argument("--summarize-parity", metavar="JSONL",
                     help="print the table of the parity errors the GPU tests logged and exit")
+    ap.add_argument("--sweep", action="store_true",
+                    help="print a markdown table of forward and backward rates over a grid of shapes and exit")
     ap.add_argument("--kernel-filter", default=None, help="regex on kernel symbols (summaries)")
     ap.add_argument("--skip", type=int, default=0, help="leading dispatches to skip (summaries)")
     ap.add_argument("--last", type=int, default=0, help="average only the last N dispatches (summaries)")
@@ -603,6 +673,9 @@ def main():
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(2)
 
+    if a.sweep:
+        print(sweep())
+        return
     log("[bench] headline: causal fp16 forward S=16384 H=32 D=128")
     head, head_inputs = bench_fwd(16384, a.steps, a.warmup)
     log(f"[bench] fwd S=16384: {head['ms']:.3f} ms  {head['tflops']:.1f} TFLOP/s")
