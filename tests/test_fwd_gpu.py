@@ -185,7 +185,7 @@ def _varlen_split_bytes(lens, H, gqa, D, causal, dt):
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("kind", ["plain", "seqused", "window_softcap_d256", "split", "split_seqused",
-                                  "split_full_d128"])
+                                  "split_full_d128", "split_ragged"])
 def test_varlen_parity(kind, dt):
     print(f"[varlen] {kind} {dt}", flush=True)
     if kind == "plain":
@@ -199,9 +199,12 @@ def test_varlen_parity(kind, dt):
         r = _varlen(dt, [700, 1300, 900], D=64, H=2, gqa=1)
     elif kind == "split_seqused":
         r = _varlen(dt, [700, 1300, 900], used_q=[650, 1300, 700], used_k=[700, 1250, 880], D=64, H=2, gqa=1)
-    else:
+    elif kind == "split_full_d128":
         assert _varlen_split_bytes([900, 1500], 2, 2, 128, False, dt) > 0
         r = _varlen(dt, [900, 1500], D=128, H=2, gqa=2, causal=False)
+    else:                              # empty and one-row sequences among split ones
+        assert _varlen_split_bytes([700, 0, 1300, 1, 900], 2, 1, 64, True, dt) > 0
+        r = _varlen(dt, [700, 0, 1300, 1, 900], D=64, H=2, gqa=1)
     o, l, o_ref, l_ref = r
     rel = orc.rel_rms(o, o_ref)
     lerr, inf_ok = lse_err(l, l_ref)
