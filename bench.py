@@ -440,7 +440,7 @@ def summarize_stats(d, kernel_re=None, skip=0, last=0):
 FWD_C2_KERNEL = r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi128ELi64ELi8ELi2ELi1EEELb1ELb0ELb0EEEv14FableFwdParamsiNS_8FwdSplitE"
 # C1 takes the key split: the split kernel, then the merge of its partials
 FWD_C1_KERNEL = (r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi64E.*ELb0ELb0ELb0EEEv14FableFwdParamsiNS_8FwdSplitE",
-                 r"_ZN2fa24fwd_split_combine_kernelIDF16_EEv14FableFwdParamsNS_8FwdSplitE")
+                 r"_ZN2fa24fwd_split_combine_kernelIDF16_Li[0-9]+EEEv14FableFwdParamsNS_8FwdSplitE")
 BWD_C3_KERNELS = (r"_ZN2fa15bwd_dsum_kernelIDF16b.*", r"_ZN2fa20bwd_dkdv_pair_kernelIDF16b.*",
                   r"_ZN2fa16bwd_dq_ds_kernelIDF16b.*")
 DEC_C4_KERNELS = (r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0ELb1EEEv14FableDecParamsiii",

@@ -30,8 +30,11 @@ static int dispatch_hd(const FableFwdParams& p, int dtype, hipStream_t st, FwdWs
 // item w = r / br (query tile, head, sequence, decoded as the forward does) and is query
 // qt*br + r % br of that sequence; rows past the sequence's end are left alone.
 // LSE = m + log(sum_s exp(lse_s - m)), O = sum_s exp(lse_s - LSE) O_s; a row no split saw gets
-// O = 0 and LSE = -inf, as in the unsplit kernel.
-template <typename T>
+// O = 0 and LSE = -inf, as in the unsplit kernel. Every share writes every row of its work
+// item (a share without keys writes O = 0, LSE = -inf). All NMAX >= n shares' values are loaded
+// before any is used (indices past n - 1 repeat the last share and are not summed), so the
+// thread waits out one memory latency instead of one per share; the sum runs in share order.
+template <typename T, int NMAX>
 __global__ __launch_bounds__(256) void fwd_split_combine_kernel(FableFwdParams p, FwdSplit sp) {
   const int ch = p.HD / 4;
   const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
@@ -44,15 +47,28 @@ __global__ __launch_bounds__(256) void fwd_split_combine_kernel(FableFwdParams p
   const SeqView sv = seq_view(p, z, h);
   const int q = qt * sp.br + (int)(r - (long long)w * sp.br);
   if (q >= sv.SQ) return;
+  float ls[NMAX];
+  f32x4 ov[NMAX];
+#pragma unroll
+  for (int k = 0; k < NMAX; k++) {
+    const long long rk = (long long)min(k, sp.n - 1) * sp.rows + r;
+    ls[k] = sp.lse[rk];
+    ov[k] = *(const f32x4*)(sp.o + rk * p.HD + 4 * c);
+  }
   float m = -INFINITY;
-  for (int k = 0; k < sp.n; k++) m = fmaxf(m, sp.lse[k * sp.rows + r]);
+#pragma unroll
+  for (int k = 0; k < NMAX; k++)
+    if (k < sp.n) m = fmaxf(m, ls[k]);
   f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
   float wsum = 0.0f;
   if (m != -INFINITY) {
-    for (int k = 0; k < sp.n; k++) {
-      const float w = __expf(sp.lse[k * sp.rows + r] - m);
-      wsum += w;
-      acc += w * *(const f32x4*)(sp.o + (k * sp.rows + r) * p.HD + 4 * c);
+#pragma unroll
+    for (int k = 0; k < NMAX; k++) {
+      if (k < sp.n) {
+        const float wk = __expf(ls[k] - m);
+        wsum += wk;
+        acc += wk * ov[k];
+      }
     }
   }
   const float inv = m != -INFINITY ? 1.0f / wsum : 0.0f;
@@ -64,13 +80,26 @@ __global__ __launch_bounds__(256) void fwd_split_combine_kernel(FableFwdParams p
   if (c == 0 && p.LSE) p.LSE[sv.lse0 + q] = m != -INFINITY ? m + __logf(wsum) : -INFINITY;
 }
 
-int launch_fwd_split_combine(const FableFwdParams& p, int dtype, const FwdSplit& sp, hipStream_t st) {
-  const long long items = sp.rows * (p.HD / 4);
-  const dim3 grid((unsigned)((items + 255) / 256)), block(256);
-  if (dtype == FA_F16)
-    hipLaunchKernelGGL(fwd_split_combine_kernel<_Float16>, grid, block, 0, st, p, sp);
+template <typename T>
+static void launch_combine(const FableFwdParams& p, const FwdSplit& sp, dim3 grid, hipStream_t st) {
+  if (sp.n <= 2)
+    hipLaunchKernelGGL((fwd_split_combine_kernel<T, 2>), grid, dim3(256), 0, st, p, sp);
+  else if (sp.n <= 4)
+    hipLaunchKernelGGL((fwd_split_combine_kernel<T, 4>), grid, dim3(256), 0, st, p, sp);
+  else if (sp.n <= 8)
+    hipLaunchKernelGGL((fwd_split_combine_kernel<T, 8>), grid, dim3(256), 0, st, p, sp);
   else
-    hipLaunchKernelGGL(fwd_split_combine_kernel<__bf16>, grid, block, 0, st, p, sp);
+    hipLaunchKernelGGL((fwd_split_combine_kernel<T, 16>), grid, dim3(256), 0, st, p, sp);
+}
+
+int launch_fwd_split_combine(const FableFwdParams& p, int dtype, const FwdSplit& sp, hipStream_t st) {
+  if (sp.n < 2 || sp.n > 16) return fail(FA_ERR_ARG, "fable_attn_fwd: %d key splits (2..16)", sp.n);
+  const long long items = sp.rows * (p.HD / 4);
+  const dim3 grid((unsigned)((items + 255) / 256));
+  if (dtype == FA_F16)
+    launch_combine<_Float16>(p, sp, grid, st);
+  else
+    launch_combine<__bf16>(p, sp, grid, st);
   return launch_status("fable_attn_fwd (split merge)");
 }
 
