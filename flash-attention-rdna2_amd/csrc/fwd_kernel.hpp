@@ -138,13 +138,22 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
     }
   }
 
+  // Fixed softmax offset (bf16 softcap without alibi, cap c <= kFixCap): every logit, in log2
+  // units c*tanh(.)*log2(e), lies in [-lcap, lcap] with lcap = c*log2(e), so the logits are
+  // formed as x - lcap <= 0 and each probability 2^(x - lcap) lies in [2^(-2 lcap), 1], at
+  // least 2^-95.3, inside the bf16 and fp32 normal ranges. The row max, its exchange and the
+  // rescale test drop out, the subtraction folds into the transform's last FMA, and the LSE
+  // adds c. (fp16 would flush such probabilities to zero; alibi leaves the logits unbounded.)
+  constexpr float kFixCap = 33.0f;
+  constexpr bool kFixT = FEAT && !DROP && std::is_same<T, __bf16>::value;
+  const bool fixm = kFixT && p.softcap > 0.0f && p.softcap <= kFixCap && !p.alibi_slopes;
   f32x16 oacc[QB][C::NDB];
   float m_run[QB], l_run[QB];
 #pragma unroll
   for (int i = 0; i < QB; i++) {
 #pragma unroll
     for (int db = 0; db < C::NDB; db++) oacc[i][db] = f32x16{};
-    m_run[i] = -INFINITY;
+    m_run[i] = fixm ? 0.0f : -INFINITY;
     l_run[i] = 0.0f;
   }
   // FEAT masks: every mask (sequence end, causal, window, chunk) leaves row qi a single
@@ -348,12 +357,16 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
   // (bit 0 softcap, bit 1 alibi), then the interval mask
   auto logit = [&](auto masked, auto cap, int i, float sv, int kb, int jb, int r, unsigned vis) -> float {
     float x;
+    // (bit 4: the fixed offset, the logit less lcap)
+    constexpr bool kFix = (decltype(cap)::value & 16) != 0;
     if constexpr ((decltype(cap)::value & 8) != 0) {
       const float u = sv * kpoly, u2 = u * u;
-      x = u * fmaf(u2, fmaf(u2, fmaf(u2, pa7, pa5), pa3), pa1);
+      const float pu = fmaf(u2, fmaf(u2, fmaf(u2, pa7, pa5), pa3), pa1);
+      x = kFix ? fmaf(u, pu, -lcap) : u * pu;
     } else if constexpr ((decltype(cap)::value & 1) != 0) {
       const float e = exp2_fast(sv * kcap);
-      x = fmaf(-2.0f * lcap, __builtin_amdgcn_rcpf(e + 1.0f), lcap);
+      x = kFix ? (-2.0f * lcap) * __builtin_amdgcn_rcpf(e + 1.0f)
+               : fmaf(-2.0f * lcap, __builtin_amdgcn_rcpf(e + 1.0f), lcap);
     } else {
       x = sv * c_log2;
     }
@@ -394,24 +407,30 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
           if (!ok) s[jb][r] = -INFINITY;
         }
     }
-    float mx = -INFINITY;
+    // cap bit 4: the fixed offset (the logits are already shifted; m_run stays 0, no rescale)
+    float corr = 1.0f, m_use = 0.0f;
+    if constexpr ((decltype(cap)::value & 16) != 0) {
+      resc = false;
+    } else {
+      float mx = -INFINITY;
 #pragma unroll
-    for (int jb = 0; jb < C::NB; jb++)
+      for (int jb = 0; jb < C::NB; jb++)
 #pragma unroll
-      for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[jb][r]);
-    mx = half_max(mx);
-    const float m_cand = fmaxf(m_run[i], FEAT ? mx : mx * c_log2);
-    const bool need = m_cand > m_run[i] + kLazyMax;
-    const float corr = need ? exp2_fast(m_run[i] - m_cand) : 1.0f;
-    // While a row's running max is -inf no key has been visible to it and its O accumulators
-    // are still zero: the first tile a row sees moves the max but needs no rescale. The feature
-    // kernels skip it (at head dim 256 a rescale is 384 VALU instructions, a tenth of a 512-key
-    // window's work: C5 +1.3%); on the long rows of the plain kernels the extra test per tile
-    // cost more than the one rescale (D=160/192 0.98x)
-    const bool scale_o = FEAT ? need && m_run[i] != -INFINITY : need;
-    m_run[i] = need ? m_cand : m_run[i];
-    resc = __builtin_amdgcn_ballot_w64(scale_o) != 0;
-    const float m_use = m_run[i] == -INFINITY ? 0.0f : m_run[i];
+        for (int r = 0; r < 16; r++) mx = fmaxf(mx, s[jb][r]);
+      mx = half_max(mx);
+      const float m_cand = fmaxf(m_run[i], FEAT ? mx : mx * c_log2);
+      const bool need = m_cand > m_run[i] + kLazyMax;
+      corr = need ? exp2_fast(m_run[i] - m_cand) : 1.0f;
+      // While a row's running max is -inf no key has been visible to it and its O accumulators
+      // are still zero: the first tile a row sees moves the max but needs no rescale. The
+      // feature kernels skip it (at head dim 256 a rescale is 384 VALU instructions, a tenth of
+      // a 512-key window's work: C5 +1.3%); on the long rows of the plain kernels the extra
+      // test per tile cost more than the one rescale (D=160/192 0.98x)
+      const bool scale_o = FEAT ? need && m_run[i] != -INFINITY : need;
+      m_run[i] = need ? m_cand : m_run[i];
+      resc = __builtin_amdgcn_ballot_w64(scale_o) != 0;
+      m_use = m_run[i] == -INFINITY ? 0.0f : m_run[i];
+    }
     // The row sum adds the fp32 probabilities (not the rounded ones the PV product takes): the
     // LSE is then exact to fp32 rounding, and the backward, which rebuilds P = exp(s - LSE),
     // sees probabilities that sum to 1. Summing the fp16-rounded values pairwise (v_dot2) ran at
@@ -465,12 +484,21 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
   };
   using Plain = std::integral_constant<bool, false>;
   using Masked = std::integral_constant<bool, true>;
-  // logit transform of the feature kernels: bit 0 softcap, bit 1 alibi
+  // logit transform of the feature kernels: bit 0 softcap, bit 1 alibi; bit 4 (with bit 0 alone)
+  // the fixed softmax offset of the bf16 softcap kernels (fixm)
   using Cap0 = std::integral_constant<int, 0>;
   const int fmode = FEAT ? (p.softcap > 0.0f ? 1 : 0) | (p.alibi_slopes ? 2 : 0) : 0;
   auto with_fmode = [&](auto f) {
     switch (fmode) {
-      case 1: f(std::integral_constant<int, 1>{}); break;
+      case 1:
+        if constexpr (kFixT) {
+          if (fixm) {
+            f(std::integral_constant<int, 1 | 16>{});
+            break;
+          }
+        }
+        f(std::integral_constant<int, 1>{});
+        break;
       case 2: f(std::integral_constant<int, 2>{}); break;
       case 3: f(std::integral_constant<int, 3>{}); break;
       default: f(Cap0{}); break;
@@ -636,7 +664,15 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
             __builtin_amdgcn_sched_barrier(0);
           }
           const float m_keep = m_run[0], l_keep = l_run[0];
-          corr[0] = softmax(Masked{}, std::integral_constant<int, 4>{}, 0, s[0], kb1, pb[0], resc[0]);
+          corr[0] = softmax(Masked{}, std::integral_constant<int, 4 | (decltype(cap)::value & 16)>{}, 0, s[0], kb1, pb[0], resc[0]);
+          if constexpr (kPoly && (decltype(cap)::value & 16) != 0) {
+            // With the fixed offset nothing in the softmax waits for the row max, and the
+            // compiler moved the exponentials past the range test below (on its fallback path
+            // they are dead): formed here, they stay in the block of the products.
+#pragma unroll
+            for (int g = 0; g < C::NG; g++) asm volatile("" : "+v"(pb[0][g]));
+            asm volatile("" : "+v"(l_run[0]));
+          }
           if constexpr (kPoly) {
             // A score outside the polynomial's range anywhere in the wave: the row state goes
             // back to before this tile, and the tile is redone with the exp/rcp form. The test
@@ -653,7 +689,7 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
                 asm volatile("" : "+v"(rv));
                 s[0][kk / 16][kk % 16] = logit(Masked{}, cap, 0, rv, kb1, kk / 16, kk % 16, vis[kk / 16]);
               }
-              corr[0] = softmax(Masked{}, std::integral_constant<int, 4>{}, 0, s[0], kb1, pb[0], resc[0]);
+              corr[0] = softmax(Masked{}, std::integral_constant<int, 4 | (decltype(cap)::value & 16)>{}, 0, s[0], kb1, pb[0], resc[0]);
             }
           }
         } else {
@@ -700,7 +736,9 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
     if (BP == 1 || t % BP == BP - 1) __syncthreads();
   }
 
-  // ---- epilogue: O = acc / l, LSE (a key split: the fp32 partial O and LSE of its keys)
+  // ---- epilogue: O = acc / l, LSE (a key split: the fp32 partial O and LSE of its keys); with
+  // the fixed offset the logits were formed less lcap
+  const float m_base = fixm ? lcap : 0.0f;
 #pragma unroll
   for (int i = 0; i < QB; i++) {
     const int qi = qw + 32 * i + l32;
@@ -711,7 +749,7 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
 #pragma unroll
       for (int db = 0; db < C::NDB; db++)
         store_cblock_f32(sp.o + r * HDr + db * 32, oacc[i][db], inv, hh, qi < SQ, HDr - db * 32);
-      if (qi < SQ && hh == 0) sp.lse[r] = l_tot > 0.0f ? m_run[i] * kLn2 + __logf(l_tot) : -INFINITY;
+      if (qi < SQ && hh == 0) sp.lse[r] = l_tot > 0.0f ? (m_run[i] + m_base) * kLn2 + __logf(l_tot) : -INFINITY;
       continue;
     }
     T* orow = Og + (long long)qi * p.sO.s;
@@ -720,7 +758,7 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
       store_cblock<T>(orow + db * 32, oacc[i][db], inv, hh, qi < SQ, HDr - db * 32);
     if (qi < SQ) {
       if (p.LSE && hh == 0)
-        p.LSE[sv.lse0 + qi] = l_tot > 0.0f ? m_run[i] * kLn2 + __logf(l_tot) : -INFINITY;
+        p.LSE[sv.lse0 + qi] = l_tot > 0.0f ? (m_run[i] + m_base) * kLn2 + __logf(l_tot) : -INFINITY;
     }
   }
 }

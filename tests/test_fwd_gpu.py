@@ -343,6 +343,54 @@ def test_softcap_polynomial_range(case, dt):
     assert inf_ok and lerr <= LSE_ABS, f"LSE abs err {lerr:.3e}"
 
 
+# bf16 softcap kernels with a cap of at most 33 (no alibi) subtract the fixed bound
+# softcap*log2(e) from every logit instead of a running row max, so the probabilities reach
+# down to 2^-95 of the largest possible one. "negative": every query is near +30 u and every
+# key near -30 u (u a unit vector), so scale*q.k is about -56 and every logit sits near -softcap
+# (the smallest probabilities the offset produces, and every block on the exact-form path);
+# a cap above 33 takes the running max. name, S, D, window left, softcap, negative
+SOFTCAP_FIXED = [
+    ("d256 narrow, logits near -30", 300, 256, 64, 30.0, True),
+    ("d256 64-key tiles, logits near -33 (largest fixed cap)", 330, 256, -1, 33.0, True),
+    ("d256 narrow, cap 40 (running max)", 300, 256, 64, 40.0, True),
+    ("d128 causal, logits near -30", 260, 128, -1, 30.0, True),
+    ("d128 causal, random scores", 260, 128, -1, 20.0, False),
+]
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("case", SOFTCAP_FIXED, ids=[c[0] for c in SOFTCAP_FIXED])
+def test_softcap_fixed_offset(case, dt):
+    import torch
+
+    from fable_attn import _C
+    name, S, D, wl, sc, neg = case
+    print(f"[fwd-softcap-fixed] {name} {dt}", flush=True)
+    B, H, Hk = 1, 4, 2
+    q = gen((B, H, S, D), 51, dt)
+    k = gen((B, Hk, S, D), 52, dt)
+    v = gen((B, Hk, S, D), 53, dt)
+    if neg:
+        u = orc.randn((D,), 54, "f32").astype(np.float64)
+        u /= np.linalg.norm(u)
+        q = orc.round_to(30.0 * u + 0.5 * q, dt)
+        k = orc.round_to(-30.0 * u + 0.5 * k, dt)
+    scale = 1.0 / math.sqrt(D)
+    o_ref, l_ref = orc.fwd(q, k, v, scale, True, wl, 0, sc, None, 0)
+    if neg:
+        assert l_ref[np.isfinite(l_ref)].max() < -0.8 * sc + math.log(S)  # logits near -softcap
+    dev = lambda a: to_dev(a, dt).transpose(1, 2).contiguous().transpose(1, 2)
+    out, lse = _C.fwd(dev(q), dev(k), dev(v), scale, True, wl, 0, sc, None, 0.0, 0)
+    torch.cuda.synchronize()
+    o, l = to_np(out), to_np(lse)
+    rel = orc.rel_rms(o, o_ref)
+    lerr, inf_ok = lse_err(l, l_ref)
+    log_errors("fwd_softcap_fixed", name, dt, o=rel, lse=lerr)
+    assert np.isfinite(o).all()
+    assert rel <= TOL[dt], f"rel_rms {rel:.3e} > {TOL[dt]}"
+    assert inf_ok and lerr <= LSE_ABS, f"LSE abs err {lerr:.3e}"
+
+
 # Small grids whose keys the library splits over several workgroups per query tile (fp32
 # partials merged by a second kernel): causal with splits that see no key, SQ < SK and SQ > SK
 # (empty rows), GQA, alibi, softcap on the one-wave D=256 loop, a right-only window, head dims
