@@ -769,8 +769,9 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
 // CF the softcap and dropout kernels, whose per-score work needs a different register
 // balance; CN the narrow masks (a window or chunk under 2048 keys), where a tall workgroup's
 // key span would be mostly masked and its fixed costs (Q rows, pipeline fill, output) are paid
-// over few tiles, so shorter workgroups, more of them per CU, win. Dropout has kernels of its
-// own, so its Philox rounds cost the other features no registers.
+// over few tiles, so shorter workgroups, more of them per CU, win; CL the plain masks on long
+// rows (below, at launch_fwd). Dropout has kernels of its own, so its Philox rounds cost the
+// other features no registers.
 template <class K>
 struct CfgTag {
   using type = K;
@@ -797,7 +798,14 @@ static int fwd_split_count(const FableFwdParams& p, long long nblk) {
   return n >= 2 ? (int)n : 1;
 }
 
-template <typename T, class C, class CF, class CN, class CS = C>
+// CL: the plain masks on long rows (no causal mask, or a causal one over at least kLongKeys
+// keys) when its grid gives at least 4 workgroups per CU (D=64: 4-wave workgroups at three
+// waves per SIMD, 1.04-1.12x over the 8-wave shape there; 0.90-0.97x on causal rows of 2048 and
+// 4096 keys, whose shorter workgroups pay the diagonal tiles and the K/V loads of half as many
+// rows more often)
+constexpr int kLongKeys = 8192;
+
+template <typename T, class C, class CF, class CN, class CS = C, class CL = C>
 static int launch_fwd(const FableFwdParams& p, hipStream_t st, FwdWs& ws) {
   const bool drop = p.dropout_p > 0.0f;
   const bool feat = drop || p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
@@ -847,6 +855,10 @@ static int launch_fwd(const FableFwdParams& p, hipStream_t st, FwdWs& ws) {
       return go(CfgTag<CF>{}, causal, Y{}, N{});
     }
     if (feat) return go(CfgTag<C>{}, causal, Y{}, N{});
+    if constexpr (!std::is_same<CL, C>::value) {
+      const long long nl = (long long)((p.SQ + CL::BR - 1) / CL::BR) * p.NH * p.batch;
+      if ((!p.causal || p.SK >= kLongKeys) && nl >= 4 * 256) return go(CfgTag<CL>{}, causal, N{}, N{});
+    }
     if constexpr (!std::is_same<CS, C>::value) {
       constexpr long long kSmallGrid = 4 * 256;  // 4 workgroups of shape C per CU
       if ((long long)((p.SQ + C::BR - 1) / C::BR) * p.NH * p.batch < kSmallGrid)
