@@ -243,18 +243,23 @@ def _check_rows(test, case, dt, got_o, got_lse, o_ref, l_ref, rows):
     # one round of causal workgroups with long rows: keys split in two
     ("key split causal fp16 B1 S8192 H6", 1, 8192, 6, True, "f16"),
     ("key split causal bf16 B1 S16384 H4", 1, 16384, 4, True, "bf16"),
+    # head dims 64 and 32 on long rows: 4-wave workgroups at three waves per SIMD
+    ("D64 long rows full fp16 B2 S4096 H32", 2, 4096, 32, False, "f16", 64),
+    ("D64 long rows causal bf16 B1 S8192 H32", 1, 8192, 32, True, "bf16", 64),
+    ("D32 long rows full fp16 B8 S1024 H16", 8, 1024, 16, False, "f16", 32),
+    ("D32 long rows causal bf16 B1 S16384 H16", 1, 16384, 16, True, "bf16", 32),
 ], ids=lambda c: c[0])
 def test_forward_full_size_sampled_rows(cfg):
     """BASELINE.json configs[1] at its full size and its S=8192 / S=4096 variants (and a
     non-causal bf16 grid of the same scale): grids that run the widest workgroup shapes.
     Sampled (batch, head) pairs and, in them, sampled query rows (first, last, both sides of
     tile boundaries, random) against the fp64 oracle, at the fp16/bf16 tolerances; LSE within
-    1e-3."""
+    1e-3. Head dims 64 and 32 on grids of long rows that take their long-row shape."""
     import torch
 
     from fable_attn import _C
-    name, B, S, H, causal, dt = cfg
-    D = 128
+    name, B, S, H, causal, dt, *width = cfg
+    D = width[0] if width else 128
     print(f"[fwd-full] {name}", flush=True)
     tdt = torch.float16 if dt == "f16" else torch.bfloat16
     g = torch.Generator(device="cuda").manual_seed(3)
