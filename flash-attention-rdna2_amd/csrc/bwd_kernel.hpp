@@ -498,10 +498,11 @@ struct BwdSplit {
   float* part;     // [n][dK | dV][rows][p.D]
 };
 
-template <int HD_, int NP_, int NSET_>
+// WPE_: waves per SIMD (two; three at head dims 32 and 64, whose kernels fit 168 registers)
+template <int HD_, int NP_, int NSET_, int WPE_ = 2>
 struct BwdKVPCfg {
   static constexpr bool PAIR = true;
-  static constexpr int HD = HD_, NP = NP_, NW = 2 * NP_, WPE = 2, DSPLIT = 1;
+  static constexpr int HD = HD_, NP = NP_, NW = 2 * NP_, WPE = WPE_, DSPLIT = 1;
   static constexpr int NSET = NSET_;       // global-load prefetch distance (tiles), 2 or 3
   static_assert(NSET == 2 || NSET == 3, "prefetch distance");
   static constexpr int NT = NW * 64;
