@@ -557,10 +557,13 @@ def cpu_baseline(inputs, heads=32, causal=True):
 SWEEP_FWD = [(1, 1024, 8, 8, 64, False), (1, 2048, 8, 8, 128, True), (1, 4096, 8, 8, 128, True),
              (1, 8192, 4, 4, 128, True), (1, 4096, 32, 32, 128, True), (1, 8192, 32, 32, 128, True),
              (1, 16384, 32, 32, 128, True), (4, 2048, 16, 16, 128, False), (1, 16384, 8, 8, 128, False),
-             (2, 2048, 16, 16, 64, True), (1, 4096, 16, 16, 256, True), (1, 8192, 32, 8, 128, True)]
+             (2, 2048, 16, 16, 64, True), (1, 4096, 16, 16, 256, True), (1, 8192, 32, 8, 128, True),
+             (2, 4096, 32, 32, 64, False), (1, 16384, 32, 32, 64, True), (8, 1024, 16, 16, 64, False),
+             (2, 4096, 32, 32, 32, False), (2, 4096, 32, 32, 96, True)]
 SWEEP_BWD = [(2, 4096, 32, 32, 128, True), (1, 4096, 8, 8, 128, True), (1, 4096, 32, 8, 128, True),
              (1, 8192, 8, 8, 128, True), (2, 2048, 16, 16, 128, False), (1, 2048, 16, 16, 64, True),
-             (1, 4096, 16, 16, 256, True), (2, 2048, 16, 16, 192, False)]
+             (1, 4096, 16, 16, 256, True), (2, 2048, 16, 16, 192, False), (2, 4096, 32, 32, 64, True),
+             (2, 4096, 32, 32, 64, False), (2, 4096, 32, 32, 32, True), (2, 4096, 32, 32, 96, True)]
 
 
 def sweep(reps=5, inner=10):
