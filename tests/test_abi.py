@@ -144,6 +144,21 @@ def test_decode_split_plan(hint, expect):
         assert 1 <= n <= 512
 
 
+@pytest.mark.parametrize("batch,ctx,expect", [
+    (16, 32768, 2),     # C4: one full round of 256 workgroups, the model's choice
+    (1, 32768, 32),     # 8 groups: the round filled (1024 keys per split)
+    (4, 32768, 8),
+    (1, 8192, 21),      # filling would leave 256 keys per split: the model's choice stays
+    (64, 4096, 1),
+])
+def test_decode_split_count(batch, ctx, expect):
+    """The automatic split count (Hq 32, Hk 8): the workgroup-round model, and a round that
+    would leave CUs idle filled while each split keeps at least 512 keys."""
+    from fable_attn import _lib
+    lib = _lib.load()
+    assert lib.fa_decode_num_splits(batch, 1, 32, 4, ctx, 0) == expect
+
+
 def _visible_tiles(SQ, SK, causal, wl=-1, wr=-1):
     """(32-key, 32-query) blocks holding at least one visible pair, counted by brute force over
     the mask of every (query, key) pair (the reference's visibility rule, bottom-right aligned)."""
