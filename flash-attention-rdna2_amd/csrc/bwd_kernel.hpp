@@ -886,10 +886,13 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt, BwdSplit sp) {
   }
 }
 
+// most shares a key block's query tiles split into (bwd_split_count)
+constexpr int kBwdMaxSplit = 8;
+
 // Sum of the query-split partials of the pair dK/dV kernel, shares in order (bitwise
 // reproducible): one thread per (row, 4 head dims), rows (dK | dV, work item, key in block);
 // keys past the sequence's end are left alone.
-template <typename T>
+template <typename T, int NMAX>
 __global__ __launch_bounds__(256) void bwd_split_merge_kernel(FableBwdParams p, BwdSplit sp) {
   const int ch = p.D / 4;
   const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
@@ -903,9 +906,16 @@ __global__ __launch_bounds__(256) void bwd_split_merge_kernel(FableBwdParams p, 
   const BwdSeq sq = bwd_seq(p, b);
   const int key = kt * sp.bk + (int)(rr - (long long)w * sp.bk);
   if (key >= sq.SK) return;
-  f32x4 acc = *(const f32x4*)(sp.part + ((long long)which * sp.rows + rr) * p.D + 4 * c);
-  for (int k = 1; k < sp.n; k++)
-    acc += *(const f32x4*)(sp.part + ((long long)(2 * k + which) * sp.rows + rr) * p.D + 4 * c);
+  // every share's partial loaded before any is added (NMAX >= n; indices past the last share
+  // repeat it and are not added): one memory latency instead of one per share
+  f32x4 v[NMAX];
+#pragma unroll
+  for (int k = 0; k < NMAX; k++)
+    v[k] = *(const f32x4*)(sp.part + ((long long)(2 * min(k, sp.n - 1) + which) * sp.rows + rr) * p.D + 4 * c);
+  f32x4 acc = v[0];
+#pragma unroll
+  for (int k = 1; k < NMAX; k++)
+    if (k < sp.n) acc += v[k];
   typename Dt<T>::V4 o;
 #pragma unroll
   for (int e = 0; e < 4; e++) o[e] = (T)acc[e];
@@ -1211,7 +1221,7 @@ inline int bwd_split_count(const FableBwdParams& p) {
   if (2 * gkv > 256) return (p.causal && steps >= 32) ? 2 : 1;
   long long n = 256 / gkv;
   n = n < steps / 16 ? n : steps / 16;
-  n = n < 8 ? n : 8;
+  n = n < kBwdMaxSplit ? n : kBwdMaxSplit;
   return n >= 2 ? (int)n : 1;
 }
 // partial rows of the split: every key block's work item times its keys
@@ -1270,7 +1280,13 @@ static int launch_bwd_ds(const FableBwdParams& p, hipStream_t st, int nkt) {
     if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;
     if (sp.n > 1) {
       const long long items = 2 * sp.rows * (p.D / 4);
-      hipLaunchKernelGGL((bwd_split_merge_kernel<T>), dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, p, sp);
+      const dim3 mg((unsigned)((items + 255) / 256));
+      if (sp.n <= 2)
+        hipLaunchKernelGGL((bwd_split_merge_kernel<T, 2>), mg, dim3(256), 0, st, p, sp);
+      else if (sp.n <= 4)
+        hipLaunchKernelGGL((bwd_split_merge_kernel<T, 4>), mg, dim3(256), 0, st, p, sp);
+      else
+        hipLaunchKernelGGL((bwd_split_merge_kernel<T, kBwdMaxSplit>), mg, dim3(256), 0, st, p, sp);
       if (int rc = launch_status("fable_attn_bwd (dkdv merge)")) return rc;
     }
   } else {

@@ -14,7 +14,7 @@ __device__ __forceinline__ float ld_as_f32(const void* p, long long i) {
   return (float)((const TI*)p)[i];
 }
 
-template <typename TI, typename TO>
+template <typename TI, typename TO, int NC>
 __global__ __launch_bounds__(256) void combine_kernel(CombineParams c) {
   const long long rows = (long long)c.B * c.S * c.H;
   const int dgrp = (c.D + 63) / 64;
@@ -26,20 +26,54 @@ __global__ __launch_bounds__(256) void combine_kernel(CombineParams c) {
   const long long bs = row / c.H;
   const int s = (int)(bs % c.S), b = (int)(bs / c.S);
   const long long lbase = (long long)b * c.lp_b + (long long)h * c.lp_h + (long long)s * c.lp_seq;
+  // splits in chunks of NC (2, 4 or 8, at least the split count up to 8) whose loads are all
+  // issued before any is used (indices past the last split repeat it and are not used): a few
+  // memory latencies instead of one per split; sums in split order
+  constexpr int kC = NC;
+  const int ns = c.nsplit;
   float m = -INFINITY;
-  for (int k = 0; k < c.nsplit; k++) m = fmaxf(m, c.lse_partial[lbase + k * c.lp_split]);
+  for (int k0 = 0; k0 < ns; k0 += kC) {
+    float l[kC];
+#pragma unroll
+    for (int u = 0; u < kC; u++) l[u] = c.lse_partial[lbase + (long long)min(k0 + u, ns - 1) * c.lp_split];
+#pragma unroll
+    for (int u = 0; u < kC; u++)
+      if (k0 + u < ns) m = fmaxf(m, l[u]);
+  }
   if (d >= c.D) return;
   const long long obase = (long long)b * c.op_b + (long long)s * c.op_seq + (long long)h * c.op_h + d;
   float acc = 0.0f, ws = 0.0f;
   if (m != -INFINITY) {
-    for (int k = 0; k < c.nsplit; k++) {
-      const float w = __expf(c.lse_partial[lbase + k * c.lp_split] - m);
-      ws += w;
-      acc += w * ld_as_f32<TI>(c.out_partial, obase + k * c.op_split);
+    for (int k0 = 0; k0 < ns; k0 += kC) {
+      float l[kC], o[kC];
+#pragma unroll
+      for (int u = 0; u < kC; u++) {
+        const long long k = min(k0 + u, ns - 1);
+        l[u] = c.lse_partial[lbase + k * c.lp_split];
+        o[u] = ld_as_f32<TI>(c.out_partial, obase + k * c.op_split);
+      }
+#pragma unroll
+      for (int u = 0; u < kC; u++) {
+        if (k0 + u < ns) {
+          const float w = __expf(l[u] - m);
+          ws += w;
+          acc += w * o[u];
+        }
+      }
     }
   }
   const float r = m != -INFINITY ? acc / fmaxf(ws, 1e-30f) : 0.0f;
   ((TO*)c.out)[row * c.D + d] = (TO)r;
+}
+
+template <typename TI, typename TO>
+static void launch_nc(const CombineParams& c, dim3 grid, dim3 block, hipStream_t st) {
+  if (c.nsplit <= 2)
+    hipLaunchKernelGGL((combine_kernel<TI, TO, 2>), grid, block, 0, st, c);
+  else if (c.nsplit <= 4)
+    hipLaunchKernelGGL((combine_kernel<TI, TO, 4>), grid, block, 0, st, c);
+  else
+    hipLaunchKernelGGL((combine_kernel<TI, TO, 8>), grid, block, 0, st, c);
 }
 
 template <typename TI>
@@ -47,9 +81,9 @@ static int launch_in(const CombineParams& c, hipStream_t st) {
   const long long items = (long long)c.B * c.S * c.H * ((c.D + 63) / 64);
   dim3 grid((unsigned)((items + 3) / 4)), block(256);
   switch (c.out_dtype) {
-    case FA_F16: hipLaunchKernelGGL((combine_kernel<TI, _Float16>), grid, block, 0, st, c); break;
-    case FA_BF16: hipLaunchKernelGGL((combine_kernel<TI, __bf16>), grid, block, 0, st, c); break;
-    case FA_F32: hipLaunchKernelGGL((combine_kernel<TI, float>), grid, block, 0, st, c); break;
+    case FA_F16: launch_nc<TI, _Float16>(c, grid, block, st); break;
+    case FA_BF16: launch_nc<TI, __bf16>(c, grid, block, st); break;
+    case FA_F32: launch_nc<TI, float>(c, grid, block, st); break;
     default: return fail(FA_ERR_DTYPE, "fa_combine_launch: out dtype %d", c.out_dtype);
   }
   return launch_status("fa_combine_launch");

@@ -533,16 +533,17 @@ __global__ __launch_bounds__(256) void dec_partial_f32_kernel(FableDecParams p, 
 }
 
 // merge nsplit partials of one (token, head): grid (batch*nq, NH), block HD
-template <typename T, int HD>
+template <typename T, int HD, int NC>
 __global__ __launch_bounds__(256) void dec_combine_kernel(FableDecParams p) {
   // one thread per column of the kernel width HD; the head dim p.HD <= HD sets the strides
   const int row = blockIdx.x, h = blockIdx.y, d = threadIdx.x, HDr = p.HD;
   const int dc = min(d, HDr - 1);  // threads past the head dim read a valid column, store nothing
   const float* base = p.scratch + ((long long)row * p.NH + h) * p.nsplit * (HDr + 2);
-  // the splits in chunks of kC whose loads are all issued before any is used (indices past the
-  // last split repeat it and are not used): a few memory latencies instead of one per split (a
-  // batch-1 decode of 21 splits took 12 us here with one load per step); sums in split order
-  constexpr int kC = 8;
+  // the splits in chunks of NC (2, 4 or 8, at least the split count up to 8) whose loads are all
+  // issued before any is used (indices past the last split repeat it and are not used): a few
+  // memory latencies instead of one per split (a batch-1 decode of 21 splits took 12 us here
+  // with one load per step); sums in split order
+  constexpr int kC = NC;
   const int ns = p.nsplit;
   auto rec = [&](int s) { return base + (long long)min(s, ns - 1) * (HDr + 2); };
   float gm = -INFINITY;
@@ -651,7 +652,13 @@ static int launch_dec(const FableDecParams& p, hipStream_t st, const void* nk, c
     if (p.nsplit == 1) return FA_OK;
   }
   if (int rc = launch_status("fable_attn_dec (partial)")) return rc;
-  hipLaunchKernelGGL((dec_combine_kernel<T, HD>), dim3(p.batch * p.nq, p.NH), dim3(HD), 0, st, p);
+  const dim3 cg(p.batch * p.nq, p.NH);
+  if (p.nsplit <= 2)
+    hipLaunchKernelGGL((dec_combine_kernel<T, HD, 2>), cg, dim3(HD), 0, st, p);
+  else if (p.nsplit <= 4)
+    hipLaunchKernelGGL((dec_combine_kernel<T, HD, 4>), cg, dim3(HD), 0, st, p);
+  else
+    hipLaunchKernelGGL((dec_combine_kernel<T, HD, 8>), cg, dim3(HD), 0, st, p);
   return launch_status("fable_attn_dec (combine)");
 }
 
