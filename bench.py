@@ -560,6 +560,10 @@ SWEEP_FWD = [(1, 1024, 8, 8, 64, False), (1, 2048, 8, 8, 128, True), (1, 4096, 8
              (2, 2048, 16, 16, 64, True), (1, 4096, 16, 16, 256, True), (1, 8192, 32, 8, 128, True),
              (2, 4096, 32, 32, 64, False), (1, 16384, 32, 32, 64, True), (8, 1024, 16, 16, 64, False),
              (2, 4096, 32, 32, 32, False), (2, 4096, 32, 32, 96, True)]
+# paged decode: (batch, ctx, page); (1, 32768, 32) is the shape of the reference's published decode
+# figure, (16, 32768, 256) is C4
+SWEEP_DEC = [(1, 32768, 32), (1, 32768, 256), (1, 131072, 256), (4, 32768, 256), (16, 32768, 256),
+             (64, 8192, 256), (128, 2048, 16)]
 SWEEP_BWD = [(2, 4096, 32, 32, 128, True), (1, 4096, 8, 8, 128, True), (1, 4096, 32, 8, 128, True),
              (1, 8192, 8, 8, 128, True), (2, 2048, 16, 16, 128, False), (1, 2048, 16, 16, 64, True),
              (1, 4096, 16, 16, 256, True), (2, 2048, 16, 16, 192, False), (2, 4096, 32, 32, 64, True),
@@ -567,10 +571,11 @@ SWEEP_BWD = [(2, 4096, 32, 32, 128, True), (1, 4096, 8, 8, 128, True), (1, 4096,
 
 
 def sweep(reps=5, inner=10):
-    """Markdown table of forward (fp16) and backward (bf16, dS workspace) rates through the
+    """Markdown tables of forward (fp16) and backward (bf16, dS workspace) rates through the
     binding the public API uses (fable_attn._C.fwd / bwd), per shape: the median of `reps`
     HIP-event timings of `inner` back-to-back calls, and whether the small-grid split applies
-    (forward: key split; backward: query split of the dK/dV kernel)."""
+    (forward: key split; backward: query split of the dK/dV kernel); and of paged decode
+    (flash_attn_with_kvcache) from graph replays."""
     import torch
     from fable_attn import _C, _lib
 
@@ -621,6 +626,37 @@ def sweep(reps=5, inner=10):
             out.append(f"| {pas} | {B} | {S} | {Hq} / {Hk} | {D} | {'yes' if causal else 'no'} | "
                        f"{str(dt)[6:]} | {ms:.4f} | {fl / (ms * 1e-3) / 1e12:.0f} | {'yes' if split else 'no'} |")
             del q, k, v
+    # paged decode through flash_attn_with_kvcache, timed as replays of a captured HIP graph of
+    # `inner` calls: at small batch a call's kernels take less time than the host needs to issue
+    # it, and back-to-back calls would time the host
+    from fable_attn.flash_attn_interface import flash_attn_with_kvcache
+    out += ["", "| pass | batch | ctx | page | Hq / Hk | D | dtype | us per call | GB/s (K+V once) | % of 8 TB/s | splits |",
+            "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for B, ctx, page in SWEEP_DEC:
+        Hq, Hk, D = 32, 8, 128
+        nb = B * (ctx // page)
+        kc = torch.randn(nb, page, Hk, D, device="cuda", dtype=torch.float16, generator=g)
+        vc = torch.randn(nb, page, Hk, D, device="cuda", dtype=torch.float16, generator=g)
+        bt = torch.randperm(nb, generator=torch.Generator().manual_seed(1)).view(B, ctx // page).int().cuda()
+        lens = torch.full((B,), ctx, dtype=torch.int32, device="cuda")
+        q = torch.randn(B, 1, Hq, D, device="cuda", dtype=torch.float16, generator=g)
+        call = lambda: flash_attn_with_kvcache(q, kc, vc, cache_seqlens=lens, block_table=bt, causal=True)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                call()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for _ in range(inner):
+                call()
+        ms = timed(graph.replay) / inner
+        byts = 2.0 * B * ctx * Hk * D * 2
+        out.append(f"| decode | {B} | {ctx} | {page} | {Hq} / {Hk} | {D} | float16 | {ms * 1e3:.1f} | "
+                   f"{byts / (ms * 1e-3) / 1e9:.0f} | {byts / (ms * 1e-3) / 8e12 * 100:.0f}% | "
+                   f"{_C.num_splits(B, 1, Hq, Hq // Hk, ctx, 0)} |")
+        del graph, kc, vc
     return "\n".join(out)
 
 
