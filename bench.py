@@ -444,7 +444,7 @@ FWD_C1_KERNEL = (r"_ZN2fa10fwd_kernelIDF16_NS_6FwdCfgILi64E.*ELb0ELb0ELb0EEEv14F
 BWD_C3_KERNELS = (r"_ZN2fa15bwd_dsum_kernelIDF16b.*", r"_ZN2fa20bwd_dkdv_pair_kernelIDF16b.*",
                   r"_ZN2fa16bwd_dq_ds_kernelIDF16b.*")
 DEC_C4_KERNELS = (r"_ZN2fa18dec_partial_kernelIDF16_Li128ELb0ELb1EEEv14FableDecParamsiii",
-                  r"_ZN2fa18dec_combine_kernelIDF16_Li128EEEv14FableDecParams")
+                  r"_ZN2fa18dec_combine_kernelIDF16_Li128ELi[0-9]+EEEv14FableDecParams")
 VARLEN_C5_KERNEL = r"_ZN2fa10fwd_kernelIDF16bNS_6FwdCfgILi256E.*ELb1ELb1ELb0EEEv14FableFwdParamsiNS_8FwdSplitE"
 
 
