@@ -769,8 +769,8 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
 // CF the softcap and dropout kernels, whose per-score work needs a different register
 // balance; CN the narrow masks (a window or chunk under 2048 keys), where a tall workgroup's
 // key span would be mostly masked and its fixed costs (Q rows, pipeline fill, output) are paid
-// over few tiles, so shorter workgroups, more of them per CU, win; CL the plain masks on long
-// rows (below, at launch_fwd). Dropout has kernels of its own, so its Philox rounds cost the
+// over few tiles, so shorter workgroups, more of them per CU, win; CL and CR the plain masks
+// on long and on short causal rows (below, at launch_fwd). Dropout has kernels of its own, so its Philox rounds cost the
 // other features no registers.
 template <class K>
 struct CfgTag {
@@ -804,8 +804,14 @@ static int fwd_split_count(const FableFwdParams& p, long long nblk) {
 // 4096 keys, whose shorter workgroups pay the diagonal tiles and the K/V loads of half as many
 // rows more often)
 constexpr int kLongKeys = 8192;
+// CR: the plain masks on short causal rows (at most kShortKeys keys) when C's grid gives at
+// least 4 workgroups per CU (D=128: 2-wave workgroups of 64 rows and 32-key tiles; on a row of
+// 512 keys half the tiles of a 256-row workgroup straddle the diagonal. Varlen batches of
+// 64-1024-token sequences 1.53-1.58x, dense B16 S1024 H32 1.22x, B64 S512 1.16x; on a grid of
+// 512 workgroups (B8 S1024 H16) 0.81x, so larger grids only)
+constexpr int kShortKeys = 1024;
 
-template <typename T, class C, class CF, class CN, class CS = C, class CL = C>
+template <typename T, class C, class CF, class CN, class CS = C, class CL = C, class CR = C>
 static int launch_fwd(const FableFwdParams& p, hipStream_t st, FwdWs& ws) {
   const bool drop = p.dropout_p > 0.0f;
   const bool feat = drop || p.softcap > 0.0f || p.alibi_slopes != nullptr || p.attn_chunk > 0 ||
@@ -855,6 +861,10 @@ static int launch_fwd(const FableFwdParams& p, hipStream_t st, FwdWs& ws) {
       return go(CfgTag<CF>{}, causal, Y{}, N{});
     }
     if (feat) return go(CfgTag<C>{}, causal, Y{}, N{});
+    if constexpr (!std::is_same<CR, C>::value) {
+      const long long nc = (long long)((p.SQ + C::BR - 1) / C::BR) * p.NH * p.batch;
+      if (p.causal && p.SK <= kShortKeys && nc >= 4 * 256) return go(CfgTag<CR>{}, causal, N{}, N{});
+    }
     if constexpr (!std::is_same<CL, C>::value) {
       const long long nl = (long long)((p.SQ + CL::BR - 1) / CL::BR) * p.NH * p.batch;
       if ((!p.causal || p.SK >= kLongKeys) && nl >= 4 * 256) return go(CfgTag<CL>{}, causal, N{}, N{});

@@ -185,7 +185,7 @@ def _varlen_split_bytes(lens, H, gqa, D, causal, dt):
 
 @pytest.mark.parametrize("dt", ["f16", "bf16"])
 @pytest.mark.parametrize("kind", ["plain", "seqused", "window_softcap_d256", "split", "split_seqused",
-                                  "split_full_d128", "split_ragged"])
+                                  "split_full_d128", "split_ragged", "short_rows_d128", "short_rows_d64"])
 def test_varlen_parity(kind, dt):
     print(f"[varlen] {kind} {dt}", flush=True)
     if kind == "plain":
@@ -202,9 +202,14 @@ def test_varlen_parity(kind, dt):
     elif kind == "split_full_d128":
         assert _varlen_split_bytes([900, 1500], 2, 2, 128, False, dt) > 0
         r = _varlen(dt, [900, 1500], D=128, H=2, gqa=2, causal=False)
-    else:                              # empty and one-row sequences among split ones
+    elif kind == "split_ragged":       # empty and one-row sequences among split ones
         assert _varlen_split_bytes([700, 0, 1300, 1, 900], 2, 1, 64, True, dt) > 0
         r = _varlen(dt, [700, 0, 1300, 1, 900], D=64, H=2, gqa=1)
+    else:                              # many short causal sequences: the short-row shape (a grid
+        # of 128 sequences x 8 heads, one 256-row tile each, at least 4 workgroups per CU)
+        lens = np.random.default_rng(12).integers(1, 257, 128).tolist()
+        lens[5], lens[77] = 0, 1
+        r = _varlen(dt, lens, D=128 if kind.endswith("d128") else 64, H=8, gqa=2)
     o, l, o_ref, l_ref = r
     rel = orc.rel_rms(o, o_ref)
     lerr, inf_ok = lse_err(l, l_ref)
@@ -243,6 +248,11 @@ def _check_rows(test, case, dt, got_o, got_lse, o_ref, l_ref, rows):
     # one round of causal workgroups with long rows: keys split in two
     ("key split causal fp16 B1 S8192 H6", 1, 8192, 6, True, "f16"),
     ("key split causal bf16 B1 S16384 H4", 1, 16384, 4, True, "bf16"),
+    # short causal rows on grids of at least 4 workgroups per CU: 2-wave workgroups of 64 rows
+    ("D128 short rows causal fp16 B16 S1024 H32", 16, 1024, 32, True, "f16", 128),
+    ("D96 short rows causal bf16 B64 S512 H32", 64, 512, 32, True, "bf16", 96),
+    ("D64 short rows causal fp16 B16 S1024 H32", 16, 1024, 32, True, "f16", 64),
+    ("D32 short rows causal bf16 B64 S512 H32", 64, 512, 32, True, "bf16", 32),
     # head dims 64 and 32 on long rows: 4-wave workgroups at three waves per SIMD
     ("D64 long rows full fp16 B2 S4096 H32", 2, 4096, 32, False, "f16", 64),
     ("D64 long rows causal bf16 B1 S8192 H32", 1, 8192, 32, True, "bf16", 64),
