@@ -1,8 +1,9 @@
 """Benchmark of the hot path on one MI355X (driver contract: one JSON line on stdout).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extras fwd,bwd,decode,varlen]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--extras fwd,bwd,decode,varlen,gemm]
 
-(--extras: fwd = C2 at S=4096/8192 and C1; c2sizes and c1 name those parts alone.)
+(--extras: fwd = C2 at S=4096/8192 and C1; c2sizes and c1 name those parts alone; gemm = the fp16
+GEMM calibration of the MFMA roofline, gemm_random its random-operand half alone.)
 
 A step is one pass of the hot path over one batch of synthetic input:
   headline (`value`): BASELINE.json configs[1], causal fp16 forward through flash_attn_func,
@@ -20,7 +21,9 @@ decode, C5 varlen), each measured the same way (at least 3 untimed steps and 150
 load, then 20 timed steps; mean and median of the per-step HIP-event times) and each with its
 own `roofline` block (over the whole step's kernels) and `cpu_baseline` (the same torch
 reference path on CPU tensors: per-head autograd for C3, pages gathered per sequence for C4,
-per sequence and head for C5); they are not the headline.
+per sequence and head for C5); they are not the headline. `extra.gemm_fp16_calibration` is the
+vendor GEMM (torch.matmul) on fp16 8192^3 with random and with constant operands: what a dense fp16
+product sustains on the same box, since the chip holds a lower clock for random operands.
 """
 import argparse
 import json
@@ -126,6 +129,31 @@ def _fwd_traffic(B, S, H, D, causal):
     if (B, S, H, D, causal) == (1, 1024, 8, 64, False):
         return profiled_traffic(FWD_C1_KERNEL)
     return None
+
+
+def bench_gemm(steps, warmup, n=8192, seed=0, warm_ms=EXTRA_WARM_MS, kinds=("random", "constant")):
+    """Calibration of the MFMA roofline on the box: the vendor GEMM (torch.matmul, hipBLASLt)
+    on fp16 n x n x n, with N(0, 1) operands like the attention workloads and with constant
+    ones. The matrix cores draw more power on random operands, and the chip holds a lower clock
+    for them (measured ~1.8 GHz against ~2.3 GHz for constant operands): the random-operand rate
+    is what a dense fp16 product sustains here, against the 2.5 PFLOP/s nameplate (2.4 GHz)."""
+    import torch
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    flops = 2.0 * n ** 3
+    res = {"n": n, "dtype": "fp16", "flops": flops}
+    for kind in kinds:
+        if kind == "random":
+            a = torch.randn(n, n, device="cuda", dtype=torch.float16, generator=g)
+            b = torch.randn(n, n, device="cuda", dtype=torch.float16, generator=g)
+        else:
+            a = torch.full((n, n), 0.001, device="cuda", dtype=torch.float16)
+            b = a.clone()
+        per = []
+        _, ev = time_steps(lambda: a @ b, steps, warmup, per, warm_ms)
+        res[f"{kind}_tflops"] = flops / (_median(per) * 1e-3) / 1e12
+        res[f"{kind}_frac"] = round(res[f"{kind}_tflops"] / PEAK_MFMA_TFLOPS, 4)
+        del a, b
+    return res
 
 
 def bench_bwd(steps, warmup, B=2, S=4096, H=32, D=128, seed=0, warm_ms=EXTRA_WARM_MS, cpu_heads=0):
@@ -668,7 +696,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-heads", type=int, default=32)
-    ap.add_argument("--extras", default="fwd,bwd,decode,varlen")
+    ap.add_argument("--extras", default="fwd,bwd,decode,varlen,gemm")
     ap.add_argument("--copy-calib", action="store_true",
                     help="also run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -744,6 +772,11 @@ def main():
             elif name == "varlen":
                 extra["varlen_C5"] = bench_varlen(max(20, a.steps), max(3, a.warmup),
                                                   cpu_heads=4 if cpu_on else 0)
+            elif name in ("gemm", "gemm_random"):
+                # (gemm_random: the random operands alone, for a counter run of one kind)
+                extra["gemm_fp16_calibration"] = bench_gemm(max(20, a.steps), max(3, a.warmup),
+                                                            kinds=("random",) if name == "gemm_random"
+                                                            else ("random", "constant"))
             log(f"[bench] extra {name} done")
         except RuntimeError as e:
             extra[name] = {"error": str(e)[:300]}
