@@ -523,25 +523,26 @@ struct BwdKVPCfg {
   static_assert(CH % LT == 0 && (BQ * DCH) % LT == 0, "loader split");
 };
 
-template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false, bool DSW = false>
-__global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
-                          amdgpu_waves_per_eu(C::WPE, C::WPE))) void
-bwd_dkdv_pair_kernel(FableBwdParams p, int nkt, BwdSplit sp) {
+// One work item of the pair kernel: key block w % nkt of K/V group w / nkt, query share `share`
+// (LOOP: called from the persistent kernel's item loop)
+template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP, bool DSW, bool LOOP>
+__device__ __forceinline__ void bwd_pair_item(const FableBwdParams& p, int nkt, const BwdSplit& sp, int w, int share) {
   using V8 = typename Dt<T>::V8;
   using V4 = typename Dt<T>::V4;
   __shared__ __attribute__((aligned(16))) T lds[4 * C::STAGE];
   __shared__ __attribute__((aligned(16))) float rowv[4][2][C::BQ];  // [stage][lse2 | D][q]
   // P deriv hand-over, [buffer][pair][rq][lane] x 4 floats: lane-contiguous 16-byte records
   __shared__ __attribute__((aligned(16))) f32x4 pdx[2][C::NP][4][64];
-  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // (in the item loop the thread index passes through an empty asm: the compiler otherwise
+  // computes the per-lane offsets once, ahead of the loop, and holds them in registers the
+  // steps need; D=128 then spilled)
+  int tid_ = threadIdx.x;
+  if constexpr (LOOP) asm volatile("" : "+v"(tid_));
+  const int tid = tid_, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31, hh = lane >> 5, j16 = lane & 15, mh = (lane >> 4) & 1;
   const bool dpw = wave >= C::NP;  // dP-wave (holds V, accumulates dK)
   const int pair = dpw ? wave - C::NP : wave;
 
-  // work item (grid share-major: every key block's first share, then the second, ...)
-  const int nitems = gridDim.x / sp.n;
-  const int share = blockIdx.x / nitems;
-  const int w = xcd_group_remap(blockIdx.x - share * nitems, nitems, nkt, 1, kBwdUMajor);
   const int kt = w % nkt, zh = w / nkt;
   const int kvh = zh % p.Hk, b = zh / p.Hk;
   const BwdSeq sq = bwd_seq(p, b);
@@ -886,6 +887,52 @@ bwd_dkdv_pair_kernel(FableBwdParams p, int nkt, BwdSplit sp) {
   }
 }
 
+// Workgroups of the persistent pair kernel per workgroup slot of a CU: the CUs of an MI355X
+// (256 in 8 XCDs)
+constexpr int kBwdPersistWG = 256, kBwdXcd = 8;
+// The persistent kernel runs grids of at least two rounds of workgroups whose longest item has
+// at most kBwdPersistMaxSteps query-tile steps (sequences of up to 512 queries, or packed
+// batches whose longest sequence is), when the batch is packed (sequences of unequal length:
+// many items are short or empty) or, for a dense batch, causal with one workgroup per CU:
+// B=64 S=512 H=32 D=128 causal 1.14x, packed 1..512-row sequences 1.32x (D=128) and 1..256-row
+// ones 1.17x (D=64, three workgroups per CU). Dense grids of three workgroups per CU (D=64
+// S=512 0.97-0.99x), dense non-causal ones (0.97-0.98x) and longer items (S=1024 0.98x, S=4096
+// 0.96x: the fixed item lists balance less well than the dispatcher once its gaps no longer
+// matter) keep the dispatched grid.
+constexpr long long kBwdPersistMinItems = 512;
+constexpr long long kBwdPersistMaxSteps = 16;
+// The pair kernel. Dispatched (PERSIST false): one work item per workgroup, the grid
+// share-major (every key block's first share, then the second, ...) and mapped to items by
+// xcd_group_remap. Persistent (PERSIST true, no query split): a fixed grid of kBwdPersistWG
+// workgroups per CU slot, each running a fixed list of items. Workgroup L of the dispatched
+// grid runs on XCD L % 8 (round-robin dispatch), so XCD x's share of the work is the items of
+// L = x + 8 j, j = 0, 1, ..., in that order; the R persistent workgroups of XCD x (blockIdx % 8
+// = x) take j in a snake, workgroup r the j = r, 2R-1-r, 2R+r, 4R-1-r, ...: a causal grid's
+// key blocks alternate heavy and light along j, and the snake pairs them. Short items (a few
+// query tiles per key block) otherwise leave CUs idle between workgroups: at B=64 S=512 H=32
+// D=128 the dispatched grid's CUs sat idle a median 7 us between 24 us workgroups.
+template <typename T, class C, bool CAUSAL, bool FEAT, bool DROP = false, bool DSW = false, bool PERSIST = false>
+__global__ __attribute__((amdgpu_flat_work_group_size(C::NT, C::NT),
+                          amdgpu_waves_per_eu(C::WPE, C::WPE))) void
+bwd_dkdv_pair_kernel(FableBwdParams p, int nkt, BwdSplit sp) {
+  if constexpr (!PERSIST) {
+    const int nitems = gridDim.x / sp.n;
+    const int share = blockIdx.x / nitems;
+    bwd_pair_item<T, C, CAUSAL, FEAT, DROP, DSW, false>(p, nkt, sp, xcd_group_remap(blockIdx.x - share * nitems, nitems, nkt, 1, kBwdUMajor),
+                                                        share);
+  } else {
+    const int x = blockIdx.x % kBwdXcd, r = blockIdx.x / kBwdXcd, R = gridDim.x / kBwdXcd;
+    const long long nitems = (long long)nkt * p.Hk * p.B;
+    for (long long k = 0;; k++) {
+      const long long j = k * R + ((k & 1) ? R - 1 - r : r);
+      const long long L = j * kBwdXcd + x;  // increases with k
+      if (L >= nitems) break;
+      if (k > 0) __syncthreads();  // the last item's LDS reads done before this one zeroes it
+      bwd_pair_item<T, C, CAUSAL, FEAT, DROP, DSW, true>(p, nkt, sp, xcd_group_remap((int)L, (int)nitems, nkt, 1, kBwdUMajor), 0);
+    }
+  }
+}
+
 // most shares a key block's query tiles split into (bwd_split_count)
 constexpr int kBwdMaxSplit = 8;
 
@@ -938,7 +985,8 @@ __global__ __launch_bounds__(256) void bwd_dsum_kernel(FableBwdParams p, int rbl
   const int h = zh % p.Hq, b = zh / p.Hq;
   if (blockIdx.x == 0) ds_build_table(p);  // the dS workspace's tile table, for the next kernels
   const BwdSeq sq = bwd_seq(p, b);
-  if (sq.SQ <= 0) return;
+  // (a packed batch's grid covers its longest sequence: the blocks past a shorter one's end)
+  if (sq.SQ <= 0 || rb * DSUM_RPT * RPB >= sq.SQ) return;
   const int c = tid % LPR;
   // chunks past a head dim p.D below HD read the row's first chunk and add nothing
   const bool cok = 8 * c < p.D;
@@ -1275,8 +1323,16 @@ static int launch_bwd_ds(const FableBwdParams& p, hipStream_t st, int nkt) {
       if (p.ds_ws_bytes >= off + (long long)n * 2 * bwd_split_rows(p) * p.D * 4)
         sp = BwdSplit{n, nkt, CKV::BK, bwd_split_rows(p), (float*)((char*)p.ds_ws + off)};
     }
-    hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)(gkv * sp.n)),
-                       dim3(CKV::NT), 0, st, p, nkt, sp);
+    // workgroups of the config that fit one CU at once (its waves per SIMD over its waves per CU)
+    constexpr int kPerCu = 4 * CKV::WPE / CKV::NW > 0 ? 4 * CKV::WPE / CKV::NW : 1;
+    const long long item_steps = (long long)((p.SQ + 31) / 32) * p.gqa;  // the most an item takes
+    const bool persist_shape = p.cu_q != nullptr || (CAUSAL && kPerCu == 1);
+    if (sp.n == 1 && persist_shape && gkv >= kBwdPersistMinItems * kPerCu && item_steps <= kBwdPersistMaxSteps)
+      hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true, true>), dim3((unsigned)(kBwdPersistWG * kPerCu)),
+                         dim3(CKV::NT), 0, st, p, nkt, sp);
+    else
+      hipLaunchKernelGGL((bwd_dkdv_pair_kernel<T, CKV, CAUSAL, FEAT, DROP, true>), dim3((unsigned)(gkv * sp.n)),
+                         dim3(CKV::NT), 0, st, p, nkt, sp);
     if (int rc = launch_status("fable_attn_bwd (dkdv)")) return rc;
     if (sp.n > 1) {
       const long long items = 2 * sp.rows * (p.D / 4);

@@ -64,6 +64,13 @@ CASES = [
     ("split D64 full S1100x900", 1, 2, 2, 1100, 900, 64, False, -1, -1, 0.0, False),
     ("split D96 window (300,0) softcap", 1, 4, 2, 700, 700, 96, True, 300, 0, 20.0, False),
     ("split D32 causal alibi", 1, 4, 4, 1200, 1200, 32, True, -1, -1, 0.0, True),
+    # grids of many short causal key blocks at head dim 128 (at least 512 work items, at most 16
+    # query tiles each): the persistent dK/dV kernel, each workgroup running a list of items
+    # ("ds" path only)
+    ("persist D128 causal B8 S512", 8, 16, 16, 512, 512, 128, True, -1, -1, 0.0, False),
+    ("persist D128 causal B8 S500 tail", 8, 16, 16, 500, 500, 128, True, -1, -1, 0.0, False),
+    ("persist D128 causal gqa2 B32 S256", 32, 16, 8, 256, 256, 128, True, -1, -1, 0.0, False),
+    ("persist D128 window (100,0) softcap", 8, 16, 16, 512, 512, 128, True, 100, 0, 20.0, False),
 ]
 
 

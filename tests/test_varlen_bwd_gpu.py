@@ -211,3 +211,46 @@ def test_varlen_backward_query_split(case, dt):
         check_grads("varlen_bwd_split", f"{case[0]} seq {i}", dt, got, ref, model, vanish_ok=True)
         if su_q:   # rows past the used lengths get zero gradient
             assert not to_np(dq[b:cq[i + 1]]).any() and not to_np(dk[d:ck[i + 1]]).any()
+
+
+# packed batches of many short sequences (lengths 1 .. 512 at head dim 128, 1 .. 256 at 64, GQA):
+# at least two rounds of dK/dV work items with at most 16 query-tile steps each, which the
+# persistent dK/dV kernel runs (each workgroup a fixed list of items)
+PERSIST_CASES = [
+    ("persist D128 causal 160 seqs", 160, 512, 4, 4, 128, True, -1, -1, 0.0),
+    ("persist D64 causal gqa2 200 seqs", 200, 256, 4, 2, 64, True, -1, -1, 0.0),
+    ("persist D128 window softcap 160 seqs", 160, 512, 4, 4, 128, True, 60, 0, 15.0),
+]
+
+
+@pytest.mark.parametrize("dt", ["f16", "bf16"])
+@pytest.mark.parametrize("case", PERSIST_CASES, ids=[c[0] for c in PERSIST_CASES])
+def test_varlen_backward_persistent(case, dt):
+    """Every sequence against the fp64 oracle (and its rounding model), bitwise reproducible over
+    two runs; lengths include 1 and the longest allowed."""
+    import torch
+
+    print(f"[varlen-bwd-persist] {case[0]} {dt}", flush=True)
+    name, nseq, lmax, Hq, Hk, D, causal, wl, wr, sc = case
+    rng = np.random.default_rng(7)
+    lens = rng.integers(1, lmax + 1, nseq)
+    lens[0], lens[1], lens[-1] = 1, lmax, 2
+    lens = [int(x) for x in lens]
+    full = (name, lens, None, Hq, Hk, D, causal, wl, wr, sc)
+    lq, lk, q, k, v, do = _make(full, dt)
+    grads = _varlen_kernel(full, dt, lq, lk, q, k, v, do)
+    out = to_np(_varlen_kernel.last_out)
+    again = _varlen_kernel(full, dt, lq, lk, q, k, v, do)
+    for a, b in zip(grads, again):
+        assert torch.equal(a, b), "varlen backward differs between runs"
+    dq, dk, dv = (to_np(x) for x in grads)
+    cu = _cu(lens)
+    scale = 1.0 / math.sqrt(D)
+    bhsd = lambda x: np.ascontiguousarray(x.transpose(1, 0, 2)[None])
+    for i in range(nseq):
+        a, b = cu[i], cu[i + 1]
+        args = (bhsd(q[a:b]), bhsd(k[a:b]), bhsd(v[a:b]), bhsd(do[a:b]), scale, causal, wl, wr, sc, None)
+        ref = orc.bwd(*args)
+        model = orc.bwd(*args, model=dt, stored_o=bhsd(out[a:b]))
+        got = [x[a:b].transpose(1, 0, 2)[None] for x in (dq, dk, dv)]
+        check_grads("varlen_bwd_persist", f"{name} seq {i} len {lens[i]}", dt, got, ref, model, vanish_ok=True)
