@@ -253,8 +253,13 @@ __device__ __forceinline__ int xcd_remap(int L, int N) {
 //    the HBM bytes (1.80 vs 1.12 GB per launch) for the same time.
 //  * Groups past the last full round of 8 are cut into 8 contiguous ranges.
 // u-major limits (items per XCD): the forward kernels keep the 4 heads per XCD of long causal
-// sequences group after group; the backward kernels gain from u-major up to 512
-constexpr int kFwdUMajor = 128, kBwdUMajor = 512;
+// sequences group after group; the backward kernels gain from u-major up to 512. Dense plain
+// causal forward grids up to head dim 128 run u-major up to kFwdUMajorCausal (their q tiles
+// range from one key tile to the whole row, and group after group left the light tiles of the
+// last heads to the end): B8 S2048 H32 D128 1.20-1.22x, D96 1.31x, D32 1.27x, B4 S4096 D96
+// 1.18x, D64 1.13-1.17x, C2 1.00-1.015x. Non-causal tiles are all alike, and u-major only
+// spread a CU's concurrent workgroups over more heads (B4 S4096 non-causal 0.92x).
+constexpr int kFwdUMajor = 128, kBwdUMajor = 512, kFwdUMajorCausal = 512;
 __device__ __forceinline__ int xcd_group_remap(int L, int N, int U, int gqa, int umajor_max) {
   constexpr int kXcd = 8;
   const int G = U * gqa;                   // items per K/V group

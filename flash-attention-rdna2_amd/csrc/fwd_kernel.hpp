@@ -86,7 +86,8 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
   // ---- work item -> (sequence z, head h, q tile), and the key split (grid split-major)
   const int nitems = gridDim.x / sp.n;
   const int split = blockIdx.x / nitems;
-  const int w = xcd_group_remap(blockIdx.x - split * nitems, nitems, nqt, p.gqa, kFwdUMajor);
+  const int umax = (CAUSAL && !FEAT && C::HD <= 128 && !p.cu_q) ? kFwdUMajorCausal : kFwdUMajor;
+  const int w = xcd_group_remap(blockIdx.x - split * nitems, nitems, nqt, p.gqa, umax);
   const int qti = w % nqt, zh = w / nqt;
   const int h = zh % p.NH, z = zh / p.NH;
   const int qt = CAUSAL ? (nqt - 1 - qti) : qti;
