@@ -587,7 +587,9 @@ SWEEP_FWD = [(1, 1024, 8, 8, 64, False), (1, 2048, 8, 8, 128, True), (1, 4096, 8
              (1, 16384, 32, 32, 128, True), (4, 2048, 16, 16, 128, False), (1, 16384, 8, 8, 128, False),
              (2, 2048, 16, 16, 64, True), (1, 4096, 16, 16, 256, True), (1, 8192, 32, 8, 128, True),
              (2, 4096, 32, 32, 64, False), (1, 16384, 32, 32, 64, True), (8, 1024, 16, 16, 64, False),
-             (2, 4096, 32, 32, 32, False), (2, 4096, 32, 32, 96, True)]
+             (2, 4096, 32, 32, 32, False), (2, 4096, 32, 32, 96, True), (8, 2048, 32, 32, 128, True),
+             (8, 2048, 32, 32, 96, True), (8, 2048, 32, 32, 32, True), (4, 4096, 32, 32, 64, True),
+             (64, 512, 32, 32, 128, True)]
 # paged decode: (batch, ctx, page); (1, 32768, 32) is the shape of the reference's published decode
 # figure, (16, 32768, 256) is C4
 SWEEP_DEC = [(1, 32768, 32), (1, 32768, 256), (1, 131072, 256), (4, 32768, 256), (16, 32768, 256),
@@ -595,7 +597,8 @@ SWEEP_DEC = [(1, 32768, 32), (1, 32768, 256), (1, 131072, 256), (4, 32768, 256),
 SWEEP_BWD = [(2, 4096, 32, 32, 128, True), (1, 4096, 8, 8, 128, True), (1, 4096, 32, 8, 128, True),
              (1, 8192, 8, 8, 128, True), (2, 2048, 16, 16, 128, False), (1, 2048, 16, 16, 64, True),
              (1, 4096, 16, 16, 256, True), (2, 2048, 16, 16, 192, False), (2, 4096, 32, 32, 64, True),
-             (2, 4096, 32, 32, 64, False), (2, 4096, 32, 32, 32, True), (2, 4096, 32, 32, 96, True)]
+             (2, 4096, 32, 32, 64, False), (2, 4096, 32, 32, 32, True), (2, 4096, 32, 32, 96, True),
+             (64, 512, 32, 32, 128, True), (16, 1024, 32, 32, 128, True), (16, 2048, 32, 32, 128, True)]
 
 
 def sweep(reps=5, inner=10):
