@@ -805,7 +805,8 @@ static int fwd_split_count(const FableFwdParams& p, long long nblk) {
 // 4096 keys, whose shorter workgroups pay the diagonal tiles and the K/V loads of half as many
 // rows more often)
 constexpr int kLongKeys = 8192;
-// CR: the plain masks on short causal rows (at most kShortKeys keys) when C's grid gives at
+// CR: the plain masks on short causal rows (at head dim 96 non-causal ones too; at most
+// kShortKeys keys) when C's grid gives at
 // least 4 workgroups per CU (D=128: 2-wave workgroups of 64 rows and 32-key tiles; on a row of
 // 512 keys half the tiles of a 256-row workgroup straddle the diagonal. Varlen batches of
 // 64-1024-token sequences 1.53-1.58x, dense B16 S1024 H32 1.22x, B64 S512 1.16x; on a grid of
@@ -864,7 +865,9 @@ static int launch_fwd(const FableFwdParams& p, hipStream_t st, FwdWs& ws) {
     if (feat) return go(CfgTag<C>{}, causal, Y{}, N{});
     if constexpr (!std::is_same<CR, C>::value) {
       const long long nc = (long long)((p.SQ + C::BR - 1) / C::BR) * p.NH * p.batch;
-      if (p.causal && p.SK <= kShortKeys && nc >= 4 * 256) return go(CfgTag<CR>{}, causal, N{}, N{});
+      // (non-causal short rows too at head dim 96: B64 S512 H32 1.14x, B16 S1024 1.07x; at 32, 64
+      // and 128 they ran 0.69-0.97x)
+      if ((p.causal || C::HD == 96) && p.SK <= kShortKeys && nc >= 4 * 256) return go(CfgTag<CR>{}, causal, N{}, N{});
     }
     if constexpr (!std::is_same<CL, C>::value) {
       const long long nl = (long long)((p.SQ + CL::BR - 1) / CL::BR) * p.NH * p.batch;

@@ -253,6 +253,9 @@ def _check_rows(test, case, dt, got_o, got_lse, o_ref, l_ref, rows):
     ("D96 short rows causal bf16 B64 S512 H32", 64, 512, 32, True, "bf16", 96),
     ("D64 short rows causal fp16 B16 S1024 H32", 16, 1024, 32, True, "f16", 64),
     ("D32 short rows causal bf16 B64 S512 H32", 64, 512, 32, True, "bf16", 32),
+    # head dim 96 runs the same shape on non-causal short rows
+    ("D96 short rows full fp16 B64 S512 H32", 64, 512, 32, False, "f16", 96),
+    ("D96 short rows full bf16 B16 S1024 H32", 16, 1024, 32, False, "bf16", 96),
     # head dims 64 and 32 on long rows: 4-wave workgroups at three waves per SIMD
     ("D64 long rows full fp16 B2 S4096 H32", 2, 4096, 32, False, "f16", 64),
     ("D64 long rows causal bf16 B1 S8192 H32", 1, 8192, 32, True, "bf16", 64),
