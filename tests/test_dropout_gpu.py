@@ -39,6 +39,8 @@ CASES = [
     ("D96 full", 1, 2, 2, 70, 90, 96, False, 0.2, 0.0),
     ("D160 causal", 1, 2, 1, 64, 64, 160, True, 0.1, 0.0),
     ("D192 full softcap", 1, 2, 2, 60, 60, 192, False, 0.3, 10.0),
+    # a grid of 512 short causal key blocks at head dim 128: the persistent dK/dV kernel
+    ("D128 causal B8 S512 persistent", 8, 16, 16, 512, 512, 128, True, 0.1, 0.0),
 ]
 
 
