@@ -220,6 +220,9 @@ PERSIST_CASES = [
     ("persist D128 causal 160 seqs", 160, 512, 4, 4, 128, True, -1, -1, 0.0),
     ("persist D64 causal gqa2 200 seqs", 200, 256, 4, 2, 64, True, -1, -1, 0.0),
     ("persist D128 window softcap 160 seqs", 160, 512, 4, 4, 128, True, 60, 0, 15.0),
+    # the other pair-kernel widths: two (D=96) and three (D=32) workgroups per CU slot
+    ("persist D96 causal 200 seqs", 200, 512, 4, 4, 96, True, -1, -1, 0.0),
+    ("persist D32 full gqa2 200 seqs", 200, 256, 4, 2, 32, False, -1, -1, 0.0),
 ]
 
 
