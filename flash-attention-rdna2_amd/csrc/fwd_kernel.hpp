@@ -86,7 +86,11 @@ fwd_kernel(FableFwdParams p, int nqt, FwdSplit sp) {
   // ---- work item -> (sequence z, head h, q tile), and the key split (grid split-major)
   const int nitems = gridDim.x / sp.n;
   const int split = blockIdx.x / nitems;
-  const int umax = (CAUSAL && !FEAT && C::HD <= 128 && !p.cu_q) ? kFwdUMajorCausal : kFwdUMajor;
+  // (rows over 2048 keys stop at half the causal limit: B8 S4096 D128 1.04x and B4 S8192 1.03x
+  // head after head at 512 items per XCD, whose K/V per head then stays in L2; at 2048 keys
+  // u-major kept 1.04-1.17x there)
+  const int umax = (CAUSAL && !FEAT && C::HD <= 128 && !p.cu_q) ? (p.SK <= 2048 ? kFwdUMajorCausal : kFwdUMajorCausal / 2)
+                                                                : kFwdUMajor;
   const int w = xcd_group_remap(blockIdx.x - split * nitems, nitems, nqt, p.gqa, umax);
   const int qti = w % nqt, zh = w / nqt;
   const int h = zh % p.NH, z = zh / p.NH;
